@@ -1,0 +1,227 @@
+/*
+ * tqf_hip.h -- C ABI of the MI355X (gfx950) HIP backend for TurboQwenFare's
+ * MTP speculative-verify hot path.
+ *
+ * The reference crate has no backend trait in code; its seams are free
+ * functions plus the ExpertValue {Cpu, Gpu} dispatch.  Each entry point below
+ * names the reference seam it replaces (paths relative to the reference
+ * checkout).  The Rust side binds these through a thin `extern "C"` module and
+ * maps a non-zero status plus tqf_hip_last_error() to BackendError::Gpu(String)
+ * (src/error.rs:285-288) or, for shape violations, ModelError::Shape.
+ *
+ * Conventions
+ *   - Every function returns int32_t status: TQF_HIP_OK (0) or an error code.
+ *     Shape violations are reported, never asserted (the reference asserts in
+ *     backend/metal/kernels.rs:565-593; a panic may not cross FFI).
+ *   - Host pointers are caller-owned and borrowed for the call; those calls
+ *     are synchronous on return.  `_device` entry points take device pointers,
+ *     are stream-ordered on the context's stream and return before the GPU
+ *     finishes (tqf_hip_synchronize() waits).
+ *   - Device weights are owned by opaque handles until their *_free call, the
+ *     analogue of BufferLease's Drop (backend/metal/buffer.rs:16-24).  Scratch
+ *     is a context-owned arena that is reused across calls (no per-token
+ *     allocation; the reference allocates per call in kernels.rs:694-697).
+ *   - A context is not thread-safe: the reference serialises the GPU behind
+ *     Mutex<GpuExecutionState> (experts/mod.rs:320, 905-917).
+ *   - Weights use GGML Q4_0 (18-byte blocks of 32: f16 scale, 16 nibble bytes;
+ *     element j = (qs[j] & 15) - 8, element j+16 = (qs[j] >> 4) - 8,
+ *     format/quant/dequant.rs:110-123).  Upload repacks them losslessly into a
+ *     device tile layout; tqf_hip_weights_download() inverts it.
+ */
+#ifndef TQF_HIP_H
+#define TQF_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TQF_HIP_OK 0
+#define TQF_HIP_ERR_INVALID 1 /* shape/argument violation (ModelError::Shape)      */
+#define TQF_HIP_ERR_DEVICE 2  /* HIP runtime failure (BackendError::Gpu)           */
+#define TQF_HIP_ERR_NOMEM 3   /* device allocation failed; nothing was allocated   */
+#define TQF_HIP_ERR_ROUTER 4  /* non-finite router logits / invalid route
+                                 (ModelError::Unsupported, experts/mod.rs:136-141) */
+
+#define TQF_HIP_TOP_K 8        /* Qwen36Geometry::ROUTED_EXPERTS_PER_TOKEN        */
+#define TQF_HIP_MAX_TOKENS 8   /* largest M (= k+1 verify rows) per MoE call      */
+
+typedef struct tqf_hip_ctx tqf_hip_ctx;
+typedef struct tqf_hip_weights tqf_hip_weights; /* one Q4_0 matrix in HBM      */
+typedef struct tqf_hip_tensor tqf_hip_tensor;   /* one f32 tensor in HBM       */
+typedef struct tqf_hip_layer tqf_hip_layer;     /* prepared MoE layer          */
+typedef struct tqf_hip_stack tqf_hip_stack;     /* prepared stack of layers    */
+
+/* ---- context: GpuExecutionState::init (backend/metal/expert.rs:77-95) --- */
+int32_t tqf_hip_create(int32_t device, tqf_hip_ctx **out);
+int32_t tqf_hip_destroy(tqf_hip_ctx *ctx);
+/* Last error text of this context ("" if none); valid until the next call. */
+const char *tqf_hip_last_error(const tqf_hip_ctx *ctx);
+int32_t tqf_hip_synchronize(tqf_hip_ctx *ctx);
+/* Device name and compute-unit count, for logs. */
+int32_t tqf_hip_device_info(tqf_hip_ctx *ctx, char *name, size_t name_len, int32_t *cu_count);
+
+/* ---- plain device buffers: MetalContext::allocate_broker_buffer_with_data
+ *      (backend/metal/context.rs:84-125) without the broker ---------------- */
+int32_t tqf_hip_buffer_alloc(tqf_hip_ctx *ctx, size_t bytes, void **dptr);
+int32_t tqf_hip_buffer_free(tqf_hip_ctx *ctx, void *dptr);
+int32_t tqf_hip_memcpy_h2d(tqf_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
+int32_t tqf_hip_memcpy_d2h(tqf_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
+
+/* ---- Q4_0 weights: GpuResidentExpert::upload (backend/metal/expert.rs:
+ *      110-147) ------------------------------------------------------------- */
+/* Device bytes an upload of this shape occupies, so the caller can reserve
+ * them with its broker *before* uploading (context.rs:84-125).  0 on a shape
+ * the backend cannot hold (cols not a multiple of 32). */
+uint64_t tqf_hip_weights_bytes_for(uint32_t rows, uint32_t cols);
+/* `q4_0` is rows x (cols/32) row-major 18-byte blocks, len must equal
+ * rows*(cols/32)*18.  On failure nothing stays allocated. */
+int32_t tqf_hip_weights_upload(tqf_hip_ctx *ctx, const uint8_t *q4_0, size_t len,
+                               uint32_t rows, uint32_t cols, tqf_hip_weights **out);
+/* Same, from a device-resident Q4_0 byte buffer (a loader that has already
+ * placed the .tqf payload in HBM). */
+int32_t tqf_hip_weights_upload_device(tqf_hip_ctx *ctx, const void *d_q4_0, size_t len,
+                                      uint32_t rows, uint32_t cols, tqf_hip_weights **out);
+/* Inverse repack back to GGML Q4_0 bytes (validation, spec's "reorder only
+ * if the values are proven unchanged"; format/quant/validate.rs:148-250). */
+int32_t tqf_hip_weights_download(tqf_hip_ctx *ctx, const tqf_hip_weights *w, uint8_t *q4_0,
+                                 size_t len);
+/* GpuResidentExpert::stored_bytes (expert.rs:152-154) for one matrix. */
+uint64_t tqf_hip_weights_bytes(const tqf_hip_weights *w);
+int32_t tqf_hip_weights_free(tqf_hip_ctx *ctx, tqf_hip_weights *w);
+
+/* f32 tensors (router [n_experts x hidden], shared input gate [hidden], norm
+ * scales [hidden]): LoadedQwen36Tensor with GgmlType::F32 (weights.rs:802). */
+int32_t tqf_hip_tensor_upload(tqf_hip_ctx *ctx, const float *data, size_t count,
+                              tqf_hip_tensor **out);
+int32_t tqf_hip_tensor_free(tqf_hip_ctx *ctx, tqf_hip_tensor *t);
+
+/* ---- Q4_0 GEMV / small-M GEMM ------------------------------------------- */
+/* Replaces backend::reference::q4k_gemv/q4k_gemm (backend/reference.rs:61-92)
+ * and metal::kernels::q4k_gemv_persistent_weights (kernels.rs:565-593) for
+ * Q4_0 (matvec_row, model/qwen36/weights.rs:827-843).  x is [m x cols] f32,
+ * y is [m x rows] f32, 1 <= m <= TQF_HIP_MAX_TOKENS. */
+int32_t tqf_hip_q4_gemv(tqf_hip_ctx *ctx, const tqf_hip_weights *w, const float *x, uint32_t m,
+                        float *y);
+int32_t tqf_hip_q4_gemv_device(tqf_hip_ctx *ctx, const tqf_hip_weights *w, const float *d_x,
+                               uint32_t m, float *d_y);
+/* `count` same-shape matrices against one shared x [cols] in one launch;
+ * d_y is [count x rows].  The rotating-pool bandwidth probe of the GEMV. */
+int32_t tqf_hip_q4_gemv_batched_device(tqf_hip_ctx *ctx, const tqf_hip_weights *const *ws,
+                                       uint32_t count, const float *d_x, float *d_y);
+
+/* ---- one expert: LoadedQwen36Expert::forward (weights.rs:566-610) and
+ *      GpuResidentExpert::forward (backend/metal/expert.rs:162-172) -------- */
+/* gate/up are [width x hidden], down is [hidden x width]; x [m x hidden],
+ * y [m x hidden].  SwiGLU is fused; no host round trip between GEMVs. */
+int32_t tqf_hip_expert_forward(tqf_hip_ctx *ctx, const tqf_hip_weights *gate,
+                               const tqf_hip_weights *up, const tqf_hip_weights *down,
+                               const float *x, uint32_t m, float *y);
+
+/* ---- one MoE layer over M rows: Qwen36StreamingMoe::forward_batch
+ *      (experts/mod.rs:1540-1577) with the arithmetic of
+ *      Qwen36ResidentMoe::forward (:1600-1634) ---------------------------- */
+typedef struct tqf_hip_moe_weights {
+    const tqf_hip_tensor *router;            /* f32 [n_experts x hidden]   */
+    const tqf_hip_tensor *shared_input_gate; /* f32 [hidden]               */
+    const tqf_hip_weights *shared_gate;      /* Q4_0 [width x hidden]      */
+    const tqf_hip_weights *shared_up;        /* Q4_0 [width x hidden]      */
+    const tqf_hip_weights *shared_down;      /* Q4_0 [hidden x width]      */
+    const tqf_hip_weights *const *routed_gate; /* [n_experts]              */
+    const tqf_hip_weights *const *routed_up;   /* [n_experts]              */
+    const tqf_hip_weights *const *routed_down; /* [n_experts]              */
+    uint32_t n_experts; /* 256: RouterResult::from_logits requires it      */
+    uint32_t hidden;    /* 2048 (multiple of 256)                          */
+    uint32_t width;     /* 512  (multiple of 256)                          */
+} tqf_hip_moe_weights;
+
+/* Builds the device-side expert table once (the analogue of pinning every
+ * expert resident: experts/mod.rs:512-545 stage_expert_values). */
+int32_t tqf_hip_moe_layer_prepare(tqf_hip_ctx *ctx, const tqf_hip_moe_weights *weights,
+                                  tqf_hip_layer **out);
+int32_t tqf_hip_moe_layer_free(tqf_hip_ctx *ctx, tqf_hip_layer *layer);
+/* x [m x hidden] f32 -> y [m x hidden]; ids [m x 8] and w [m x 8] receive the
+ * routes (RouterResult; may be NULL), for RouterTrace parity
+ * (runtime/decode.rs:14-17).  TQF_HIP_ERR_ROUTER if a router logit is not
+ * finite. */
+int32_t tqf_hip_moe_layer(tqf_hip_ctx *ctx, const tqf_hip_layer *layer, const float *x,
+                          uint32_t m, float *y, uint16_t *ids, float *w);
+/* Same with bf16 activations (converted exactly to f32 on entry). */
+int32_t tqf_hip_moe_layer_bf16(tqf_hip_ctx *ctx, const tqf_hip_layer *layer,
+                               const uint16_t *x_bf16, uint32_t m, float *y, uint16_t *ids,
+                               float *w);
+/* Device-pointer form; d_status (may be NULL) receives 0 or TQF_HIP_ERR_ROUTER. */
+int32_t tqf_hip_moe_layer_device(tqf_hip_ctx *ctx, const tqf_hip_layer *layer, const float *d_x,
+                                 uint32_t m, float *d_y, uint16_t *d_ids, float *d_w,
+                                 int32_t *d_status);
+
+/* ---- stacked layers: the layer wrapper of bounded_layer_forward
+ *      (model/qwen36/runtime.rs:777-802): h <- h + MoE_l(rmsnorm_l(h)) ------ */
+int32_t tqf_hip_stack_prepare(tqf_hip_ctx *ctx, const tqf_hip_layer *const *layers,
+                              const tqf_hip_tensor *const *ffn_norms, uint32_t n_layers,
+                              tqf_hip_stack **out);
+int32_t tqf_hip_stack_free(tqf_hip_ctx *ctx, tqf_hip_stack *stack);
+/* d_h [m x hidden] f32 is updated in place.  d_ids/d_w ([n_layers x m x 8],
+ * may be NULL) receive every layer's route.  Captured once into a HIP graph
+ * per argument set and replayed afterwards. */
+int32_t tqf_hip_stack_forward_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack, float *d_h,
+                                     uint32_t m, uint16_t *d_ids, float *d_w,
+                                     int32_t *d_status);
+
+/* ---- acceptance: Sampler::select (sampling/mod.rs:68-74) and
+ *      mtp::verify_pair (runtime/mtp.rs:98-104) generalised to k drafts ------
+ * target [k+1 x vocab], draft [k x vocab] (ignored when greedy), draft_tokens
+ * [k].  Greedy (the temperature == 0 identity path, sampling/mod.rs:43-50):
+ * accept while argmax(target_i) == draft_i (argmax as
+ * top_logit_candidates, runtime/decode.rs:48-64); k == 1 is verify_pair.
+ * Stochastic: accept draft i iff u[i] < p_i(d)/q_i(d) with p, q the softmax of
+ * logits/temperature; on the first rejection resample from
+ * norm(max(0, p - q)) with u_resample[i]; if all k are accepted the bonus
+ * token is drawn from p_k with u_resample[k].  Writes *accepted (0..k) and
+ * tokens_out[k+1] (tokens_out[0..accepted] are emitted, the rest are -1).
+ * Bit-exact with the CPU definition for identical inputs. */
+int32_t tqf_hip_accept(tqf_hip_ctx *ctx, const float *target, const float *draft,
+                       const int32_t *draft_tokens, uint32_t k, uint32_t vocab, float temperature,
+                       int32_t greedy, const float *u, const float *u_resample, int32_t *accepted,
+                       int32_t *tokens_out);
+int32_t tqf_hip_accept_device(tqf_hip_ctx *ctx, const float *d_target, const float *d_draft,
+                              const int32_t *d_draft_tokens, uint32_t k, uint32_t vocab,
+                              float temperature, int32_t greedy, const float *d_u,
+                              const float *d_u_resample, int32_t *d_accepted,
+                              int32_t *d_tokens_out);
+/* top_logit_candidates (runtime/decode.rs:48-64) over `rows` rows of vocab
+ * logits: tokens4/logits4 are [rows x 4]. */
+int32_t tqf_hip_top_logit_candidates(tqf_hip_ctx *ctx, const float *logits, uint32_t rows,
+                                     uint32_t vocab, uint32_t *tokens4, float *logits4);
+
+/* ---- one MTP verify step: the stack over the k+1 verify rows, then the
+ *      acceptance, as one stream-ordered (graph-replayed) unit.  The verify
+ *      loop the reference leaves unwired (runtime/mtp.rs:1-20). ------------- */
+int32_t tqf_hip_verify_step_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack, float *d_h,
+                                   uint32_t m, const float *d_target, const float *d_draft,
+                                   const int32_t *d_draft_tokens, uint32_t vocab,
+                                   float temperature, int32_t greedy, const float *d_u,
+                                   const float *d_u_resample, int32_t *d_accepted,
+                                   int32_t *d_tokens_out);
+
+/* ---- profiling: the HIP counterpart of backend/metal/timing.rs:23-80 ----- */
+#define TQF_HIP_KERNEL_ROUTE 0    /* rmsnorm + router + top-8 + union plan    */
+#define TQF_HIP_KERNEL_GATE_UP 1  /* union-expert gate/up GEMV + SwiGLU       */
+#define TQF_HIP_KERNEL_DOWN 2     /* union-expert down GEMV + weighted combine */
+#define TQF_HIP_KERNEL_GEMV 3     /* standalone Q4_0 GEMV                     */
+#define TQF_HIP_KERNEL_ACCEPT 4   /* the acceptance kernels, summed           */
+#define TQF_HIP_KERNEL_KINDS 5
+/* While enabled, eager (non-graph) launches of each kind are bracketed by HIP
+ * events on the context stream.  Enabling clears the totals. */
+int32_t tqf_hip_profile_enable(tqf_hip_ctx *ctx, int32_t enable);
+/* Synchronises, then reports launches, summed kernel milliseconds and the
+ * summed algorithmic HBM bytes of those launches for one kind. */
+int32_t tqf_hip_profile_read(tqf_hip_ctx *ctx, int32_t kind, uint64_t *launches,
+                             double *total_ms, double *algorithmic_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TQF_HIP_H */

@@ -1,0 +1,173 @@
+/*
+ * tqf_oracle.h -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C CPU restatement of the reference crate's scalar path for the
+ * MTP speculative-verify hot path (Q4_0 MoE expert FFN + acceptance).  It is
+ * the checker the HIP backend is compared against.  Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it; the
+ * product library never links or calls it.
+ *
+ * Every function names the reference file:line whose semantics it restates
+ * (paths relative to the reference checkout).  Rust semantics reproduced:
+ *   - no FMA contraction (build with -ffp-contract=off);
+ *   - `Iterator::sum::<f32>()` is a sequential left fold seeded with -0.0;
+ *   - `f32::exp` is the platform libm expf;
+ *   - `sort_by` is stable, `total_cmp` is IEEE total order.
+ *
+ * Pinning status (what checks each function against something other than
+ * itself) is listed beside each declaration and enforced in
+ * tests/test_oracle.py.
+ */
+#ifndef TQF_ORACLE_H
+#define TQF_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- a1: binary16 <-> binary32 ---------------------------------------- */
+/* dequant.rs:19-48.  Pinned: dequant.rs:244-251 known values; exhaustive
+ * agreement with the arithmetic twin below over all 65,536 patterns
+ * (simd/mod.rs:459-475 does the same). */
+float orc_f16_to_f32(uint16_t bits);
+/* validate.rs:48-69 (independent arithmetic decoder). */
+float orc_f16_to_f32_indep(uint16_t bits);
+/* dequant.rs:54-100 (round to nearest, ties to even).  Pinned: dequant.rs:
+ * 279-284 round-trip set; numpy float16 conversion over a dense sweep. */
+uint16_t orc_f32_to_f16(float value);
+
+/* ---- a2: Q4_0 block decode -------------------------------------------- */
+/* dequant.rs:110-123.  Pinned: dequant.rs:253-264 KAT; validate.rs:270-299
+ * byte pattern i*37+11 against the independent decoder below. */
+void orc_dequantize_q4_0(const uint8_t *block18, float *out32);
+/* validate.rs:71-87 (arithmetic nibble extraction, independent f16). */
+void orc_dequantize_q4_0_indep(const uint8_t *block18, float *out32);
+
+/* ---- a3: Q4_0 matvec -------------------------------------------------- */
+/* weights.rs:617-750 (matvec_payload shape checks) and :827-843 (matvec_row
+ * Q4_0: per-block iterator sum, then sequential row accumulate).
+ * `w` is rows x (cols/32) row-major 18-byte blocks.  Returns 0, or -1 on a
+ * shape error (the reference returns ModelError::Shape).  Pinned:
+ * weights.rs:2500-2508 (224.0), :2458-2480 (7.0 x32 / 0.0 x32), :2511-2530;
+ * a float64 brute-force dot on random shapes. */
+int orc_q4_0_matvec(const uint8_t *w, size_t len, uint32_t rows, uint32_t cols,
+                    const float *x, float *y);
+
+/* ---- a5: F32 matvec (router) ------------------------------------------ */
+/* weights.rs:802-808 (F32 matvec_row) and :306-323 (dot = 1-row matvec).
+ * Pinned: weights.rs:2440-2456 ([14, 32]); float64 brute force. */
+void orc_f32_matvec(const float *w, uint32_t rows, uint32_t cols, const float *x,
+                    float *y);
+
+/* ---- a6: router softmax / stable top-8 / renormalise ------------------ */
+/* experts/mod.rs:134-197.  n must be 256 (require_len).  Returns 0, or -1 on
+ * a wrong length, a non-finite logit, or a failed validate().  Pinned:
+ * experts/mod.rs:1639-1673 KATs; invariants (ids descend by probability,
+ * ties to lower id, sum of weights within 1e-4 of one). */
+int orc_router_from_logits(const float *logits, uint32_t n, uint16_t *ids8,
+                           float *weights8);
+/* validate() alone (experts/mod.rs:169-197), for the duplicate-id KAT. */
+int orc_router_validate(const uint16_t *ids8, const float *weights8);
+
+/* ---- a7 / a21: activation algebra ------------------------------------- */
+/* weights.rs:241-259: out = (g / (1 + exp(-g))) * u.  Pinned: silu(0)=0
+ * (reference.rs:124-128), sign/limit closed forms. */
+void orc_silu_mul(const float *g, const float *u, float *out, uint32_t n);
+/* weights.rs:216-239 (eps 1e-6).  Pinned: unit-RMS KAT (weights.rs:2483). */
+void orc_qwen_rmsnorm(const float *x, const float *w, uint32_t n, float *out);
+/* reference.rs:116-118 / experts/mod.rs:1514: 1 / (1 + exp(-v)). */
+float orc_sigmoid(float v);
+
+/* ---- a10: one routed/shared expert ------------------------------------ */
+/* weights.rs:566-610: gate [width x hidden], up [width x hidden], down
+ * [hidden x width], all Q4_0; y = down(silu(gate x) * up x).  Returns 0 or
+ * -1 on a shape error.  Pinned: one-hot-expert and linearity invariants,
+ * float64 brute force. */
+int orc_expert_forward(const uint8_t *gate, const uint8_t *up, const uint8_t *down,
+                       uint32_t hidden, uint32_t width, const float *x, float *y);
+
+/* ---- a11 / a12: MoE layer over M rows --------------------------------- */
+typedef struct orc_moe_layer {
+    const float *router;            /* f32 [n_experts x hidden]          */
+    const float *shared_input_gate; /* f32 [hidden]                      */
+    const uint8_t *shared_gate;     /* Q4_0 [width x hidden]             */
+    const uint8_t *shared_up;       /* Q4_0 [width x hidden]             */
+    const uint8_t *shared_down;     /* Q4_0 [hidden x width]             */
+    const uint8_t *const *routed_gate; /* [n_experts] -> Q4_0 planes     */
+    const uint8_t *const *routed_up;
+    const uint8_t *const *routed_down;
+    uint32_t n_experts;             /* 256 (router requires it)          */
+    uint32_t hidden;                /* 2048                              */
+    uint32_t width;                 /* 512                               */
+} orc_moe_layer;
+
+/* experts/mod.rs:1540-1577 (forward_batch) with the per-row arithmetic of
+ * :1600-1634: route every row; shared expert (gate/up/SwiGLU/down) scaled by
+ * sigmoid(shared_input_gate . x); then add_scaled_in_place (weights.rs:
+ * 267-281) for each route in route order.  x, y are [m x hidden]; ids/w are
+ * [m x 8] (may be NULL).  nthreads > 1 parallelises over output rows with
+ * OpenMP; each row's arithmetic is unchanged, so results are bit-identical
+ * to nthreads == 1.  Returns 0, or -1 on a router error. */
+int orc_moe_forward_batch(const orc_moe_layer *layer, const float *x, uint32_t m,
+                          float *y, uint16_t *ids, float *w, int nthreads);
+
+/* Distinct-expert union of M routes in first-demand order (experts/mod.rs:
+ * 268-275 BatchExpertPlan, :937 prepare_batch_route).  Returns the count. */
+uint32_t orc_batch_union(const uint16_t *ids, uint32_t m, uint16_t *out_union);
+
+/* ---- a16: top_logit_candidates ---------------------------------------- */
+/* runtime/decode.rs:48-64: 4 slots, strict '>' (ties to the lower index, NaN
+ * never enters).  Pinned: sampling/mod.rs:412-452 KATs. */
+void orc_top_logit_candidates(const float *logits, uint32_t n, uint32_t *tokens4,
+                              float *logits4);
+
+/* ---- a17 / a18: stochastic draw and xoshiro256++ ---------------------- */
+/* sampling/mod.rs:166-190 (softmax, sorted descending, ties to lower token,
+ * NaN last) then :227-248 (inverse CDF with u*total, first cum >= target;
+ * top-token fallback on a non-finite/zero total).  `u` is the uniform that
+ * rng.next_f32() would supply.  Pinned: sampling/mod.rs:476-499 frequency
+ * test, :500-519 temperature test, NaN tests. */
+uint32_t orc_softmax_draw(const float *logits, uint32_t n, float temperature, float u);
+
+typedef struct orc_xoshiro { uint64_t s[4]; } orc_xoshiro;
+/* sampling/mod.rs:283-298 SplitMix64 seeding. */
+void orc_xoshiro_seed(orc_xoshiro *rng, uint64_t seed);
+/* sampling/mod.rs:311-326.  Pinned: sampling/mod.rs:662-669 (16,777,217). */
+uint64_t orc_xoshiro_next_u64(orc_xoshiro *rng);
+/* sampling/mod.rs:328-330. */
+float orc_xoshiro_next_f32(orc_xoshiro *rng);
+
+/* ---- Philox4x32-10 (Salmon et al., SC'11) ----------------------------- */
+/* No reference code (the configs name a seeded Philox stream).  Pinned:
+ * Random123 known-answer vectors and ROCm's open-source
+ * rocrand_philox4x32_10.h (vectors committed under tests/golden/). */
+void orc_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+
+/* ---- a22: k-token speculative acceptance (no reference code) ---------- */
+/* The exact, order-independent algorithm the HIP kernels implement (see the
+ * definition in oracle/tqf_oracle.c above orc_accept).  target [k+1 x V],
+ * draft [k x V] (unused when greedy), draft_tokens [k], u [k],
+ * u_resample [k+1].  Writes *accepted and tokens_out[k+1] (entries past
+ * accepted are -1).  Returns 0, or -1 on invalid arguments.  Pinned: greedy
+ * k=1 == verify_pair (mtp.rs:98-104, 212-221); closed forms (p == q always
+ * accepts, p(d)=0<q(d) always rejects, one-hot target accepts); chi-square
+ * test that emitted tokens are distributed as the target softmax. */
+int orc_accept(const float *target, const float *draft, const int32_t *draft_tokens,
+               uint32_t k, uint32_t vocab, float temperature, int greedy,
+               const float *u, const float *u_resample, int32_t *accepted,
+               int32_t *tokens_out);
+
+/* Building blocks of orc_accept, exported so tests can pin them. */
+float orc_accept_exp(float z);               /* Cody-Waite + degree-7 Taylor */
+uint64_t orc_fix40(float v);                 /* floor(v * 2^40), v in [0,1]  */
+uint64_t orc_fix62(float v);                 /* floor(v * 2^62), v in [0,1]  */
+float orc_u64_to_f32(uint64_t v);            /* round to nearest even        */
+uint64_t orc_scale_floor(uint64_t total, float u); /* floor(total * u) exact */
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TQF_ORACLE_H */

@@ -1,0 +1,325 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle on the
+same seeded inputs.  Tolerances: expert-FFN outputs within 1e-3 of the
+reference metric |g - c| / max(|c|, 1) (backend/metal/expert.rs:309-310);
+routes, union plans, acceptance decisions and tokens bit-exact."""
+import numpy as np
+import pytest
+
+import cpu_oracle as orc
+from conftest import rel_err
+from turboqwenfare_amd import mtp, synth
+from turboqwenfare_amd._lib import ERR_INVALID, ERR_ROUTER, HipError
+
+pytestmark = pytest.mark.gpu
+
+FFN_TOL = 1e-3
+
+
+def q4_block(scale_bits: int, qs: bytes) -> bytes:
+    return scale_bits.to_bytes(2, "little") + qs
+
+
+# ---- device / layout --------------------------------------------------------
+def test_device_is_gfx950(backend):
+    name, cus = backend.device_info()
+    print(name, cus)
+    assert "gfx950" in name
+    assert cus > 0
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 32), (7, 96), (64, 256), (65, 288), (130, 2080),
+                                       (512, 2048), (2048, 512)])
+def test_repack_is_lossless(backend, rows, cols):
+    rng = np.random.default_rng(rows * 1000 + cols)
+    q = rng.integers(0, 256, size=rows * (cols // 32) * 18, dtype=np.uint8)
+    w = backend.upload_q4_0(q, rows, cols)
+    assert np.array_equal(backend.download_q4_0(w), q)
+    assert backend.weights_bytes(w) >= q.nbytes
+    backend.free_weights(w)
+
+
+def test_device_synth_matches_host_generator(backend):
+    w = backend.synth_q4_0(512, 2048, 7, 3)
+    assert np.array_equal(backend.download_q4_0(w), synth.q4_0_synthetic(512, 2048, 7, 3))
+    w2 = backend.synth_q4_0(2048, 512, 123456, 0)
+    assert np.array_equal(backend.download_q4_0(w2), synth.q4_0_synthetic(2048, 512, 123456, 0))
+    backend.free_weights(w)
+    backend.free_weights(w2)
+
+
+def test_upload_rejects_bad_shapes(backend):
+    with pytest.raises(HipError) as e:
+        backend.upload_q4_0(np.zeros(18, np.uint8), 1, 48)
+    assert e.value.status == ERR_INVALID
+    with pytest.raises(HipError) as e:
+        backend.upload_q4_0(np.zeros(17, np.uint8), 1, 32)
+    assert e.value.status == ERR_INVALID
+
+
+# ---- a3: GEMV ---------------------------------------------------------------
+def test_gemv_canonical_q4_zero_block_kat(backend):
+    # weights.rs:2500-2508: scale 1.0, every nibble 15 -> 7 x 32 ones = 224.
+    w = backend.upload_q4_0(np.frombuffer(q4_block(0x3C00, b"\xff" * 16), np.uint8), 1, 32)
+    assert backend.q4_gemv(w, np.ones(32, np.float32))[0] == 224.0
+    # weights.rs:2511-2530: the second plane (all-zero bytes) gives 0.0.
+    two = np.frombuffer(q4_block(0x3C00, b"\xff" * 16) + bytes(18), np.uint8)
+    w2 = backend.upload_q4_0(two, 2, 32)
+    assert list(backend.q4_gemv(w2, np.ones(32, np.float32))) == [224.0, 0.0]
+
+
+def test_gemv_one_hot_probe_recovers_every_element(backend):
+    # kernels.rs:1168-1196 technique: x = e_j returns column j exactly.
+    rows, cols = 64, 256
+    q = synth.q4_0_synthetic(rows, cols, 11, 0)
+    w = backend.upload_q4_0(q, rows, cols)
+    dense = np.stack([np.concatenate([orc.dequantize_q4_0(q[(r * (cols // 32) + b) * 18:
+                                                              (r * (cols // 32) + b + 1) * 18])
+                                      for b in range(cols // 32)]) for r in range(rows)])
+    eye = np.eye(cols, dtype=np.float32)
+    for j0 in range(0, cols, 8):
+        y = backend.q4_gemv(w, eye[j0:j0 + 8])
+        assert np.array_equal(y, dense[:, j0:j0 + 8].T)
+
+
+def test_gemv_config1_parity(backend):
+    rows, cols = 512, 2048
+    q = synth.q4_0_synthetic(rows, cols, 1, 0)
+    x = synth.normal((cols,), seed=0)
+    w = backend.upload_q4_0(q, rows, cols)
+    assert rel_err(backend.q4_gemv(w, x), orc.q4_0_matvec(q, rows, cols, x)) < 1e-5
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 32), (7, 96), (65, 288), (130, 2080), (2048, 512)])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8])
+def test_gemv_shape_sweep(backend, rows, cols, m):
+    q = synth.q4_0_synthetic(rows, cols, rows + cols, m)
+    x = synth.normal((m, cols), seed=m, std=2.0)
+    w = backend.upload_q4_0(q, rows, cols)
+    y = backend.q4_gemv(w, x)
+    for t in range(m):
+        assert rel_err(y[t], orc.q4_0_matvec(q, rows, cols, x[t])) < 1e-5
+    backend.free_weights(w)
+
+
+def test_gemv_propagates_non_finite_input(backend):
+    q = synth.q4_0_synthetic(64, 256, 5, 5)
+    w = backend.upload_q4_0(q, 64, 256)
+    x = np.ones(256, np.float32)
+    x[40] = np.nan
+    assert np.all(np.isnan(backend.q4_gemv(w, x)))
+
+
+def test_gemv_wide_dynamic_range(backend):
+    rows, cols = 64, 512
+    q = synth.q4_0_synthetic(rows, cols, 9, 9)
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal(cols) * np.exp2(rng.integers(-40, 40, cols))).astype(np.float32)
+    w = backend.upload_q4_0(q, rows, cols)
+    got = backend.q4_gemv(w, x)
+    want = orc.q4_0_matvec(q, rows, cols, x)
+    scale = np.max(np.abs(x)) * 0.02 * 8
+    assert np.max(np.abs(got - want)) <= 1e-5 * scale * np.sqrt(cols)
+
+
+def test_gemv_batched_matches_single(backend):
+    ws = [backend.synth_q4_0(512, 2048, 100 + i, 0) for i in range(5)]
+    x = synth.normal((2048,), seed=4)
+    dx = backend.to_device(x)
+    dy = backend.alloc(5 * 512 * 4)
+    backend.q4_gemv_batched_device(ws, dx, dy)
+    y = backend.read(dy, np.float32, (5, 512))
+    for i, w in enumerate(ws):
+        assert np.array_equal(y[i], backend.q4_gemv(w, x))
+    backend.free(dx)
+    backend.free(dy)
+    for w in ws:
+        backend.free_weights(w)
+
+
+# ---- a10: one expert --------------------------------------------------------
+@pytest.mark.parametrize("m", [1, 4])
+def test_expert_forward_parity(backend, m):
+    g = backend.synth_q4_0(512, 2048, 21, 0)
+    u = backend.synth_q4_0(512, 2048, 22, 0)
+    d = backend.synth_q4_0(2048, 512, 23, 0)
+    x = synth.normal((m, 2048), seed=m)
+    y = backend.expert_forward(g, u, d, x)
+    gq, uq, dq = (backend.download_q4_0(t) for t in (g, u, d))
+    for t in range(m):
+        assert rel_err(y[t], orc.expert_forward(gq, uq, dq, 2048, 512, x[t])) < FFN_TOL
+    for t in (g, u, d):
+        backend.free_weights(t)
+
+
+# ---- a11/a12: MoE layer -----------------------------------------------------
+class Layer:
+    """One synthetic layer resident on the device with host copies for the
+    oracle (router ~N(0, 1/2048), shared input gate ~N(0, 1/2048))."""
+
+    def __init__(self, be, layer_id: int, seed: int = 0, router_std=2048 ** -0.5):
+        E, H, F = 256, 2048, 512
+        base = 10_000 * (layer_id + 1)
+        self.router = synth.normal((E, H), seed=base + 1, std=router_std)
+        self.gate_vec = synth.normal((H,), seed=base + 2, std=2048 ** -0.5)
+        mats = []
+        for e in range(E + 1):
+            mats.append((be.synth_q4_0(F, H, base + 3 * e + 10, seed),
+                         be.synth_q4_0(F, H, base + 3 * e + 11, seed),
+                         be.synth_q4_0(H, F, base + 3 * e + 12, seed)))
+        self.dev = be.prepare_moe_layer(be.upload_f32(self.router), be.upload_f32(self.gate_vec),
+                                        mats[E], [m[0] for m in mats[:E]],
+                                        [m[1] for m in mats[:E]], [m[2] for m in mats[:E]])
+        host = [[be.download_q4_0(t) for t in m] for m in mats]
+        self.host = orc.MoeLayerHost(self.router, self.gate_vec, *host[E],
+                                     [h[0] for h in host[:E]], [h[1] for h in host[:E]],
+                                     [h[2] for h in host[:E]])
+        self.mats = mats
+
+
+@pytest.fixture(scope="module")
+def layer(backend):
+    return Layer(backend, 0)
+
+
+@pytest.mark.parametrize("m", [1, 4])
+def test_moe_layer_parity(backend, layer, m):
+    x = synth.normal((m, 2048), seed=100 + m)
+    y, ids, w = backend.moe_forward_batch(layer.dev, x)
+    yc, idc, wc = layer.host.forward_batch(x)
+    assert np.array_equal(ids, idc)
+    assert rel_err(w, wc) < 1e-5
+    assert rel_err(y, yc) < FFN_TOL
+    print(f"m={m} rel err {rel_err(y, yc):.3e} union {len(mtp.routes_union(ids))}")
+
+
+def test_moe_layer_bf16_input(backend, layer):
+    x = synth.normal((4, 2048), seed=7)
+    xb = (x.view(np.uint32) >> 16).astype(np.uint16)
+    xf = (xb.astype(np.uint32) << 16).view(np.float32)
+    y, ids, _ = backend.moe_forward_batch_bf16(layer.dev, xb)
+    yc, idc, _ = layer.host.forward_batch(xf)
+    assert np.array_equal(ids, idc)
+    assert rel_err(y, yc) < FFN_TOL
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_moe_routes_and_union_over_seeds(backend, layer, seed):
+    x = synth.normal((4, 2048), seed=1000 + seed)
+    y, ids, _ = backend.moe_forward_batch(layer.dev, x)
+    yc, idc, _ = layer.host.forward_batch(x)
+    assert np.array_equal(ids, idc)
+    assert mtp.routes_union(ids) == orc.batch_union(idc)
+    assert rel_err(y, yc) < FFN_TOL
+
+
+def test_moe_duplicate_rows_give_identical_outputs(backend, layer):
+    x = np.repeat(synth.normal((1, 2048), seed=55), 4, axis=0)
+    y, ids, _ = backend.moe_forward_batch(layer.dev, x)
+    assert all(np.array_equal(ids[0], ids[t]) for t in range(4))
+    assert all(np.array_equal(y[0], y[t]) for t in range(4))
+
+
+def test_moe_rejects_non_finite_router_input(backend, layer):
+    x = synth.normal((2, 2048), seed=3)
+    x[1, 17] = np.inf
+    with pytest.raises(HipError) as e:
+        backend.moe_forward_batch(layer.dev, x)
+    assert e.value.status == ERR_ROUTER
+    # the context stays usable afterwards
+    y, _, _ = backend.moe_forward_batch(layer.dev, x[:1])
+    assert np.all(np.isfinite(y))
+
+
+# ---- stacked layers (runtime.rs:777-802) and the graph-replayed verify step --
+@pytest.fixture(scope="module")
+def stack3(backend, layer):
+    layers = [layer, Layer(backend, 1), Layer(backend, 2)]
+    norms = [1.0 + 0.1 * synth.normal((2048,), seed=900 + i) for i in range(3)]
+    st = backend.prepare_stack([l.dev for l in layers], [backend.upload_f32(n) for n in norms])
+    return layers, norms, st
+
+
+def oracle_stack(layers, norms, h):
+    h = h.copy()
+    routes = []
+    for L, nw in zip(layers, norms):
+        xn = np.stack([orc.qwen_rmsnorm(h[t], nw) for t in range(h.shape[0])])
+        y, ids, _ = L.host.forward_batch(xn)
+        h = (h + y).astype(np.float32)
+        routes.append(ids)
+    return h, routes
+
+
+def test_stack_forward_parity(backend, stack3):
+    layers, norms, st = stack3
+    h0 = synth.normal((4, 2048), seed=77)
+    dh = backend.to_device(h0)
+    dids = backend.alloc(3 * 4 * 8 * 2)
+    backend.stack_forward_device(st, dh, 4, dids)
+    h = backend.read(dh, np.float32, (4, 2048))
+    ids = backend.read(dids, np.uint16, (3, 4, 8))
+    hc, routes = oracle_stack(layers, norms, h0)
+    for l in range(3):
+        assert np.array_equal(ids[l], routes[l])
+    assert rel_err(h, hc) < FFN_TOL
+    backend.free(dh)
+    backend.free(dids)
+
+
+def test_verify_step_graph_replays_match_eager(backend, stack3):
+    layers, norms, st = stack3
+    vocab, k = 151936, 3
+    rng = np.random.default_rng(5)
+    target = (rng.standard_normal((k + 1, vocab)) * 3).astype(np.float32)
+    draft = (rng.standard_normal((k, vocab)) * 3).astype(np.float32)
+    dtok = np.array([int(np.argmax(target[i])) for i in range(k)], np.int32)
+    u = synth.philox_uniforms(0, 0, k)
+    ur = synth.philox_uniforms(0, 1, k + 1)
+    h0 = synth.normal((4, 2048), seed=88)
+    bufs = {n: backend.to_device(a) for n, a in
+            dict(t=target, d=draft, dt=dtok, u=u, ur=ur).items()}
+    acc = backend.alloc(4)
+    toks = backend.alloc(4 * (k + 1))
+    # eager reference (profiling forces eager launches): stack forward
+    dh_e = backend.to_device(h0)
+    backend.profile_enable(True)
+    backend.stack_forward_device(st, dh_e, 4)
+    h_e = backend.read(dh_e, np.float32, (4, 2048))
+    backend.profile_enable(False)
+    want = orc.accept(target, draft, dtok, 0.7, False, u, ur)
+    dh = backend.to_device(h0)
+    for rep in range(3):
+        backend.write(dh, h0)
+        backend.synchronize()
+        backend.verify_step_device(st, dh, 4, bufs["t"], bufs["d"], bufs["dt"], vocab, 0.7,
+                                   False, bufs["u"], bufs["ur"], acc, toks)
+        h = backend.read(dh, np.float32, (4, 2048))
+        a = int(backend.read(acc, np.int32, (1,))[0])
+        tk = backend.read(toks, np.int32, (k + 1,))
+        assert np.array_equal(h, h_e), f"replay {rep} differs from the eager stack"
+        assert (a, [int(v) for v in tk[: a + 1]]) == want
+    for b in list(bufs.values()) + [acc, toks, dh, dh_e]:
+        backend.free(b)
+
+
+# ---- a16: top_logit_candidates ----------------------------------------------
+def test_top_logit_candidates_parity(backend):
+    rng = np.random.default_rng(0)
+    rows = []
+    for s in range(6):
+        v = (rng.standard_normal(151936) * 3).astype(np.float32)
+        rows.append(v)
+    ties = np.full(151936, -5.0, np.float32)
+    ties[[10, 7, 99999, 3]] = 2.0
+    ties[50] = np.nan
+    rows.append(ties)
+    rows.append(np.full(151936, -np.inf, np.float32))
+    allnan = np.full(151936, np.nan, np.float32)
+    allnan[151935] = 1.0
+    rows.append(allnan)
+    lg = np.stack(rows)
+    toks, vals = backend.top_logit_candidates(lg)
+    for r in range(lg.shape[0]):
+        tc, vc = orc.top_logit_candidates(lg[r])
+        assert list(toks[r]) == list(tc)
+        assert np.array_equal(vals[r], vc)

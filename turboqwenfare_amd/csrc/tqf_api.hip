@@ -1,0 +1,1088 @@
+// tqf_api.hip -- the C ABI (include/tqf_hip.h): context, weights arena,
+// scratch, host/device entry points, HIP-graph replay and event profiling.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/tqf_hip.h"
+#include "../../include/tqf_hip_synth.h"
+#include "tqf_internal.h"
+
+using namespace tqf;
+
+namespace tqf {
+struct GraphEntry {
+    std::vector<uint64_t> key;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+}  // namespace tqf
+
+namespace {
+
+constexpr size_t kSlabBytes = size_t(256) << 20;
+constexpr size_t kAlign = 256;
+constexpr int kRingSize = 4096;
+constexpr size_t kMaxGraphs = 16;
+
+int32_t fail(tqf_hip_ctx *ctx, int32_t code, const std::string &msg) {
+    if (ctx) ctx->last_error = msg;
+    return code;
+}
+
+int32_t hip_fail(tqf_hip_ctx *ctx, const char *what, hipError_t e) {
+    return fail(ctx, TQF_HIP_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define TQF_HIP(ctx, expr)                                  \
+    do {                                                    \
+        hipError_t _e = (expr);                             \
+        if (_e != hipSuccess) return hip_fail(ctx, #expr, _e); \
+    } while (0)
+
+#define TQF_ENTER(ctx)                                                      \
+    do {                                                                    \
+        if (!(ctx)) return TQF_HIP_ERR_INVALID;                             \
+        (ctx)->last_error.clear();                                          \
+        hipError_t _e = hipSetDevice((ctx)->device);                        \
+        if (_e != hipSuccess) return hip_fail(ctx, "hipSetDevice", _e);     \
+    } while (0)
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// ---- arena ----------------------------------------------------------------
+hipError_t arena_alloc(tqf_hip_ctx *ctx, size_t bytes, void **out) {
+    bytes = align_up(bytes ? bytes : 1, kAlign);
+    if (bytes > kSlabBytes / 2) {
+        uint8_t *p = nullptr;
+        hipError_t e = hipMalloc(&p, bytes);
+        if (e != hipSuccess) return e;
+        ctx->slabs.push_back(Slab{p, bytes, bytes, 1});
+        *out = p;
+        return hipSuccess;
+    }
+    for (auto it = ctx->slabs.rbegin(); it != ctx->slabs.rend(); ++it) {
+        if (it->size == kSlabBytes && it->size - it->used >= bytes) {
+            *out = it->base + it->used;
+            it->used += bytes;
+            it->live += 1;
+            return hipSuccess;
+        }
+    }
+    uint8_t *p = nullptr;
+    hipError_t e = hipMalloc(&p, kSlabBytes);
+    if (e != hipSuccess) return e;
+    ctx->slabs.push_back(Slab{p, kSlabBytes, bytes, 1});
+    *out = p;
+    return hipSuccess;
+}
+
+void arena_free(tqf_hip_ctx *ctx, void *ptr) {
+    if (!ptr) return;
+    uint8_t *p = static_cast<uint8_t *>(ptr);
+    for (size_t i = 0; i < ctx->slabs.size(); ++i) {
+        Slab &s = ctx->slabs[i];
+        if (p >= s.base && p < s.base + s.size) {
+            if (--s.live == 0) {
+                (void)hipFree(s.base);
+                ctx->slabs.erase(ctx->slabs.begin() + (long)i);
+            }
+            return;
+        }
+    }
+}
+
+// ---- graphs ---------------------------------------------------------------
+void drop_graphs(tqf_hip_ctx *ctx) {
+    for (GraphEntry *g : ctx->graphs) {
+        if (g->exec) (void)hipGraphExecDestroy(g->exec);
+        if (g->graph) (void)hipGraphDestroy(g->graph);
+        delete g;
+    }
+    ctx->graphs.clear();
+}
+
+GraphEntry *find_graph(tqf_hip_ctx *ctx, const std::vector<uint64_t> &key) {
+    for (GraphEntry *g : ctx->graphs)
+        if (g->key == key) return g;
+    return nullptr;
+}
+
+// ---- scratch --------------------------------------------------------------
+template <typename T>
+hipError_t grow(T *&ptr, size_t &have, size_t need) {
+    if (have >= need && ptr) return hipSuccess;
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    have = 0;
+    hipError_t e = hipMalloc(&ptr, need);
+    if (e == hipSuccess) have = need;
+    return e;
+}
+
+int32_t ensure_moe_scratch(tqf_hip_ctx *ctx, uint32_t hidden, uint32_t width, uint32_t experts) {
+    Scratch &sc = ctx->scratch;
+    if (sc.xprep && hidden <= sc.hidden && width <= sc.width && experts <= sc.experts)
+        return TQF_HIP_OK;
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    drop_graphs(ctx);
+    hidden = std::max(hidden, sc.hidden);
+    width = std::max(width, sc.width);
+    experts = std::max(experts, sc.experts);
+    (void)hipFree(sc.xprep);
+    (void)hipFree(sc.hprep);
+    (void)hipFree(sc.logits);
+    (void)hipFree(sc.plan);
+    (void)hipFree(sc.partial);
+    (void)hipFree(sc.counters);
+    sc.xprep = sc.hprep = sc.counters = nullptr;
+    sc.logits = sc.partial = nullptr;
+    sc.plan = nullptr;
+    sc.hidden = sc.width = sc.experts = 0;
+    const size_t xprep = (size_t)kMaxTokens * (hidden / 32) * kXprepDwords * 4;
+    const size_t hprep = (size_t)kMaxSlots * kMaxTokens * (width / 32) * kXprepDwords * 4;
+    const size_t logits = (size_t)kMaxTokens * (experts + 1) * 4;
+    const size_t partial = (size_t)((kMaxSlots + 3) / 4) * kMaxTokens * hidden * 4;
+    const size_t counters = (size_t)(64 + hidden / 64) * 4;
+    TQF_HIP(ctx, hipMalloc(&sc.xprep, xprep));
+    TQF_HIP(ctx, hipMalloc(&sc.hprep, hprep));
+    TQF_HIP(ctx, hipMalloc(&sc.logits, logits));
+    TQF_HIP(ctx, hipMalloc(&sc.plan, sizeof(Plan)));
+    TQF_HIP(ctx, hipMalloc(&sc.partial, partial));
+    TQF_HIP(ctx, hipMalloc(&sc.counters, counters));
+    TQF_HIP(ctx, hipMemset(sc.xprep, 0, xprep));
+    TQF_HIP(ctx, hipMemset(sc.hprep, 0, hprep));
+    TQF_HIP(ctx, hipMemset(sc.plan, 0, sizeof(Plan)));
+    TQF_HIP(ctx, hipMemset(sc.counters, 0, counters));
+    sc.hidden = hidden;
+    sc.width = width;
+    sc.experts = experts;
+    return TQF_HIP_OK;
+}
+
+int32_t ensure_accept_scratch(tqf_hip_ctx *ctx, size_t bytes) {
+    Scratch &sc = ctx->scratch;
+    if (sc.accept && sc.accept_bytes >= bytes) return TQF_HIP_OK;
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    drop_graphs(ctx);
+    TQF_HIP(ctx, grow(sc.accept, sc.accept_bytes, bytes));
+    return TQF_HIP_OK;
+}
+
+int32_t ensure_stage(tqf_hip_ctx *ctx, size_t bytes) {
+    if (ctx->d_stage && ctx->stage_bytes >= bytes) return TQF_HIP_OK;
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    TQF_HIP(ctx, grow(ctx->d_stage, ctx->stage_bytes, std::max(bytes, size_t(1) << 20)));
+    return TQF_HIP_OK;
+}
+
+// ---- profiling ------------------------------------------------------------
+hipEvent_t take_event(tqf_hip_ctx *ctx) {
+    if (!ctx->event_pool.empty()) {
+        hipEvent_t e = ctx->event_pool.back();
+        ctx->event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+void resolve_profile(tqf_hip_ctx *ctx) {
+    if (ctx->prof_pending.empty()) return;
+    (void)hipStreamSynchronize(ctx->stream);
+    for (const ProfileSlot &p : ctx->prof_pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, p.start, p.stop) == hipSuccess) {
+            ctx->prof_launches[p.kind] += 1;
+            ctx->prof_ms[p.kind] += ms;
+            double bytes = p.fixed_bytes;
+            if (p.ring_index >= 0) bytes += p.per_slot_bytes * ctx->prof_ring[p.ring_index];
+            ctx->prof_bytes[p.kind] += bytes;
+        }
+        ctx->event_pool.push_back(p.start);
+        ctx->event_pool.push_back(p.stop);
+    }
+    ctx->prof_pending.clear();
+    ctx->prof_ring_next = 0;
+}
+
+struct Prof {
+    tqf_hip_ctx *ctx;
+    hipEvent_t start = nullptr;
+    explicit Prof(tqf_hip_ctx *c) : ctx(c) {
+        if (ctx->profiling && !ctx->capturing) {
+            if (ctx->prof_ring_next >= kRingSize) resolve_profile(ctx);
+            start = take_event(ctx);
+            if (start) (void)hipEventRecord(start, ctx->stream);
+        }
+    }
+    // per_slot_bytes > 0 reads plan->n_slots of the launch just made.
+    void end(int kind, double fixed_bytes, double per_slot_bytes, const Plan *plan) {
+        if (!start) return;
+        hipEvent_t stop = take_event(ctx);
+        if (!stop) return;
+        (void)hipEventRecord(stop, ctx->stream);
+        int ring = -1;
+        if (per_slot_bytes > 0 && plan) {
+            ring = ctx->prof_ring_next++;
+            (void)hipMemcpyAsync(&ctx->prof_ring[ring], &plan->n_slots, sizeof(int32_t),
+                                 hipMemcpyDeviceToHost, ctx->stream);
+        }
+        ctx->prof_pending.push_back(ProfileSlot{start, stop, kind, fixed_bytes, per_slot_bytes, ring});
+        start = nullptr;
+    }
+};
+
+double q4_bytes(uint32_t rows, uint32_t cols) { return (double)rows * (cols / 32) * kQ4Block; }
+
+// ---- validation -----------------------------------------------------------
+bool valid_weights(const tqf_hip_weights *w) { return w && w->tiles; }
+
+// ---- the layer sequence ---------------------------------------------------
+// One MoE layer: route (optionally RMSNorm) -> gate/up -> down (+ residual).
+int32_t enqueue_layer(tqf_hip_ctx *ctx, const LayerDev &L, const float *h, const float *norm,
+                      uint32_t m, const float *resid, float *out, uint16_t *ids, float *w,
+                      int32_t *status) {
+    Scratch &sc = ctx->scratch;
+    const double H = L.hidden, F = L.width;
+    const double pairs = (double)m * (kTopK + 1);
+    {
+        Prof p(ctx);
+        hipError_t e = launch_route(ctx->stream, L, h, norm, m, sc, ids, w, status);
+        if (e != hipSuccess) return hip_fail(ctx, "route kernel launch", e);
+        p.end(TQF_HIP_KERNEL_ROUTE, (L.n_experts + 1) * H * 4 + m * H * 4 + (norm ? H * 4 : 0), 0,
+              nullptr);
+    }
+    {
+        Prof p(ctx);
+        hipError_t e = launch_gate_up(ctx->stream, L, m, sc, sc.plan, sc.xprep);
+        if (e != hipSuccess) return hip_fail(ctx, "gate/up kernel launch", e);
+        p.end(TQF_HIP_KERNEL_GATE_UP, m * H * 4 + pairs * F * 4, 2 * q4_bytes(L.width, L.hidden),
+              sc.plan);
+    }
+    {
+        Prof p(ctx);
+        hipError_t e = launch_down(ctx->stream, L, m, sc, sc.plan, resid, out);
+        if (e != hipSuccess) return hip_fail(ctx, "down kernel launch", e);
+        p.end(TQF_HIP_KERNEL_DOWN, pairs * F * 4 + m * H * 4 * (resid ? 2 : 1),
+              q4_bytes(L.hidden, L.width), sc.plan);
+    }
+    return TQF_HIP_OK;
+}
+
+int32_t enqueue_stack(tqf_hip_ctx *ctx, const tqf_hip_stack *st, float *d_h, uint32_t m,
+                      uint16_t *d_ids, float *d_w, int32_t *d_status) {
+    for (size_t l = 0; l < st->layers.size(); ++l) {
+        const LayerDev &L = st->layers[l]->dev;
+        uint16_t *ids = d_ids ? d_ids + l * (size_t)m * kTopK : nullptr;
+        float *w = d_w ? d_w + l * (size_t)m * kTopK : nullptr;
+        int32_t rc = enqueue_layer(ctx, L, d_h, st->norms[l], m, d_h, d_h, ids, w, d_status);
+        if (rc) return rc;
+    }
+    return TQF_HIP_OK;
+}
+
+int32_t enqueue_accept(tqf_hip_ctx *ctx, const float *t, const float *d, const int32_t *dt,
+                       uint32_t k, uint32_t vocab, float T, int32_t greedy, const float *u,
+                       const float *ur, int32_t *acc, int32_t *tok) {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    Prof p(ctx);
+    hipError_t e = launch_accept(ctx->stream, t, d, dt, k, vocab, T, greedy, u, ur, acc, tok,
+                                 ctx->scratch.accept, e0, e1);
+    if (e != hipSuccess) return hip_fail(ctx, "acceptance kernel launch", e);
+    p.end(TQF_HIP_KERNEL_ACCEPT, (double)(greedy ? k + 1 : 2 * k + 1) * vocab * 4, 0, nullptr);
+    return TQF_HIP_OK;
+}
+
+// Runs `enqueue` eagerly, or captures it once per key into a HIP graph and
+// replays it.  Profiling forces eager execution so events bracket kernels.
+template <typename F>
+int32_t run_graphed(tqf_hip_ctx *ctx, const std::vector<uint64_t> &key, F enqueue) {
+    if (ctx->profiling) return enqueue();
+    GraphEntry *g = find_graph(ctx, key);
+    if (!g) {
+        if (ctx->graphs.size() >= kMaxGraphs) {
+            GraphEntry *old = ctx->graphs.front();
+            (void)hipGraphExecDestroy(old->exec);
+            (void)hipGraphDestroy(old->graph);
+            delete old;
+            ctx->graphs.erase(ctx->graphs.begin());
+        }
+        TQF_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+        ctx->capturing = true;
+        int32_t rc = enqueue();
+        ctx->capturing = false;
+        hipGraph_t graph = nullptr;
+        hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+        if (rc) {
+            if (graph) (void)hipGraphDestroy(graph);
+            return rc;
+        }
+        if (e != hipSuccess) return hip_fail(ctx, "hipStreamEndCapture", e);
+        hipGraphExec_t exec = nullptr;
+        e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            (void)hipGraphDestroy(graph);
+            return hip_fail(ctx, "hipGraphInstantiate", e);
+        }
+        g = new GraphEntry{key, graph, exec};
+        ctx->graphs.push_back(g);
+    }
+    TQF_HIP(ctx, hipGraphLaunch(g->exec, ctx->stream));
+    return TQF_HIP_OK;
+}
+
+uint64_t k64(const void *p) { return (uint64_t)(uintptr_t)p; }
+
+}  // namespace
+
+// ===========================================================================
+// context
+// ===========================================================================
+extern "C" int32_t tqf_hip_create(int32_t device, tqf_hip_ctx **out) {
+    if (!out) return TQF_HIP_ERR_INVALID;
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) return TQF_HIP_ERR_DEVICE;
+    if (device < 0 || device >= count) return TQF_HIP_ERR_INVALID;
+    if (hipSetDevice(device) != hipSuccess) return TQF_HIP_ERR_DEVICE;
+    tqf_hip_ctx *ctx = new tqf_hip_ctx();
+    ctx->device = device;
+    if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete ctx;
+        return TQF_HIP_ERR_DEVICE;
+    }
+    if (hipHostMalloc(reinterpret_cast<void **>(&ctx->prof_ring), kRingSize * sizeof(int32_t),
+                      hipHostMallocDefault) != hipSuccess) {
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return TQF_HIP_ERR_NOMEM;
+    }
+    const size_t adhoc = align_up(3 * sizeof(void *), kAlign) + sizeof(Plan);
+    uint8_t *p = nullptr;
+    if (hipMalloc(&p, adhoc) != hipSuccess) {
+        (void)hipHostFree(ctx->prof_ring);
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return TQF_HIP_ERR_NOMEM;
+    }
+    ctx->d_adhoc_mats = reinterpret_cast<const uint8_t **>(p);
+    ctx->d_adhoc_plan = reinterpret_cast<Plan *>(p + align_up(3 * sizeof(void *), kAlign));
+    *out = ctx;
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_destroy(tqf_hip_ctx *ctx) {
+    if (!ctx) return TQF_HIP_ERR_INVALID;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    drop_graphs(ctx);
+    for (const ProfileSlot &p : ctx->prof_pending) {
+        (void)hipEventDestroy(p.start);
+        (void)hipEventDestroy(p.stop);
+    }
+    for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
+    Scratch &sc = ctx->scratch;
+    (void)hipFree(sc.xprep);
+    (void)hipFree(sc.hprep);
+    (void)hipFree(sc.logits);
+    (void)hipFree(sc.plan);
+    (void)hipFree(sc.partial);
+    (void)hipFree(sc.counters);
+    (void)hipFree(sc.accept);
+    (void)hipFree(ctx->d_stage);
+    (void)hipFree(ctx->d_table);
+    (void)hipFree(ctx->d_gemv_xprep);
+    (void)hipFree(const_cast<const uint8_t **>(ctx->d_adhoc_mats));
+    for (Slab &s : ctx->slabs) (void)hipFree(s.base);
+    (void)hipHostFree(ctx->prof_ring);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return TQF_HIP_OK;
+}
+
+extern "C" const char *tqf_hip_last_error(const tqf_hip_ctx *ctx) {
+    return ctx ? ctx->last_error.c_str() : "null context";
+}
+
+extern "C" int32_t tqf_hip_synchronize(tqf_hip_ctx *ctx) {
+    TQF_ENTER(ctx);
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_device_info(tqf_hip_ctx *ctx, char *name, size_t name_len,
+                                       int32_t *cu_count) {
+    TQF_ENTER(ctx);
+    hipDeviceProp_t prop;
+    TQF_HIP(ctx, hipGetDeviceProperties(&prop, ctx->device));
+    if (name && name_len) {
+        std::snprintf(name, name_len, "%s (%s)", prop.name, prop.gcnArchName);
+    }
+    if (cu_count) *cu_count = prop.multiProcessorCount;
+    return TQF_HIP_OK;
+}
+
+// ===========================================================================
+// plain buffers
+// ===========================================================================
+extern "C" int32_t tqf_hip_buffer_alloc(tqf_hip_ctx *ctx, size_t bytes, void **dptr) {
+    TQF_ENTER(ctx);
+    if (!dptr) return fail(ctx, TQF_HIP_ERR_INVALID, "null output pointer");
+    *dptr = nullptr;
+    hipError_t e = hipMalloc(dptr, bytes ? bytes : 1);
+    if (e != hipSuccess) {
+        *dptr = nullptr;
+        return fail(ctx, TQF_HIP_ERR_NOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
+    }
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_buffer_free(tqf_hip_ctx *ctx, void *dptr) {
+    TQF_ENTER(ctx);
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    TQF_HIP(ctx, hipFree(dptr));
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_memcpy_h2d(tqf_hip_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    TQF_ENTER(ctx);
+    TQF_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_memcpy_d2h(tqf_hip_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    TQF_ENTER(ctx);
+    TQF_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return TQF_HIP_OK;
+}
+
+// ===========================================================================
+// weights
+// ===========================================================================
+extern "C" uint64_t tqf_hip_weights_bytes_for(uint32_t rows, uint32_t cols) {
+    if (rows == 0 || cols == 0 || cols % 32) return 0;
+    return align_up(tile_bytes(matrix_dims(rows, cols)), kAlign) + kAlign;
+}
+
+namespace {
+int32_t weights_alloc(tqf_hip_ctx *ctx, uint32_t rows, uint32_t cols, tqf_hip_weights **out) {
+    const MatrixDims d = matrix_dims(rows, cols);
+    const size_t bytes = tile_bytes(d);
+    void *tiles = nullptr, *self = nullptr;
+    hipError_t e = arena_alloc(ctx, bytes, &tiles);
+    if (e != hipSuccess) return fail(ctx, TQF_HIP_ERR_NOMEM, "weights allocation failed");
+    e = arena_alloc(ctx, sizeof(void *), &self);
+    if (e != hipSuccess) {
+        arena_free(ctx, tiles);
+        return fail(ctx, TQF_HIP_ERR_NOMEM, "weights allocation failed");
+    }
+    const uint8_t *tp = static_cast<const uint8_t *>(tiles);
+    e = hipMemsetAsync(tiles, 0, bytes, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpy(self, &tp, sizeof(void *), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        arena_free(ctx, self);
+        arena_free(ctx, tiles);
+        return hip_fail(ctx, "weights initialisation", e);
+    }
+    tqf_hip_weights *w = new tqf_hip_weights();
+    w->dims = d;
+    w->tiles = static_cast<uint8_t *>(tiles);
+    w->bytes = bytes;
+    w->d_self = static_cast<const uint8_t **>(self);
+    *out = w;
+    return TQF_HIP_OK;
+}
+
+void weights_release(tqf_hip_ctx *ctx, tqf_hip_weights *w) {
+    arena_free(ctx, const_cast<const uint8_t **>(w->d_self));
+    arena_free(ctx, w->tiles);
+    delete w;
+}
+
+int32_t check_q4_shape(tqf_hip_ctx *ctx, size_t len, uint32_t rows, uint32_t cols) {
+    if (rows == 0 || cols == 0 || cols % 32)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "Q4_0 matrix needs rows > 0 and cols a positive multiple of 32");
+    if (len != (size_t)rows * (cols / 32) * kQ4Block)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "Q4_0 byte length does not match rows x cols");
+    return TQF_HIP_OK;
+}
+}  // namespace
+
+extern "C" int32_t tqf_hip_weights_upload(tqf_hip_ctx *ctx, const uint8_t *q4_0, size_t len,
+                                          uint32_t rows, uint32_t cols, tqf_hip_weights **out) {
+    TQF_ENTER(ctx);
+    if (!q4_0 || !out) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    *out = nullptr;
+    if (int32_t rc = check_q4_shape(ctx, len, rows, cols)) return rc;
+    if (int32_t rc = ensure_stage(ctx, len)) return rc;
+    tqf_hip_weights *w = nullptr;
+    if (int32_t rc = weights_alloc(ctx, rows, cols, &w)) return rc;
+    hipError_t e = hipMemcpyAsync(ctx->d_stage, q4_0, len, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess)
+        e = launch_repack(ctx->stream, static_cast<const uint8_t *>(ctx->d_stage), w->dims, w->tiles);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        weights_release(ctx, w);
+        return hip_fail(ctx, "weights upload", e);
+    }
+    *out = w;
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_weights_upload_device(tqf_hip_ctx *ctx, const void *d_q4_0, size_t len,
+                                                 uint32_t rows, uint32_t cols,
+                                                 tqf_hip_weights **out) {
+    TQF_ENTER(ctx);
+    if (!d_q4_0 || !out) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    *out = nullptr;
+    if (int32_t rc = check_q4_shape(ctx, len, rows, cols)) return rc;
+    tqf_hip_weights *w = nullptr;
+    if (int32_t rc = weights_alloc(ctx, rows, cols, &w)) return rc;
+    hipError_t e = launch_repack(ctx->stream, static_cast<const uint8_t *>(d_q4_0), w->dims, w->tiles);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        weights_release(ctx, w);
+        return hip_fail(ctx, "weights upload", e);
+    }
+    *out = w;
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_weights_synth(tqf_hip_ctx *ctx, uint32_t rows, uint32_t cols,
+                                         uint32_t tensor_id, uint32_t seed, tqf_hip_weights **out) {
+    TQF_ENTER(ctx);
+    if (!out) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    *out = nullptr;
+    if (rows == 0 || cols == 0 || cols % 32)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "Q4_0 matrix needs cols a positive multiple of 32");
+    tqf_hip_weights *w = nullptr;
+    if (int32_t rc = weights_alloc(ctx, rows, cols, &w)) return rc;
+    hipError_t e = launch_synth_q4_0(ctx->stream, w->dims, tensor_id, seed, w->tiles);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        weights_release(ctx, w);
+        return hip_fail(ctx, "synthetic weights", e);
+    }
+    *out = w;
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_weights_download(tqf_hip_ctx *ctx, const tqf_hip_weights *w,
+                                            uint8_t *q4_0, size_t len) {
+    TQF_ENTER(ctx);
+    if (!valid_weights(w) || !q4_0) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    const MatrixDims &d = w->dims;
+    const uint32_t blocks = d.cols / 32;
+    if (len != (size_t)d.rows * blocks * kQ4Block)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "Q4_0 byte length does not match the matrix");
+    std::vector<uint8_t> tiles(w->bytes);
+    TQF_HIP(ctx, hipMemcpyAsync(tiles.data(), w->tiles, w->bytes, hipMemcpyDeviceToHost, ctx->stream));
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    for (uint32_t r = 0; r < d.rows; ++r) {
+        const uint32_t g = r / kRowsPerGroup, lane = r % kRowsPerGroup;
+        for (uint32_t b = 0; b < blocks; ++b) {
+            const uint8_t *tile = tiles.data() + ((size_t)g * d.chunks + b / kChunkBlocks) * kTileBytes;
+            const uint32_t j = b % kChunkBlocks;
+            uint8_t *dst = q4_0 + ((size_t)r * blocks + b) * kQ4Block;
+            std::memcpy(dst, tile + kTileNibbleBytes + lane * 16 + j * 2, 2);
+            std::memcpy(dst + 2, tile + j * 1024 + lane * 16, 16);
+        }
+    }
+    return TQF_HIP_OK;
+}
+
+extern "C" uint64_t tqf_hip_weights_bytes(const tqf_hip_weights *w) { return w ? w->bytes : 0; }
+
+extern "C" int32_t tqf_hip_weights_free(tqf_hip_ctx *ctx, tqf_hip_weights *w) {
+    TQF_ENTER(ctx);
+    if (!w) return TQF_HIP_OK;
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    drop_graphs(ctx);
+    weights_release(ctx, w);
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_tensor_upload(tqf_hip_ctx *ctx, const float *data, size_t count,
+                                         tqf_hip_tensor **out) {
+    TQF_ENTER(ctx);
+    if (!data || !out || count == 0) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer or empty tensor");
+    *out = nullptr;
+    void *p = nullptr;
+    if (arena_alloc(ctx, count * sizeof(float), &p) != hipSuccess)
+        return fail(ctx, TQF_HIP_ERR_NOMEM, "tensor allocation failed");
+    hipError_t e = hipMemcpyAsync(p, data, count * sizeof(float), hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        arena_free(ctx, p);
+        return hip_fail(ctx, "tensor upload", e);
+    }
+    *out = new tqf_hip_tensor{static_cast<float *>(p), count};
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_tensor_free(tqf_hip_ctx *ctx, tqf_hip_tensor *t) {
+    TQF_ENTER(ctx);
+    if (!t) return TQF_HIP_OK;
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    drop_graphs(ctx);
+    arena_free(ctx, t->data);
+    delete t;
+    return TQF_HIP_OK;
+}
+
+// ===========================================================================
+// GEMV
+// ===========================================================================
+namespace {
+int32_t gemv_enqueue(tqf_hip_ctx *ctx, const uint8_t *const *table, uint32_t count,
+                     const MatrixDims &d, const float *d_x, uint32_t m, float *d_y) {
+    const uint32_t bp = d.chunks * kChunkBlocks;
+    const size_t xb = (size_t)m * bp * kXprepDwords * 4;
+    if (!ctx->d_gemv_xprep || ctx->gemv_xprep_bytes < xb) {
+        TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        drop_graphs(ctx);
+        TQF_HIP(ctx, grow(ctx->d_gemv_xprep, ctx->gemv_xprep_bytes, xb));
+    }
+    hipError_t e = launch_prep(ctx->stream, d_x, m, d.cols, bp, ctx->d_gemv_xprep);
+    if (e != hipSuccess) return hip_fail(ctx, "prep kernel launch", e);
+    Prof p(ctx);
+    e = launch_gemv(ctx->stream, table, count, d, ctx->d_gemv_xprep, m, d_y);
+    if (e != hipSuccess) return hip_fail(ctx, "gemv kernel launch", e);
+    p.end(TQF_HIP_KERNEL_GEMV,
+          (double)count * (q4_bytes(d.rows, d.cols) + (double)m * d.rows * 4) + (double)m * d.cols * 4,
+          0, nullptr);
+    return TQF_HIP_OK;
+}
+}  // namespace
+
+extern "C" int32_t tqf_hip_q4_gemv(tqf_hip_ctx *ctx, const tqf_hip_weights *w, const float *x,
+                                   uint32_t m, float *y) {
+    TQF_ENTER(ctx);
+    if (!valid_weights(w) || !x || !y) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (m == 0 || m > kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "m must be in 1..8");
+    const MatrixDims &d = w->dims;
+    const size_t xb = (size_t)m * d.cols * 4, yb = (size_t)m * d.rows * 4;
+    if (int32_t rc = ensure_stage(ctx, align_up(xb, kAlign) + yb)) return rc;
+    float *dx = static_cast<float *>(ctx->d_stage);
+    float *dy = reinterpret_cast<float *>(static_cast<uint8_t *>(ctx->d_stage) + align_up(xb, kAlign));
+    TQF_HIP(ctx, hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream));
+    if (int32_t rc = gemv_enqueue(ctx, w->d_self, 1, d, dx, m, dy)) return rc;
+    TQF_HIP(ctx, hipMemcpyAsync(y, dy, yb, hipMemcpyDeviceToHost, ctx->stream));
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_q4_gemv_device(tqf_hip_ctx *ctx, const tqf_hip_weights *w,
+                                          const float *d_x, uint32_t m, float *d_y) {
+    TQF_ENTER(ctx);
+    if (!valid_weights(w) || !d_x || !d_y) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (m == 0 || m > kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "m must be in 1..8");
+    return gemv_enqueue(ctx, w->d_self, 1, w->dims, d_x, m, d_y);
+}
+
+extern "C" int32_t tqf_hip_q4_gemv_batched_device(tqf_hip_ctx *ctx,
+                                                  const tqf_hip_weights *const *ws, uint32_t count,
+                                                  const float *d_x, float *d_y) {
+    TQF_ENTER(ctx);
+    if (!ws || !d_x || !d_y || count == 0) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer or count 0");
+    if (count > 65535) return fail(ctx, TQF_HIP_ERR_INVALID, "count must be <= 65535");
+    std::vector<const uint8_t *> table(count);
+    for (uint32_t i = 0; i < count; ++i) {
+        if (!valid_weights(ws[i])) return fail(ctx, TQF_HIP_ERR_INVALID, "null weights in batch");
+        if (ws[i]->dims.rows != ws[0]->dims.rows || ws[i]->dims.cols != ws[0]->dims.cols)
+            return fail(ctx, TQF_HIP_ERR_INVALID, "batched matrices must share one shape");
+        table[i] = ws[i]->tiles;
+    }
+    if (table != ctx->table_shadow) {
+        TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        drop_graphs(ctx);
+        TQF_HIP(ctx, grow(ctx->d_table, ctx->table_cap, count * sizeof(void *)));
+        TQF_HIP(ctx, hipMemcpy(ctx->d_table, table.data(), count * sizeof(void *), hipMemcpyHostToDevice));
+        ctx->table_shadow = table;
+    }
+    return gemv_enqueue(ctx, ctx->d_table, count, ws[0]->dims, d_x, 1, d_y);
+}
+
+// ===========================================================================
+// expert forward
+// ===========================================================================
+extern "C" int32_t tqf_hip_expert_forward(tqf_hip_ctx *ctx, const tqf_hip_weights *gate,
+                                          const tqf_hip_weights *up, const tqf_hip_weights *down,
+                                          const float *x, uint32_t m, float *y) {
+    TQF_ENTER(ctx);
+    if (!valid_weights(gate) || !valid_weights(up) || !valid_weights(down) || !x || !y)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (m == 0 || m > kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "m must be in 1..8");
+    const uint32_t F = gate->dims.rows, H = gate->dims.cols;
+    if (up->dims.rows != F || up->dims.cols != H || down->dims.rows != H || down->dims.cols != F)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "expert shapes: gate/up [width x hidden], down [hidden x width]");
+    if (H % 256 || F % 256)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "expert hidden and width must be multiples of 256");
+    if (int32_t rc = ensure_moe_scratch(ctx, H, F, 0)) return rc;
+    const size_t xb = (size_t)m * H * 4;
+    if (int32_t rc = ensure_stage(ctx, 2 * align_up(xb, kAlign))) return rc;
+    float *dx = static_cast<float *>(ctx->d_stage);
+    float *dy = reinterpret_cast<float *>(static_cast<uint8_t *>(ctx->d_stage) + align_up(xb, kAlign));
+    const uint8_t *mats[3] = {gate->tiles, up->tiles, down->tiles};
+    Plan plan;
+    std::memset(&plan, 0, sizeof plan);
+    plan.n_slots = 1;
+    plan.slot_expert[0] = 0;
+    plan.slot_mask[0] = (1u << m) - 1u;
+    for (uint32_t t = 0; t < m; ++t) plan.coef[0][t] = 1.0f;
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    drop_graphs(ctx);
+    TQF_HIP(ctx, hipMemcpy(ctx->d_adhoc_mats, mats, sizeof mats, hipMemcpyHostToDevice));
+    TQF_HIP(ctx, hipMemcpy(ctx->d_adhoc_plan, &plan, sizeof plan, hipMemcpyHostToDevice));
+    TQF_HIP(ctx, hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream));
+    LayerDev L{nullptr, nullptr, ctx->d_adhoc_mats, 0, H, F};
+    Scratch &sc = ctx->scratch;
+    hipError_t e = launch_prep(ctx->stream, dx, m, H, H / 32, sc.xprep);
+    if (e == hipSuccess) e = launch_gate_up(ctx->stream, L, m, sc, ctx->d_adhoc_plan, sc.xprep);
+    if (e == hipSuccess) e = launch_down(ctx->stream, L, m, sc, ctx->d_adhoc_plan, nullptr, dy);
+    if (e != hipSuccess) return hip_fail(ctx, "expert kernels", e);
+    TQF_HIP(ctx, hipMemcpyAsync(y, dy, xb, hipMemcpyDeviceToHost, ctx->stream));
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return TQF_HIP_OK;
+}
+
+// ===========================================================================
+// MoE layer
+// ===========================================================================
+extern "C" int32_t tqf_hip_moe_layer_prepare(tqf_hip_ctx *ctx, const tqf_hip_moe_weights *mw,
+                                             tqf_hip_layer **out) {
+    TQF_ENTER(ctx);
+    if (!mw || !out) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    *out = nullptr;
+    const uint32_t E = mw->n_experts, H = mw->hidden, F = mw->width;
+    if (E != 256) return fail(ctx, TQF_HIP_ERR_INVALID, "router requires n_experts == 256 (experts/mod.rs:135)");
+    if (H == 0 || H % 256 || H > 2048) return fail(ctx, TQF_HIP_ERR_INVALID, "hidden must be a multiple of 256, at most 2048");
+    if (F == 0 || F % 256) return fail(ctx, TQF_HIP_ERR_INVALID, "width must be a multiple of 256");
+    if (!mw->router || mw->router->count != (size_t)E * H)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "router must be f32 [n_experts x hidden]");
+    if (!mw->shared_input_gate || mw->shared_input_gate->count != H)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "shared_input_gate must be f32 [hidden]");
+    if (!mw->routed_gate || !mw->routed_up || !mw->routed_down)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "null routed expert table");
+    auto ok_gu = [&](const tqf_hip_weights *w) { return valid_weights(w) && w->dims.rows == F && w->dims.cols == H; };
+    auto ok_d = [&](const tqf_hip_weights *w) { return valid_weights(w) && w->dims.rows == H && w->dims.cols == F; };
+    std::vector<const uint8_t *> mats((size_t)(E + 1) * 3);
+    for (uint32_t e = 0; e <= E; ++e) {
+        const tqf_hip_weights *g = e < E ? mw->routed_gate[e] : mw->shared_gate;
+        const tqf_hip_weights *u = e < E ? mw->routed_up[e] : mw->shared_up;
+        const tqf_hip_weights *d = e < E ? mw->routed_down[e] : mw->shared_down;
+        if (!ok_gu(g) || !ok_gu(u) || !ok_d(d))
+            return fail(ctx, TQF_HIP_ERR_INVALID,
+                        "expert " + std::to_string(e) + ": gate/up must be [width x hidden] and down [hidden x width]");
+        mats[(size_t)e * 3 + 0] = g->tiles;
+        mats[(size_t)e * 3 + 1] = u->tiles;
+        mats[(size_t)e * 3 + 2] = d->tiles;
+    }
+    if (int32_t rc = ensure_moe_scratch(ctx, H, F, E)) return rc;
+    void *dm = nullptr;
+    if (arena_alloc(ctx, mats.size() * sizeof(void *), &dm) != hipSuccess)
+        return fail(ctx, TQF_HIP_ERR_NOMEM, "layer table allocation failed");
+    hipError_t e = hipMemcpy(dm, mats.data(), mats.size() * sizeof(void *), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        arena_free(ctx, dm);
+        return hip_fail(ctx, "layer table upload", e);
+    }
+    tqf_hip_layer *layer = new tqf_hip_layer();
+    layer->d_mats = static_cast<const uint8_t **>(dm);
+    layer->dev = LayerDev{mw->router->data, mw->shared_input_gate->data, layer->d_mats, E, H, F};
+    *out = layer;
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_moe_layer_free(tqf_hip_ctx *ctx, tqf_hip_layer *layer) {
+    TQF_ENTER(ctx);
+    if (!layer) return TQF_HIP_OK;
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    drop_graphs(ctx);
+    arena_free(ctx, const_cast<const uint8_t **>(layer->d_mats));
+    delete layer;
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_moe_layer_device(tqf_hip_ctx *ctx, const tqf_hip_layer *layer,
+                                            const float *d_x, uint32_t m, float *d_y,
+                                            uint16_t *d_ids, float *d_w, int32_t *d_status) {
+    TQF_ENTER(ctx);
+    if (!layer || !d_x || !d_y) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (m == 0 || m > kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "m must be in 1..8");
+    if (d_x == d_y) return fail(ctx, TQF_HIP_ERR_INVALID, "x and y must not alias");
+    const LayerDev &L = layer->dev;
+    if (int32_t rc = ensure_moe_scratch(ctx, L.hidden, L.width, L.n_experts)) return rc;
+    return enqueue_layer(ctx, L, d_x, nullptr, m, nullptr, d_y, d_ids, d_w, d_status);
+}
+
+extern "C" int32_t tqf_hip_moe_layer(tqf_hip_ctx *ctx, const tqf_hip_layer *layer, const float *x,
+                                     uint32_t m, float *y, uint16_t *ids, float *w) {
+    TQF_ENTER(ctx);
+    if (!layer || !x || !y) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (m == 0 || m > kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "m must be in 1..8");
+    const LayerDev &L = layer->dev;
+    if (int32_t rc = ensure_moe_scratch(ctx, L.hidden, L.width, L.n_experts)) return rc;
+    const size_t xb = align_up((size_t)m * L.hidden * 4, kAlign);
+    const size_t ib = align_up((size_t)m * kTopK * 2, kAlign), wb = align_up((size_t)m * kTopK * 4, kAlign);
+    if (int32_t rc = ensure_stage(ctx, 2 * xb + ib + wb + kAlign)) return rc;
+    uint8_t *base = static_cast<uint8_t *>(ctx->d_stage);
+    float *dx = reinterpret_cast<float *>(base);
+    float *dy = reinterpret_cast<float *>(base + xb);
+    uint16_t *dids = reinterpret_cast<uint16_t *>(base + 2 * xb);
+    float *dw = reinterpret_cast<float *>(base + 2 * xb + ib);
+    int32_t *dstatus = reinterpret_cast<int32_t *>(base + 2 * xb + ib + wb);
+    const int32_t zero = 0;
+    TQF_HIP(ctx, hipMemcpyAsync(dstatus, &zero, 4, hipMemcpyHostToDevice, ctx->stream));
+    TQF_HIP(ctx, hipMemcpyAsync(dx, x, (size_t)m * L.hidden * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (int32_t rc = enqueue_layer(ctx, L, dx, nullptr, m, nullptr, dy, dids, dw, dstatus)) return rc;
+    int32_t status = 0;
+    TQF_HIP(ctx, hipMemcpyAsync(&status, dstatus, 4, hipMemcpyDeviceToHost, ctx->stream));
+    TQF_HIP(ctx, hipMemcpyAsync(y, dy, (size_t)m * L.hidden * 4, hipMemcpyDeviceToHost, ctx->stream));
+    if (ids) TQF_HIP(ctx, hipMemcpyAsync(ids, dids, (size_t)m * kTopK * 2, hipMemcpyDeviceToHost, ctx->stream));
+    if (w) TQF_HIP(ctx, hipMemcpyAsync(w, dw, (size_t)m * kTopK * 4, hipMemcpyDeviceToHost, ctx->stream));
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (status != 0)
+        return fail(ctx, TQF_HIP_ERR_ROUTER, "exact router logits must all be finite (experts/mod.rs:136-141)");
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_moe_layer_bf16(tqf_hip_ctx *ctx, const tqf_hip_layer *layer,
+                                          const uint16_t *x_bf16, uint32_t m, float *y,
+                                          uint16_t *ids, float *w) {
+    TQF_ENTER(ctx);
+    if (!layer || !x_bf16 || !y) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (m == 0 || m > kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "m must be in 1..8");
+    const size_t n = (size_t)m * layer->dev.hidden;
+    std::vector<float> x(n);
+    for (size_t i = 0; i < n; ++i) {
+        const uint32_t bits = (uint32_t)x_bf16[i] << 16;
+        std::memcpy(&x[i], &bits, 4);
+    }
+    return tqf_hip_moe_layer(ctx, layer, x.data(), m, y, ids, w);
+}
+
+// ===========================================================================
+// stack
+// ===========================================================================
+extern "C" int32_t tqf_hip_stack_prepare(tqf_hip_ctx *ctx, const tqf_hip_layer *const *layers,
+                                         const tqf_hip_tensor *const *ffn_norms, uint32_t n_layers,
+                                         tqf_hip_stack **out) {
+    TQF_ENTER(ctx);
+    if (!layers || !ffn_norms || !out || n_layers == 0)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer or no layers");
+    *out = nullptr;
+    tqf_hip_stack *st = new tqf_hip_stack();
+    st->hidden = layers[0] ? layers[0]->dev.hidden : 0;
+    st->width = layers[0] ? layers[0]->dev.width : 0;
+    st->experts = layers[0] ? layers[0]->dev.n_experts : 0;
+    for (uint32_t l = 0; l < n_layers; ++l) {
+        const tqf_hip_layer *L = layers[l];
+        const tqf_hip_tensor *nw = ffn_norms[l];
+        if (!L || !nw || L->dev.hidden != st->hidden || L->dev.width != st->width ||
+            L->dev.n_experts != st->experts || nw->count != st->hidden) {
+            delete st;
+            return fail(ctx, TQF_HIP_ERR_INVALID,
+                        "layer " + std::to_string(l) + ": layers must share one geometry and norms be f32 [hidden]");
+        }
+        st->layers.push_back(L);
+        st->norms.push_back(nw->data);
+    }
+    *out = st;
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_stack_free(tqf_hip_ctx *ctx, tqf_hip_stack *stack) {
+    TQF_ENTER(ctx);
+    if (!stack) return TQF_HIP_OK;
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    drop_graphs(ctx);
+    delete stack;
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_stack_forward_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack,
+                                                float *d_h, uint32_t m, uint16_t *d_ids,
+                                                float *d_w, int32_t *d_status) {
+    TQF_ENTER(ctx);
+    if (!stack || !d_h) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (m == 0 || m > kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "m must be in 1..8");
+    if (int32_t rc = ensure_moe_scratch(ctx, stack->hidden, stack->width, stack->experts)) return rc;
+    std::vector<uint64_t> key = {1, k64(stack), k64(d_h), m, k64(d_ids), k64(d_w), k64(d_status)};
+    return run_graphed(ctx, key, [&]() { return enqueue_stack(ctx, stack, d_h, m, d_ids, d_w, d_status); });
+}
+
+// ===========================================================================
+// acceptance
+// ===========================================================================
+namespace {
+int32_t check_accept(tqf_hip_ctx *ctx, uint32_t k, uint32_t vocab, float T, int32_t greedy,
+                     bool have_draft, bool have_u) {
+    if (vocab == 0) return fail(ctx, TQF_HIP_ERR_INVALID, "vocab must be > 0");
+    if (k > kMaxTokens - 1) return fail(ctx, TQF_HIP_ERR_INVALID, "k must be <= 7");
+    if (!greedy) {
+        if (!(T > 0.0f) || !(T <= 3.402823466e38f))
+            return fail(ctx, TQF_HIP_ERR_INVALID, "temperature must be finite and > 0 when sampling");
+        if (!have_draft || !have_u)
+            return fail(ctx, TQF_HIP_ERR_INVALID, "stochastic acceptance needs draft logits and uniforms");
+    }
+    return TQF_HIP_OK;
+}
+}  // namespace
+
+extern "C" int32_t tqf_hip_accept_device(tqf_hip_ctx *ctx, const float *d_target,
+                                         const float *d_draft, const int32_t *d_draft_tokens,
+                                         uint32_t k, uint32_t vocab, float temperature,
+                                         int32_t greedy, const float *d_u, const float *d_ures,
+                                         int32_t *d_accepted, int32_t *d_tokens) {
+    TQF_ENTER(ctx);
+    if (!d_target || !d_accepted || !d_tokens || (k > 0 && !d_draft_tokens))
+        return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (int32_t rc = check_accept(ctx, k, vocab, temperature, greedy, d_draft != nullptr,
+                                  d_u != nullptr && d_ures != nullptr))
+        return rc;
+    if (int32_t rc = ensure_accept_scratch(ctx, accept_scratch_bytes(k, vocab))) return rc;
+    return enqueue_accept(ctx, d_target, d_draft, d_draft_tokens, k, vocab, temperature, greedy,
+                          d_u, d_ures, d_accepted, d_tokens);
+}
+
+extern "C" int32_t tqf_hip_accept(tqf_hip_ctx *ctx, const float *target, const float *draft,
+                                  const int32_t *draft_tokens, uint32_t k, uint32_t vocab,
+                                  float temperature, int32_t greedy, const float *u,
+                                  const float *u_resample, int32_t *accepted,
+                                  int32_t *tokens_out) {
+    TQF_ENTER(ctx);
+    if (!target || !accepted || !tokens_out || (k > 0 && !draft_tokens))
+        return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (int32_t rc = check_accept(ctx, k, vocab, temperature, greedy, draft != nullptr,
+                                  u != nullptr && u_resample != nullptr))
+        return rc;
+    for (uint32_t i = 0; i < k; ++i)
+        if (draft_tokens[i] < 0 || (uint32_t)draft_tokens[i] >= vocab)
+            return fail(ctx, TQF_HIP_ERR_INVALID, "draft token out of vocabulary");
+    if (!greedy) {
+        for (uint32_t i = 0; i < k; ++i)
+            if (!(u[i] >= 0.0f && u[i] < 1.0f)) return fail(ctx, TQF_HIP_ERR_INVALID, "uniforms must lie in [0, 1)");
+        for (uint32_t i = 0; i <= k; ++i)
+            if (!(u_resample[i] >= 0.0f && u_resample[i] < 1.0f))
+                return fail(ctx, TQF_HIP_ERR_INVALID, "uniforms must lie in [0, 1)");
+    }
+    const size_t tb = align_up((size_t)(k + 1) * vocab * 4, kAlign);
+    const size_t db = greedy ? 0 : align_up((size_t)k * vocab * 4, kAlign);
+    const size_t small = 4 * kAlign;
+    if (int32_t rc = ensure_stage(ctx, tb + db + small)) return rc;
+    if (int32_t rc = ensure_accept_scratch(ctx, accept_scratch_bytes(k, vocab))) return rc;
+    uint8_t *base = static_cast<uint8_t *>(ctx->d_stage);
+    float *dt = reinterpret_cast<float *>(base);
+    float *dd = greedy ? nullptr : reinterpret_cast<float *>(base + tb);
+    uint8_t *sm = base + tb + db;
+    int32_t *dtok = reinterpret_cast<int32_t *>(sm);
+    float *du = reinterpret_cast<float *>(sm + kAlign);
+    float *dur = reinterpret_cast<float *>(sm + 2 * kAlign);
+    int32_t *dout = reinterpret_cast<int32_t *>(sm + 3 * kAlign);  // [accepted, tokens...]
+    TQF_HIP(ctx, hipMemcpyAsync(dt, target, (size_t)(k + 1) * vocab * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (!greedy) {
+        TQF_HIP(ctx, hipMemcpyAsync(dd, draft, (size_t)k * vocab * 4, hipMemcpyHostToDevice, ctx->stream));
+        if (k) TQF_HIP(ctx, hipMemcpyAsync(du, u, k * 4, hipMemcpyHostToDevice, ctx->stream));
+        TQF_HIP(ctx, hipMemcpyAsync(dur, u_resample, (k + 1) * 4, hipMemcpyHostToDevice, ctx->stream));
+    }
+    if (k) TQF_HIP(ctx, hipMemcpyAsync(dtok, draft_tokens, k * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (int32_t rc = enqueue_accept(ctx, dt, dd, k ? dtok : nullptr, k, vocab, temperature, greedy,
+                                    greedy ? nullptr : du, greedy ? nullptr : dur, dout, dout + 1))
+        return rc;
+    std::vector<int32_t> res(k + 2);
+    TQF_HIP(ctx, hipMemcpyAsync(res.data(), dout, (k + 2) * 4, hipMemcpyDeviceToHost, ctx->stream));
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    *accepted = res[0];
+    std::memcpy(tokens_out, res.data() + 1, (k + 1) * 4);
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_top_logit_candidates(tqf_hip_ctx *ctx, const float *logits,
+                                                uint32_t rows, uint32_t vocab, uint32_t *tokens4,
+                                                float *logits4) {
+    TQF_ENTER(ctx);
+    if (!logits || !tokens4 || !logits4 || rows == 0 || vocab == 0)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer or empty logits");
+    if (rows > 65535) return fail(ctx, TQF_HIP_ERR_INVALID, "rows must be <= 65535");
+    const size_t lb = align_up((size_t)rows * vocab * 4, kAlign);
+    const size_t ob = align_up((size_t)rows * 16, kAlign);
+    if (int32_t rc = ensure_stage(ctx, lb + 2 * ob)) return rc;
+    uint8_t *base = static_cast<uint8_t *>(ctx->d_stage);
+    float *dl = reinterpret_cast<float *>(base);
+    uint32_t *dtok = reinterpret_cast<uint32_t *>(base + lb);
+    float *dval = reinterpret_cast<float *>(base + lb + ob);
+    TQF_HIP(ctx, hipMemcpyAsync(dl, logits, (size_t)rows * vocab * 4, hipMemcpyHostToDevice, ctx->stream));
+    hipError_t e = launch_top4(ctx->stream, dl, rows, vocab, dtok, dval);
+    if (e != hipSuccess) return hip_fail(ctx, "top-4 kernel launch", e);
+    TQF_HIP(ctx, hipMemcpyAsync(tokens4, dtok, (size_t)rows * 16, hipMemcpyDeviceToHost, ctx->stream));
+    TQF_HIP(ctx, hipMemcpyAsync(logits4, dval, (size_t)rows * 16, hipMemcpyDeviceToHost, ctx->stream));
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return TQF_HIP_OK;
+}
+
+// ===========================================================================
+// verify step
+// ===========================================================================
+extern "C" int32_t tqf_hip_verify_step_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack,
+                                              float *d_h, uint32_t m, const float *d_target,
+                                              const float *d_draft, const int32_t *d_dtok,
+                                              uint32_t vocab, float temperature, int32_t greedy,
+                                              const float *d_u, const float *d_ures,
+                                              int32_t *d_accepted, int32_t *d_tokens) {
+    TQF_ENTER(ctx);
+    if (!stack || !d_h || !d_target || !d_accepted || !d_tokens)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (m == 0 || m > kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "m must be in 1..8");
+    const uint32_t k = m - 1;
+    if (k > 0 && !d_dtok) return fail(ctx, TQF_HIP_ERR_INVALID, "null draft tokens");
+    if (int32_t rc = check_accept(ctx, k, vocab, temperature, greedy, d_draft != nullptr,
+                                  d_u != nullptr && d_ures != nullptr))
+        return rc;
+    if (int32_t rc = ensure_moe_scratch(ctx, stack->hidden, stack->width, stack->experts)) return rc;
+    if (int32_t rc = ensure_accept_scratch(ctx, accept_scratch_bytes(k, vocab))) return rc;
+    uint32_t tbits;
+    std::memcpy(&tbits, &temperature, 4);
+    std::vector<uint64_t> key = {2,          k64(stack), k64(d_h),   m,           k64(d_target),
+                                 k64(d_draft), k64(d_dtok), vocab,     tbits,       (uint64_t)greedy,
+                                 k64(d_u),   k64(d_ures), k64(d_accepted), k64(d_tokens)};
+    return run_graphed(ctx, key, [&]() {
+        if (int32_t rc = enqueue_stack(ctx, stack, d_h, m, nullptr, nullptr, nullptr)) return rc;
+        return enqueue_accept(ctx, d_target, d_draft, d_dtok, k, vocab, temperature, greedy, d_u,
+                              d_ures, d_accepted, d_tokens);
+    });
+}
+
+// ===========================================================================
+// profiling
+// ===========================================================================
+extern "C" int32_t tqf_hip_profile_enable(tqf_hip_ctx *ctx, int32_t enable) {
+    TQF_ENTER(ctx);
+    resolve_profile(ctx);
+    ctx->profiling = enable != 0;
+    for (int i = 0; i < TQF_HIP_KERNEL_KINDS; ++i) {
+        ctx->prof_launches[i] = 0;
+        ctx->prof_ms[i] = 0.0;
+        ctx->prof_bytes[i] = 0.0;
+    }
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_profile_read(tqf_hip_ctx *ctx, int32_t kind, uint64_t *launches,
+                                        double *total_ms, double *algorithmic_bytes) {
+    TQF_ENTER(ctx);
+    if (kind < 0 || kind >= TQF_HIP_KERNEL_KINDS) return fail(ctx, TQF_HIP_ERR_INVALID, "unknown kernel kind");
+    resolve_profile(ctx);
+    if (launches) *launches = ctx->prof_launches[kind];
+    if (total_ms) *total_ms = ctx->prof_ms[kind];
+    if (algorithmic_bytes) *algorithmic_bytes = ctx->prof_bytes[kind];
+    return TQF_HIP_OK;
+}

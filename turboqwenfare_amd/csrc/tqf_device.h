@@ -1,0 +1,141 @@
+// tqf_device.h -- device helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tqf_internal.h"
+
+namespace tqf {
+
+__device__ __forceinline__ float f16_to_f32(uint32_t h16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(h16 & 0xFFFFu));
+}
+
+// Scale of a 32-element activation block: x = X * 2^e with |X| <= 2^22.
+// Returns 2^e; 0 for a block whose max |x| is below 2^-100 (its products are
+// below fp32 resolution of any finite output); NaN if the block holds a
+// non-finite value, so the non-finite input propagates to the outputs.
+__device__ __forceinline__ float block_scale(float amax, bool bad, int &e) {
+    e = 0;
+    if (bad) return __int_as_float(0x7FC00000);
+    if (!(amax >= 0x1p-100f)) return 0.0f;
+    e = (int)((__float_as_uint(amax) >> 23) & 0xFFu) - 127 - 21;
+    return __uint_as_float((uint32_t)(e + 127) << 23);
+}
+
+// Balanced base-256 digits of X = rint(x * 2^-e): X = d0 + 256 d1 + 65536 d2.
+__device__ __forceinline__ void split_digits(float x, int e, float scale, int &d0, int &d1,
+                                             int &d2) {
+    int X = 0;
+    if (scale > 0.0f) X = (int)__builtin_rintf(__builtin_ldexpf(x, -e));
+    d0 = (int)(int8_t)(X & 0xFF);
+    int X1 = (X - d0) >> 8;
+    d1 = (int)(int8_t)(X1 & 0xFF);
+    d2 = (X1 - d1) >> 8;
+}
+
+// Writes one xprep record for a 32-element block held by a group of
+// 32/EPL lanes (EPL consecutive elements per lane, group-aligned lanes).
+template <int EPL>
+__device__ __forceinline__ void prep_block(const float (&v)[EPL], int lane_in_group,
+                                           uint32_t *__restrict__ rec) {
+    constexpr int LPB = 32 / EPL;
+    float amax = 0.0f;
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+        float a = fabsf(v[i]);
+        bool b = !(a <= 3.402823466e38f);
+        bad |= b;
+        amax = fmaxf(amax, b ? 0.0f : a);
+    }
+    int badi = bad ? 1 : 0;
+#pragma unroll
+    for (int off = 1; off < LPB; off <<= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off));
+        badi |= __shfl_xor(badi, off);
+    }
+    int e;
+    float scale = block_scale(amax, badi != 0, e);
+    int s0 = 0, s1 = 0, s2 = 0;
+    uint32_t pk0[(EPL + 3) / 4] = {}, pk1[(EPL + 3) / 4] = {}, pk2[(EPL + 3) / 4] = {};
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+        int d0, d1, d2;
+        split_digits(v[i], e, scale, d0, d1, d2);
+        s0 += d0;
+        s1 += d1;
+        s2 += d2;
+        pk0[i / 4] |= ((uint32_t)d0 & 0xFFu) << (8 * (i % 4));
+        pk1[i / 4] |= ((uint32_t)d1 & 0xFFu) << (8 * (i % 4));
+        pk2[i / 4] |= ((uint32_t)d2 & 0xFFu) << (8 * (i % 4));
+    }
+#pragma unroll
+    for (int off = 1; off < LPB; off <<= 1) {
+        s0 += __shfl_xor(s0, off);
+        s1 += __shfl_xor(s1, off);
+        s2 += __shfl_xor(s2, off);
+    }
+    if constexpr (EPL >= 4) {
+#pragma unroll
+        for (int q = 0; q < EPL / 4; ++q) {
+            int dw = lane_in_group * (EPL / 4) + q;
+            rec[dw] = pk0[q];
+            rec[8 + dw] = pk1[q];
+            rec[16 + dw] = pk2[q];
+        }
+    } else {
+        uint8_t *b = reinterpret_cast<uint8_t *>(rec);
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+            int j = lane_in_group * EPL + i;
+            b[j] = (uint8_t)(pk0[0] >> (8 * i));
+            b[32 + j] = (uint8_t)(pk1[0] >> (8 * i));
+            b[64 + j] = (uint8_t)(pk2[0] >> (8 * i));
+        }
+    }
+    if (lane_in_group == 0) {
+        rec[24] = (uint32_t)(-8 * s0);
+        rec[25] = (uint32_t)(-8 * s1);
+        rec[26] = (uint32_t)(-8 * s2);
+        rec[27] = __float_as_uint(scale);
+        rec[28] = 0;
+        rec[29] = 0;
+        rec[30] = 0;
+        rec[31] = 0;
+    }
+}
+
+// sum_j (q_j - 8) * x_j of one Q4_0 block against one xprep record, in fp32.
+// `w` is the block's 16 nibble bytes.  The integer part is exact.
+__device__ __forceinline__ float q4_block_dot(const uint4 w, const uint32_t *__restrict__ xp) {
+    int a0 = (int)xp[24], a1 = (int)xp[25], a2 = (int)xp[26];
+    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = wv[i] & 0x0F0F0F0Fu;
+        const uint32_t hi = (wv[i] >> 4) & 0x0F0F0F0Fu;
+        a0 = __builtin_amdgcn_sdot4((int)lo, (int)xp[i], a0, false);
+        a0 = __builtin_amdgcn_sdot4((int)hi, (int)xp[4 + i], a0, false);
+        a1 = __builtin_amdgcn_sdot4((int)lo, (int)xp[8 + i], a1, false);
+        a1 = __builtin_amdgcn_sdot4((int)hi, (int)xp[12 + i], a1, false);
+        a2 = __builtin_amdgcn_sdot4((int)lo, (int)xp[16 + i], a2, false);
+        a2 = __builtin_amdgcn_sdot4((int)hi, (int)xp[20 + i], a2, false);
+    }
+    const int v = a0 + a1 * 256 + a2 * 65536;
+    return (float)v * __uint_as_float(xp[27]);
+}
+
+// Scale j (0..7) of a tile's per-lane scale vector.
+__device__ __forceinline__ float tile_scale(const uint4 s, int j) {
+    const uint32_t sv[4] = {s.x, s.y, s.z, s.w};
+    const uint32_t word = sv[j >> 1];
+    return f16_to_f32((j & 1) ? (word >> 16) : word);
+}
+
+__device__ __forceinline__ uint4 load_u4(const uint8_t *p) {
+    return *reinterpret_cast<const uint4 *>(p);
+}
+
+}  // namespace tqf

@@ -1,0 +1,215 @@
+// tqf_internal.h -- shared definitions of the gfx950 HIP backend (not ABI).
+//
+// Device layout of one Q4_0 matrix ("tile layout").  A GGML Q4_0 matrix is
+// rows x B blocks of 18 bytes (f16 scale d, 16 nibble bytes qs; element j of
+// a block is (qs[j] & 15) - 8, element j + 16 is (qs[j] >> 4) - 8;
+// format/quant/dequant.rs:110-123).  The backend stores it as
+//   row groups of 64 rows  x  chunks of 8 blocks (256 columns)
+// and each (group, chunk) tile is 9216 contiguous bytes:
+//   bytes [j*1024 + lane*16, +16)  qs of block j of row (group*64 + lane)
+//   bytes [8192 + lane*16, +16)    the 8 f16 scales of that row's blocks
+// so lane L of a 64-wide wavefront reads its row's 16 nibble bytes with one
+// 128-bit load and a wavefront reads 1 KiB contiguously.  Rows are padded to
+// 64 and blocks to 8 with zero scales (their products are exactly zero).  The
+// bytes are the GGML bytes moved, never re-encoded: the repack is lossless
+// and tqf_hip_weights_download() inverts it.
+//
+// Activation prep ("xprep").  A Q4_0 dot is evaluated with exact integer
+// arithmetic: each 32-element activation block is written as
+//   x_j = X_j * 2^e,  |X_j| <= 2^22,  e chosen per block from max |x_j|
+// and X_j is split into three signed base-256 digits D0 + 256 D1 + 65536 D2.
+// With q_j the nibbles, sum_j (q_j - 8) X_j is three v_dot4_i32_i8 chains
+// (nibbles 0..15 are non-negative int8 lanes) seeded with -8 * sum_j D_kj, and
+// the block contributes d * 2^e * (float)that.  The representation keeps 22
+// bits of every block relative to its largest element, so the only rounding
+// beyond the fp32 accumulation is 2^-23 of each block's max |x|.  One xprep
+// record per (token, block) is 32 dwords:
+//   dw[0..8)   digit 0 (byte j of dword i = element 4i + j)
+//   dw[8..16)  digit 1,  dw[16..24) digit 2
+//   dw[24..27) -8 * sum of digit k (int32),  dw[27] 2^e (float),  dw[28..32) 0
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/tqf_hip.h"
+
+namespace tqf {
+
+constexpr int kWave = 64;
+constexpr int kRowsPerGroup = 64;
+constexpr int kChunkBlocks = 8;
+constexpr int kChunkCols = kChunkBlocks * 32;  // 256
+constexpr int kTileNibbleBytes = kChunkBlocks * kRowsPerGroup * 16;  // 8192
+constexpr int kTileBytes = kTileNibbleBytes + kRowsPerGroup * 16;    // 9216
+constexpr int kXprepDwords = 32;
+constexpr int kTopK = TQF_HIP_TOP_K;
+constexpr int kMaxTokens = TQF_HIP_MAX_TOKENS;
+constexpr int kMaxExperts = 256;
+constexpr int kMaxSlots = kMaxTokens * kTopK + 1;  // union + shared expert
+// Algorithmic bytes of one GGML Q4_0 block.
+constexpr int kQ4Block = 18;
+
+struct MatrixDims {
+    uint32_t rows, cols;
+    uint32_t groups;  // ceil(rows / 64)
+    uint32_t chunks;  // ceil(cols / 256)
+};
+
+inline MatrixDims matrix_dims(uint32_t rows, uint32_t cols) {
+    MatrixDims d;
+    d.rows = rows;
+    d.cols = cols;
+    d.groups = (rows + kRowsPerGroup - 1) / kRowsPerGroup;
+    d.chunks = (cols + kChunkCols - 1) / kChunkCols;
+    return d;
+}
+inline size_t tile_bytes(const MatrixDims &d) {
+    return (size_t)d.groups * d.chunks * kTileBytes;
+}
+
+// Route plan written by the route kernel and read by the expert kernels.
+// Slot 0 is the shared expert (all tokens); slots 1.. are the distinct routed
+// experts in first-demand order (experts/mod.rs:268-275 BatchExpertPlan).
+struct Plan {
+    int32_t n_slots;
+    int32_t status;  // 0 or TQF_HIP_ERR_ROUTER
+    int32_t pad[2];
+    int32_t slot_expert[kMaxSlots];   // expert index; n_experts = shared
+    uint32_t slot_mask[kMaxSlots];    // bit t: token t uses this slot
+    float coef[kMaxSlots][kMaxTokens];  // combine coefficient per (slot, token)
+    uint16_t ids[kMaxTokens][kTopK];
+    float weights[kMaxTokens][kTopK];
+    float gate_logit[kMaxTokens];
+};
+
+// Device-side description of one MoE layer (passed by value to kernels).
+struct LayerDev {
+    const float *router;             // [n_experts x hidden]
+    const float *shared_input_gate;  // [hidden]
+    const uint8_t *const *mats;      // [(n_experts + 1) x 3]: gate, up, down
+    uint32_t n_experts, hidden, width;
+};
+
+// Per-context device scratch (allocated once, grown on demand).
+struct Scratch {
+    uint32_t *xprep = nullptr;   // [kMaxTokens x hidden/32 x 32]
+    uint32_t *hprep = nullptr;   // [kMaxSlots x kMaxTokens x width/32 x 32]
+    float *logits = nullptr;     // [kMaxTokens x (n_experts + 1)]
+    Plan *plan = nullptr;
+    float *partial = nullptr;    // [slot groups x kMaxTokens x hidden]
+    uint32_t *counters = nullptr;  // [64 + hidden/64] last-arriver counters
+    void *accept = nullptr;      // acceptance partials
+    size_t accept_bytes = 0;
+    uint32_t hidden = 0, width = 0, experts = 0;
+};
+
+struct ProfileSlot {
+    hipEvent_t start, stop;
+    int kind;
+    double fixed_bytes;     // algorithmic bytes independent of the route
+    double per_slot_bytes;  // algorithmic bytes per expert slot of the plan
+    int ring_index;         // pinned-host copy of plan->n_slots, or -1
+};
+
+// Weights arena: large slabs sub-allocated with a bump pointer, released when
+// their last allocation is freed (few large hipMallocs for an 18 GB model).
+struct Slab {
+    uint8_t *base;
+    size_t size, used, live;
+};
+
+}  // namespace tqf
+
+struct tqf_hip_weights {
+    tqf::MatrixDims dims;
+    uint8_t *tiles;              // device
+    size_t bytes;
+    const uint8_t **d_self;      // device: one-entry table {tiles}
+};
+
+struct tqf_hip_tensor {
+    float *data;  // device
+    size_t count;
+};
+
+struct tqf_hip_layer {
+    tqf::LayerDev dev;
+    const uint8_t **d_mats;  // device array owned by the layer
+};
+
+struct tqf_hip_stack {
+    std::vector<const tqf_hip_layer *> layers;
+    std::vector<const float *> norms;
+    uint32_t hidden, width, experts;
+};
+
+namespace tqf {
+struct GraphEntry;
+}
+
+struct tqf_hip_ctx {
+    int device;
+    hipStream_t stream;
+    std::string last_error;
+    tqf::Scratch scratch;
+    // profiling
+    bool profiling = false;
+    std::vector<tqf::ProfileSlot> prof_pending;
+    std::vector<hipEvent_t> event_pool;
+    uint64_t prof_launches[TQF_HIP_KERNEL_KINDS] = {};
+    double prof_ms[TQF_HIP_KERNEL_KINDS] = {};
+    double prof_bytes[TQF_HIP_KERNEL_KINDS] = {};
+    int32_t *prof_ring = nullptr;  // pinned host ring of n_slots copies
+    int prof_ring_next = 0;
+    bool capturing = false;
+    std::vector<tqf::GraphEntry *> graphs;
+    std::vector<tqf::Slab> slabs;
+    // device pointer table for batched GEMV (+ host shadow to skip re-copies)
+    const uint8_t **d_table = nullptr;
+    std::vector<const uint8_t *> table_shadow;
+    size_t table_cap = 0;
+    uint32_t *d_gemv_xprep = nullptr;
+    size_t gemv_xprep_bytes = 0;
+    // host staging for the synchronous host-pointer entry points
+    void *d_stage = nullptr;
+    size_t stage_bytes = 0;
+    // one-matrix / one-expert layer tables reused by the non-MoE entry points
+    const uint8_t **d_adhoc_mats = nullptr;
+    tqf::Plan *d_adhoc_plan = nullptr;
+};
+
+namespace tqf {
+
+// ---- launchers (defined in the .hip translation units) -------------------
+// All are asynchronous on ctx->stream and return a hipError_t.
+hipError_t launch_repack(hipStream_t s, const uint8_t *d_aos, const MatrixDims &d,
+                         uint8_t *tiles);
+hipError_t launch_synth_q4_0(hipStream_t s, const MatrixDims &d, uint32_t tensor_id,
+                             uint32_t seed, uint8_t *tiles);
+hipError_t launch_prep(hipStream_t s, const float *x, uint32_t m, uint32_t cols,
+                       uint32_t blocks_padded, uint32_t *xprep);
+hipError_t launch_gemv(hipStream_t s, const uint8_t *const *d_tiles, uint32_t count,
+                       const MatrixDims &d, const uint32_t *xprep, uint32_t m, float *y);
+// status_out (may be null) is set to TQF_HIP_ERR_ROUTER when routing fails and
+// left untouched otherwise (a sticky flag the caller zeroes).
+hipError_t launch_route(hipStream_t s, const LayerDev &L, const float *h, const float *norm,
+                        uint32_t m, Scratch &sc, uint16_t *ids_out, float *w_out,
+                        int32_t *status_out);
+hipError_t launch_gate_up(hipStream_t s, const LayerDev &L, uint32_t m, Scratch &sc,
+                          const Plan *plan, const uint32_t *xprep);
+hipError_t launch_down(hipStream_t s, const LayerDev &L, uint32_t m, Scratch &sc,
+                       const Plan *plan, const float *resid, float *out);
+size_t accept_scratch_bytes(uint32_t k, uint32_t vocab);
+hipError_t launch_accept(hipStream_t s, const float *target, const float *draft,
+                         const int32_t *dtok, uint32_t k, uint32_t vocab, float temperature,
+                         int32_t greedy, const float *u, const float *ures, int32_t *accepted,
+                         int32_t *tokens, void *scratch, hipEvent_t ev_start, hipEvent_t ev_stop);
+hipError_t launch_top4(hipStream_t s, const float *logits, uint32_t rows, uint32_t vocab,
+                       uint32_t *tokens4, float *logits4);
+
+}  // namespace tqf

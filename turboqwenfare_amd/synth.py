@@ -1,0 +1,78 @@
+"""Seeded synthetic workloads (host side), byte-identical to the device
+generator in ``csrc/tqf_synth.hip``.
+
+No reference counterpart: the reference benchmarks real checkpoints; the
+MI355X configurations are defined on synthetic data from a seeded Philox
+stream.  Philox4x32-10 follows Salmon, Moraes, Dror & Shaw, "Parallel random
+numbers: as easy as 1, 2, 3" (SC'11).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+_M32 = np.uint64(0xFFFFFFFF)
+PHILOX_M0 = 0xD2511F53
+PHILOX_M1 = 0xCD9E8D57
+PHILOX_W0 = 0x9E3779B9
+PHILOX_W1 = 0xBB67AE85
+UNIFORM_KEY1 = 0x243F6A88
+
+
+def philox4x32_10(ctr: np.ndarray, key: tuple[int, int]) -> np.ndarray:
+    """Philox4x32-10 of counters ``ctr`` [N, 4] (uint32) under ``key``."""
+    c = np.asarray(ctr, dtype=np.uint32).astype(np.uint64)
+    c0, c1, c2, c3 = c[:, 0], c[:, 1], c[:, 2], c[:, 3]
+    k0, k1 = int(key[0]) & 0xFFFFFFFF, int(key[1]) & 0xFFFFFFFF
+    for rnd in range(10):
+        if rnd:
+            k0 = (k0 + PHILOX_W0) & 0xFFFFFFFF
+            k1 = (k1 + PHILOX_W1) & 0xFFFFFFFF
+        p0 = np.uint64(PHILOX_M0) * c0
+        p1 = np.uint64(PHILOX_M1) * c2
+        n0 = (p1 >> np.uint64(32)) ^ c1 ^ np.uint64(k0)
+        n2 = (p0 >> np.uint64(32)) ^ c3 ^ np.uint64(k1)
+        c0, c1, c2, c3 = n0, p1 & _M32, n2, p0 & _M32
+    return np.stack([c0, c1, c2, c3], axis=1).astype(np.uint32)
+
+
+def q4_0_synthetic(rows: int, cols: int, tensor_id: int, seed: int) -> np.ndarray:
+    """GGML Q4_0 bytes [rows * cols/32 * 18] of (tensor_id, seed).
+
+    Block b (row-major): Philox(ctr=(b_lo, b_hi, 0, 0)) gives the 16 nibble
+    bytes (little-endian words); Philox(ctr=(b_lo, b_hi, 1, 0)) word 0 gives
+    u = (w >> 8) 2^-24 and the scale d = 0.005 + 0.015 u (binary32, no fused
+    multiply-add), stored as binary16 rounded to nearest even.
+    """
+    if cols % 32:
+        raise ValueError("cols must be a multiple of 32")
+    n = rows * (cols // 32)
+    idx = np.arange(n, dtype=np.uint64)
+    lo = (idx & _M32).astype(np.uint32)
+    hi = (idx >> np.uint64(32)).astype(np.uint32)
+    zeros = np.zeros(n, dtype=np.uint32)
+    q = philox4x32_10(np.stack([lo, hi, zeros, zeros], axis=1), (tensor_id, seed))
+    s = philox4x32_10(np.stack([lo, hi, np.ones(n, dtype=np.uint32), zeros], axis=1),
+                      (tensor_id, seed))
+    u = (s[:, 0] >> np.uint32(8)).astype(np.float32) * np.float32(2.0 ** -24)
+    d = np.float32(0.005) + np.float32(0.015) * u
+    d16 = d.astype(np.float16).view(np.uint16)
+    out = np.empty((n, 18), dtype=np.uint8)
+    out[:, 0:2] = d16.view(np.uint8).reshape(n, 2)
+    out[:, 2:18] = q.view(np.uint8).reshape(n, 16)
+    return out.reshape(-1)
+
+
+def philox_uniforms(seed: int, stream: int, count: int) -> np.ndarray:
+    """``count`` uniforms in [0, 1) with 24 bits: (word0 >> 8) 2^-24 of
+    Philox(ctr=(i, stream, 0, 0), key=(seed, 0x243F6A88))."""
+    i = np.arange(count, dtype=np.uint32)
+    ctr = np.stack([i, np.full(count, stream, np.uint32), np.zeros(count, np.uint32),
+                    np.zeros(count, np.uint32)], axis=1)
+    w = philox4x32_10(ctr, (seed, UNIFORM_KEY1))[:, 0]
+    return (w >> np.uint32(8)).astype(np.float32) * np.float32(2.0 ** -24)
+
+
+def normal(shape, seed: int, std: float = 1.0) -> np.ndarray:
+    """Seeded N(0, std^2) float32 activations / router weights (host only)."""
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
