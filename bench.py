@@ -1,0 +1,265 @@
+#!/usr/bin/env python3
+"""MTP k=3 verify-step benchmark on one MI355X.
+
+One step = the full-depth verify pass over the k+1 = 4 verify rows: 40
+stacked MoE FFN layers h <- h + MoE_l(rmsnorm_l(h)) (model/qwen36/runtime.rs:
+777-802), each with its own seeded Q4_0 experts resident in HBM (256 routed +
+1 shared per layer, 18.2 GB), router softmax top-8 + gated shared expert +
+SwiGLU experts, followed by acceptance sampling over fp32 logits [4, 151936]
+at T = 0.7 with Philox uniforms.  Inputs are resident in HBM before timing.
+
+Prints ONE JSON line (progress goes to stderr).  `value` is verify steps/s.
+The roofline object is for the dominant kernel (union-expert gate/up GEMV)
+timed with HIP events on the library's stream; `cpu_baseline` is the
+reference's scalar path (the C restatement in oracle/) timed on this host's
+cores on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+E, H, F, V, K = 256, 2048, 512, 151936, 3
+M = K + 1
+TEMPERATURE = 0.7
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build_model(be, n_layers: int, seed: int):
+    """Seeded synthetic 40-layer weight set generated directly in HBM."""
+    from turboqwenfare_amd import synth
+
+    layers, norms, host_f32 = [], [], []
+    for l in range(n_layers):
+        base = 1_000_000 * (l + 1)
+        mats = [(be.synth_q4_0(F, H, base + 3 * e, seed), be.synth_q4_0(F, H, base + 3 * e + 1, seed),
+                 be.synth_q4_0(H, F, base + 3 * e + 2, seed)) for e in range(E + 1)]
+        router = synth.normal((E, H), seed=base + 7, std=H ** -0.5)
+        gate = synth.normal((H,), seed=base + 8, std=H ** -0.5)
+        norm = (1.0 + 0.05 * synth.normal((H,), seed=base + 9)).astype(np.float32)
+        layers.append(be.prepare_moe_layer(be.upload_f32(router), be.upload_f32(gate), mats[E],
+                                           [m[0] for m in mats[:E]], [m[1] for m in mats[:E]],
+                                           [m[2] for m in mats[:E]]))
+        norms.append(be.upload_f32(norm))
+        host_f32.append((router, gate, norm) if l < 4 else None)
+        if (l + 1) % 10 == 0:
+            log(f"bench: {l + 1}/{n_layers} layers resident")
+    return layers, norms, host_f32
+
+
+def verify_inputs(seed: int):
+    from turboqwenfare_amd import synth
+
+    rng = np.random.default_rng(seed)
+    target = (rng.standard_normal((M, V)) * 3.0).astype(np.float32)
+    draft = (rng.standard_normal((K, V)) * 3.0).astype(np.float32)
+    dtok = np.argmax(draft, axis=1).astype(np.int32)
+    u = synth.philox_uniforms(seed, 0, K)
+    ur = synth.philox_uniforms(seed, 1, K + 1)
+    h0 = synth.normal((M, H), seed=seed + 1)
+    return target, draft, dtok, u, ur, h0
+
+
+def cpu_baseline(be, layers, host_f32, inputs, budget_s: float):
+    """The reference's portable scalar path (C restatement, -O3
+    -ffp-contract=off) on this host: MoE layers at M = 4 plus the acceptance
+    at V = 151936, timed on a bounded sample of layers and scaled to 40."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import cpu_oracle as orc  # the baseline being timed (not the GPU path)
+
+    target, draft, dtok, u, ur, h0 = inputs
+    threads = int(os.environ.get("OMP_NUM_THREADS") or len(os.sched_getaffinity(0)))
+    n_sample = min(4, len(layers))
+    hosts, norm_host = [], []
+    for L, (router, gate, norm) in zip(layers[:n_sample], host_f32[:n_sample]):
+        mats = L.owned[2:]
+        sg, su, sd = mats[0:3]
+        rg, ru, rd = mats[3:3 + E], mats[3 + E:3 + 2 * E], mats[3 + 2 * E:3 + 3 * E]
+        hosts.append(orc.MoeLayerHost(
+            router, gate, *(be.download_q4_0(w) for w in (sg, su, sd)),
+            [be.download_q4_0(w) for w in rg], [be.download_q4_0(w) for w in ru],
+            [be.download_q4_0(w) for w in rd]))
+        norm_host.append(norm)
+
+    def run_layers(nthreads):
+        h = h0.copy()
+        for Lh, nw in zip(hosts, norm_host):
+            xn = np.stack([orc.qwen_rmsnorm(h[t], nw) for t in range(M)])
+            y, _, _ = Lh.forward_batch(xn, nthreads=nthreads)
+            h = h + y
+
+    def timed(fn, min_s):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= min_s or reps >= 50:
+                return el / reps
+
+    res = {}
+    t_acc = timed(lambda: orc.accept(target, draft, dtok, TEMPERATURE, False, u, ur), 0.5)
+    for nt in sorted({1, threads}):
+        per_sample = timed(lambda: run_layers(nt), budget_s / 2)
+        per_step = per_sample / n_sample * len(layers) + t_acc
+        res[nt] = 1.0 / per_step
+        log(f"bench: cpu {nt} thread(s): {per_sample / n_sample * 1e3:.1f} ms/layer, "
+            f"{per_step * 1e3:.1f} ms/step")
+    return res, threads, n_sample
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--layers", type=int, default=40)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--greedy", action="store_true", help="greedy instead of stochastic acceptance")
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--gemv-pool", type=int, default=2048,
+                    help="distinct 512x2048 matrices in the config-1 GEMV bandwidth pool")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE {world}); multi-GPU sharding is design-only.", file=sys.stderr)
+        sys.exit(2)
+
+    from turboqwenfare_amd import _lib, mtp
+    from turboqwenfare_amd.backend import HipBackend
+
+    be = HipBackend(0)
+    name, cus = be.device_info()
+    log(f"bench: device {name}, {cus} CUs")
+    t0 = time.perf_counter()
+    layers, norms, host_f32 = build_model(be, args.layers, args.seed)
+    log(f"bench: model resident in {time.perf_counter() - t0:.1f} s")
+
+    inputs = verify_inputs(args.seed)
+    target, draft, dtok, u, ur, h0 = inputs
+    d = {k: be.to_device(v) for k, v in dict(t=target, d=draft, dt=dtok, u=u, ur=ur, h0=h0,
+                                              h=h0).items()}
+    d_acc, d_tok = be.alloc(4), be.alloc(4 * M)
+    st = be.prepare_stack(layers, norms)
+
+    def step():
+        be.verify_step_device(st, d["h0"], d["h"], M, d["t"], None if args.greedy else d["d"],
+                              d["dt"], V, TEMPERATURE, args.greedy, d["u"], d["ur"], d_acc, d_tok)
+
+    for _ in range(args.warmup):
+        step()
+    be.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    be.synchronize()
+    elapsed = time.perf_counter() - t0
+    steps_per_s = args.steps / elapsed
+    log(f"bench: graph-replayed verify step {elapsed / args.steps * 1e3:.3f} ms")
+
+    # Kernel timing with HIP events (eager launches on the same stream).
+    be.profile_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    be.synchronize()
+    eager_ms = (time.perf_counter() - t0) / args.steps * 1e3
+    prof = {}
+    for kind, nm in ((_lib.KERNEL_ROUTE, "route"), (_lib.KERNEL_GATE_UP, "gate_up"),
+                     (_lib.KERNEL_DOWN, "down"), (_lib.KERNEL_ACCEPT, "accept")):
+        n, ms, by = be.profile_read(kind)
+        prof[nm] = dict(launches=n, avg_us=ms / max(n, 1) * 1e3,
+                        gbs=(by / (ms * 1e-3) / 1e9) if ms > 0 else 0.0, bytes_per_launch=by / max(n, 1))
+    be.profile_enable(False)
+    log("bench: kernel profile " + json.dumps(prof))
+
+    # Config-1 GEMV bandwidth: a rotating pool of distinct 512x2048 matrices
+    # (far beyond the 256 MB Infinity Cache) against one x, one launch.
+    from turboqwenfare_amd import synth
+
+    pool = [be.synth_q4_0(512, 2048, 900_000 + i, args.seed) for i in range(args.gemv_pool)]
+    dx = be.to_device(synth.normal((2048,), seed=args.seed))
+    dy = be.alloc(args.gemv_pool * 512 * 4)
+    be.q4_gemv_batched_device(pool, dx, dy)
+    be.profile_enable(True)
+    for _ in range(10):
+        be.q4_gemv_batched_device(pool, dx, dy)
+    n, ms, by = be.profile_read(_lib.KERNEL_GEMV)
+    be.profile_enable(False)
+    gemv = dict(matrices=args.gemv_pool, bytes_per_launch=by / n, avg_us=ms / n * 1e3,
+                gbs=by / (ms * 1e-3) / 1e9)
+    gemv["frac"] = gemv["gbs"] / HBM_PEAK_GBS
+    for w in pool:
+        be.free_weights(w)
+    log("bench: config-1 GEMV pool " + json.dumps(gemv))
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        res, threads, n_sample = cpu_baseline(be, layers, host_f32, inputs, args.cpu_budget)
+        cpu = dict(value=res[threads], unit="verify steps/s", cores=threads, kind="port",
+                   sample=f"{n_sample} of {args.layers} MoE layers at M=4 plus one acceptance at "
+                          f"V={V}, scaled to {args.layers} layers; oracle/tqf_oracle.c -O3 "
+                          f"-ffp-contract=off, OpenMP over output rows",
+                   single_thread_value=res[1])
+
+    traffic = None
+    tfile = ROOT / "profiles" / "gate_up_verify_traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+
+    gu = prof["gate_up"]
+    line = {
+        "metric": "MTP k=3 verify steps/sec + Q4 expert GEMV HBM GB/s (% of peak), 1 GPU",
+        "value": steps_per_s,
+        "unit": "verify steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": elapsed / args.steps * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_0 weights, fp32 activations, int8 dot4 + fp32 accumulate",
+        "data": "synthetic (seeded Philox Q4_0 experts, N(0,1) activations, N(0,9) logits)",
+        "config": {"workload": "config 4: full-depth MTP verify step, 40 MoE layers at M=4 "
+                               "(k=3) + stochastic acceptance" if not args.greedy else
+                               "config 4: full-depth MTP verify step, 40 MoE layers at M=4 "
+                               "(k=3) + greedy acceptance",
+                   "layers": args.layers, "hidden": H, "experts": E, "top_k": 8,
+                   "expert_width": F, "vocab": V, "temperature": TEMPERATURE,
+                   "resident_weight_gb": round(args.layers * (E + 1) * 3 * 589824 / 1e9, 2)},
+        "effective_tokens_per_s": {str(a): steps_per_s * mtp.expected_tokens_per_step(a, K)
+                                   for a in (0.6, 0.8)},
+        "roofline": {"bound": "hbm", "achieved": gu["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": gu["gbs"] / HBM_PEAK_GBS, "traffic": traffic,
+                     "kernel": "gate_up_kernel (union-expert gate/up GEMV + SwiGLU)",
+                     "avg_us": gu["avg_us"], "algorithmic_bytes_per_launch": gu["bytes_per_launch"]},
+        "kernels": prof,
+        "gemv_config1": gemv,
+        "eager_profiled_ms_per_step": eager_ms,
+        "cpu_baseline": cpu,
+    }
+    if cpu:
+        line["speedup_vs_cpu"] = steps_per_s / cpu["value"]
+    print(json.dumps(line), flush=True)
+    be.close()
+
+
+if __name__ == "__main__":
+    main()

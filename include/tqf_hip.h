@@ -163,12 +163,15 @@ int32_t tqf_hip_stack_prepare(tqf_hip_ctx *ctx, const tqf_hip_layer *const *laye
                               const tqf_hip_tensor *const *ffn_norms, uint32_t n_layers,
                               tqf_hip_stack **out);
 int32_t tqf_hip_stack_free(tqf_hip_ctx *ctx, tqf_hip_stack *stack);
-/* d_h [m x hidden] f32 is updated in place.  d_ids/d_w ([n_layers x m x 8],
- * may be NULL) receive every layer's route.  Captured once into a HIP graph
- * per argument set and replayed afterwards. */
-int32_t tqf_hip_stack_forward_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack, float *d_h,
-                                     uint32_t m, uint16_t *d_ids, float *d_w,
-                                     int32_t *d_status);
+/* d_h_in [m x hidden] f32 is the layer-0 input (the verify rows' hidden
+ * state); the result is written to d_h [m x hidden].  d_h_in may be NULL or
+ * equal d_h to update d_h in place.  d_ids/d_w ([n_layers x m x 8], may be
+ * NULL) receive every layer's route; *d_status (may be NULL, zeroed by the
+ * caller) is set to TQF_HIP_ERR_ROUTER if any layer's routing fails.
+ * Captured once into a HIP graph per argument set and replayed afterwards. */
+int32_t tqf_hip_stack_forward_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack,
+                                     const float *d_h_in, float *d_h, uint32_t m,
+                                     uint16_t *d_ids, float *d_w, int32_t *d_status);
 
 /* ---- acceptance: Sampler::select (sampling/mod.rs:68-74) and
  *      mtp::verify_pair (runtime/mtp.rs:98-104) generalised to k drafts ------
@@ -199,8 +202,9 @@ int32_t tqf_hip_top_logit_candidates(tqf_hip_ctx *ctx, const float *logits, uint
 /* ---- one MTP verify step: the stack over the k+1 verify rows, then the
  *      acceptance, as one stream-ordered (graph-replayed) unit.  The verify
  *      loop the reference leaves unwired (runtime/mtp.rs:1-20). ------------- */
-int32_t tqf_hip_verify_step_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack, float *d_h,
-                                   uint32_t m, const float *d_target, const float *d_draft,
+int32_t tqf_hip_verify_step_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack,
+                                   const float *d_h_in, float *d_h, uint32_t m,
+                                   const float *d_target, const float *d_draft,
                                    const int32_t *d_draft_tokens, uint32_t vocab,
                                    float temperature, int32_t greedy, const float *d_u,
                                    const float *d_u_resample, int32_t *d_accepted,

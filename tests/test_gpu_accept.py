@@ -1,0 +1,176 @@
+"""GPU acceptance sampling (a22) against the CPU definition: accepted length
+and token ids must be bit-exact for identical logits and uniforms."""
+import numpy as np
+import pytest
+
+import cpu_oracle as orc
+from turboqwenfare_amd import mtp, synth
+from turboqwenfare_amd._lib import ERR_INVALID, HipError
+
+pytestmark = pytest.mark.gpu
+
+V = 151936
+
+
+def case(seed: int, k: int = 3, vocab: int = V, noise: float = 1.0):
+    """Target = draft + noise: small noise -> mostly accepted, large -> rejected.
+    Draft tokens are drawn from the draft softmax at T = 0.7 (as a real
+    drafter would) with the reference's own inverse-CDF draw."""
+    rng = np.random.default_rng(seed)
+    draft = (rng.standard_normal((k, vocab)) * 3).astype(np.float32)
+    target = np.empty((k + 1, vocab), np.float32)
+    target[:k] = draft + (rng.standard_normal((k, vocab)) * noise).astype(np.float32)
+    target[k] = (rng.standard_normal(vocab) * 3).astype(np.float32)
+    ud = synth.philox_uniforms(seed, 7, k)
+    dtok = np.array([orc.softmax_draw(draft[i], 0.7, float(ud[i])) for i in range(k)], np.int32)
+    u = synth.philox_uniforms(seed, 0, k)
+    ur = synth.philox_uniforms(seed, 1, k + 1)
+    return target, draft, dtok, u, ur
+
+
+@pytest.mark.parametrize("noise", [0.05, 0.5, 3.0])
+def test_stochastic_bit_exact_over_seeds(backend, noise):
+    accepted = []
+    for seed in range(0, 64, 4):
+        target, draft, dtok, u, ur = case(seed, noise=noise)
+        got = backend.accept(target, draft, dtok, 0.7, False, u, ur)
+        want = orc.accept(target, draft, dtok, 0.7, False, u, ur)
+        assert got == want, f"seed {seed}"
+        accepted.append(got[0])
+    print(f"noise {noise}: accepted lengths {accepted}")
+
+
+def test_stochastic_exercises_every_accepted_length(backend):
+    seen = set()
+    for seed in range(64):
+        target, draft, dtok, u, ur = case(seed, vocab=4096, noise=0.6)
+        got = backend.accept(target, draft, dtok, 0.7, False, u, ur)
+        assert got == orc.accept(target, draft, dtok, 0.7, False, u, ur), f"seed {seed}"
+        seen.add(got[0])
+    assert seen == {0, 1, 2, 3}
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_greedy_bit_exact(backend, seed):
+    target, draft, dtok, _, _ = case(seed, noise=0.3)
+    # make some drafts match the target argmax
+    for i in range(3):
+        if (seed >> i) & 1:
+            dtok[i] = int(np.argmax(target[i]))
+    got = backend.accept(target, None, dtok, 0.0, True)
+    want = orc.accept(target, None, dtok, 0.0, True)
+    assert got == want
+
+
+def test_greedy_k1_is_verify_pair(backend):
+    rng = np.random.default_rng(1)
+    for seed in range(8):
+        target = (rng.standard_normal((2, 1000)) * 3).astype(np.float32)
+        a0 = int(np.argmax(target[0]))
+        for d in (a0, (a0 + 1) % 1000):
+            acc, toks = backend.accept(target, None, [d], 0.0, True)
+            out = mtp.verify_pair(a0, d)
+            assert out.accepted == (acc == 1)
+            assert out.emitted_tokens == len(toks)
+            assert toks[0] == a0
+
+
+@pytest.mark.parametrize("k", [0, 1, 2, 5, 7])
+def test_other_draft_lengths(backend, k):
+    for seed in range(4):
+        target, draft, dtok, u, ur = case(100 + seed, k=k, vocab=20000, noise=0.4)
+        for greedy in (False, True):
+            got = backend.accept(target, draft, dtok, 0.7, greedy, u, ur)
+            assert got == orc.accept(target, draft, dtok, 0.7, greedy, u, ur)
+
+
+def test_identical_distributions_always_accept(backend):
+    rng = np.random.default_rng(3)
+    draft = (rng.standard_normal((3, 5000)) * 3).astype(np.float32)
+    target = np.concatenate([draft, draft[:1]])
+    dtok = [17, 99, 4000]
+    u = np.array([0.999999, 0.5, 0.0], np.float32)
+    ur = synth.philox_uniforms(3, 1, 4)
+    got = backend.accept(target, draft, dtok, 0.9, False, u, ur)
+    assert got[0] == 3
+    assert got == orc.accept(target, draft, dtok, 0.9, False, u, ur)
+
+
+def test_zero_target_probability_always_rejects(backend):
+    draft = np.zeros((1, 64), np.float32)
+    target = np.zeros((2, 64), np.float32)
+    target[0, 5] = -np.inf  # p(d) = 0 < q(d)
+    got = backend.accept(target, draft, [5], 0.7, False, np.array([0.0], np.float32),
+                         np.array([0.3, 0.3], np.float32))
+    assert got[0] == 0 and got[1][0] != 5
+    assert got == orc.accept(target, draft, [5], 0.7, False, np.array([0.0], np.float32),
+                             np.array([0.3, 0.3], np.float32))
+
+
+def test_one_hot_target_accepts(backend):
+    rng = np.random.default_rng(4)
+    draft = (rng.standard_normal((2, 3000)) * 3).astype(np.float32)
+    target = np.full((3, 3000), -1e4, np.float32)
+    target[0, 42] = 10.0
+    target[1, 7] = 10.0
+    target[2, 2999] = 10.0
+    u = np.array([0.99, 0.99], np.float32)
+    ur = np.array([0.5, 0.5, 0.5], np.float32)
+    got = backend.accept(target, draft, [42, 7], 0.7, False, u, ur)
+    assert got == (2, [42, 7, 2999])
+    assert got == orc.accept(target, draft, [42, 7], 0.7, False, u, ur)
+
+
+def test_nan_and_inf_logits(backend):
+    rng = np.random.default_rng(5)
+    target = (rng.standard_normal((4, 9000)) * 3).astype(np.float32)
+    draft = (rng.standard_normal((3, 9000)) * 3).astype(np.float32)
+    target[0, ::7] = np.nan
+    draft[1, ::5] = np.nan
+    target[2, 100] = np.inf
+    draft[2, :] = -np.inf
+    target[3, :] = np.nan
+    dtok = [int(np.nanargmax(target[0])), 3, 100]
+    u = np.array([0.2, 0.4, 0.6], np.float32)
+    ur = np.array([0.1, 0.9, 0.5, 0.7], np.float32)
+    for greedy in (False, True):
+        got = backend.accept(target, draft, dtok, 0.7, greedy, u, ur)
+        assert got == orc.accept(target, draft, dtok, 0.7, greedy, u, ur)
+
+
+def test_ties_and_tiny_vocab(backend):
+    for vocab in (1, 2, 3, 4097):
+        target = np.zeros((3, vocab), np.float32)
+        draft = np.zeros((2, vocab), np.float32)
+        dtok = [0, vocab - 1]
+        u = np.array([0.0, 0.75], np.float32)
+        ur = np.array([0.999, 0.0, 0.5], np.float32)
+        for greedy in (False, True):
+            got = backend.accept(target, draft, dtok, 0.7, greedy, u, ur)
+            assert got == orc.accept(target, draft, dtok, 0.7, greedy, u, ur), vocab
+
+
+def test_rejects_invalid_arguments(backend):
+    t = np.zeros((2, 10), np.float32)
+    with pytest.raises(HipError) as e:
+        backend.accept(t, t[:1], [10], 0.7, False, np.zeros(1, np.float32), np.zeros(2, np.float32))
+    assert e.value.status == ERR_INVALID
+    with pytest.raises(HipError):
+        backend.accept(t, t[:1], [1], 0.7, False, np.ones(1, np.float32), np.zeros(2, np.float32))
+    with pytest.raises(HipError):
+        backend.accept(t, t[:1], [1], 0.0, False, np.zeros(1, np.float32), np.zeros(2, np.float32))
+
+
+def test_device_entry_point_matches_host(backend):
+    target, draft, dtok, u, ur = case(9)
+    bufs = [backend.to_device(a) for a in (target, draft, dtok, u, ur)]
+    acc = backend.alloc(4)
+    toks = backend.alloc(16)
+    for rep in range(2):
+        backend.accept_device(bufs[0], bufs[1], bufs[2], 3, V, 0.7, False, bufs[3], bufs[4], acc,
+                              toks)
+        a = int(backend.read(acc, np.int32, (1,))[0])
+        tk = [int(v) for v in backend.read(toks, np.int32, (4,))[: a + 1]]
+        assert (a, tk) == orc.accept(target, draft, dtok, 0.7, False, u, ur)
+    for b in bufs + [acc, toks]:
+        backend.free(b)

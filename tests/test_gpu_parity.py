@@ -291,8 +291,8 @@ def test_verify_step_graph_replays_match_eager(backend, stack3):
     for rep in range(3):
         backend.write(dh, h0)
         backend.synchronize()
-        backend.verify_step_device(st, dh, 4, bufs["t"], bufs["d"], bufs["dt"], vocab, 0.7,
-                                   False, bufs["u"], bufs["ur"], acc, toks)
+        backend.verify_step_device(st, None, dh, 4, bufs["t"], bufs["d"], bufs["dt"], vocab,
+                                   0.7, False, bufs["u"], bufs["ur"], acc, toks)
         h = backend.read(dh, np.float32, (4, 2048))
         a = int(backend.read(acc, np.int32, (1,))[0])
         tk = backend.read(toks, np.int32, (k + 1,))

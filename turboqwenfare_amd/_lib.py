@@ -84,12 +84,12 @@ SIGNATURES = {
     "tqf_hip_moe_layer_device": (_i32, [_vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp]),
     "tqf_hip_stack_prepare": (_i32, [_vp, _vp, _vp, _u32, _pp]),
     "tqf_hip_stack_free": (_i32, [_vp, _vp]),
-    "tqf_hip_stack_forward_device": (_i32, [_vp, _vp, _vp, _u32, _vp, _vp, _vp]),
+    "tqf_hip_stack_forward_device": (_i32, [_vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp]),
     "tqf_hip_accept": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _f32, _i32, _vp, _vp, _vp, _vp]),
     "tqf_hip_accept_device": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _f32, _i32, _vp, _vp, _vp, _vp]),
     "tqf_hip_top_logit_candidates": (_i32, [_vp, _vp, _u32, _u32, _vp, _vp]),
     "tqf_hip_verify_step_device": (
-        _i32, [_vp, _vp, _vp, _u32, _vp, _vp, _vp, _u32, _f32, _i32, _vp, _vp, _vp, _vp]),
+        _i32, [_vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _u32, _f32, _i32, _vp, _vp, _vp, _vp]),
     "tqf_hip_profile_enable": (_i32, [_vp, _i32]),
     "tqf_hip_profile_read": (_i32, [_vp, _i32, C.POINTER(_u64), C.POINTER(C.c_double),
                                     C.POINTER(C.c_double)]),

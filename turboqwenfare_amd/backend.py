@@ -268,18 +268,22 @@ class HipBackend:
 
     def stack_forward_device(self, st: Stack, d_h: DeviceBuffer, m: int,
                              d_ids: DeviceBuffer | None = None, d_w: DeviceBuffer | None = None,
-                             d_status: DeviceBuffer | None = None) -> None:
+                             d_status: DeviceBuffer | None = None,
+                             d_h_in: DeviceBuffer | None = None) -> None:
+        """h <- stack(h_in) (in place when d_h_in is None)."""
         self._check(self.lib.tqf_hip_stack_forward_device(
-            self.ctx, st.handle, d_h.ptr, m, d_ids.ptr if d_ids else None,
-            d_w.ptr if d_w else None, d_status.ptr if d_status else None))
+            self.ctx, st.handle, d_h_in.ptr if d_h_in else None, d_h.ptr, m,
+            d_ids.ptr if d_ids else None, d_w.ptr if d_w else None,
+            d_status.ptr if d_status else None))
 
-    def verify_step_device(self, st: Stack, d_h: DeviceBuffer, m: int, d_target: DeviceBuffer,
-                           d_draft: DeviceBuffer | None, d_dtok: DeviceBuffer, vocab: int,
-                           temperature: float, greedy: bool, d_u: DeviceBuffer | None,
-                           d_ures: DeviceBuffer | None, d_accepted: DeviceBuffer,
-                           d_tokens: DeviceBuffer) -> None:
+    def verify_step_device(self, st: Stack, d_h_in: DeviceBuffer | None, d_h: DeviceBuffer,
+                           m: int, d_target: DeviceBuffer, d_draft: DeviceBuffer | None,
+                           d_dtok: DeviceBuffer, vocab: int, temperature: float, greedy: bool,
+                           d_u: DeviceBuffer | None, d_ures: DeviceBuffer | None,
+                           d_accepted: DeviceBuffer, d_tokens: DeviceBuffer) -> None:
         self._check(self.lib.tqf_hip_verify_step_device(
-            self.ctx, st.handle, d_h.ptr, m, d_target.ptr, d_draft.ptr if d_draft else None,
+            self.ctx, st.handle, d_h_in.ptr if d_h_in else None, d_h.ptr, m, d_target.ptr,
+            d_draft.ptr if d_draft else None,
             d_dtok.ptr, vocab, temperature, 1 if greedy else 0, d_u.ptr if d_u else None,
             d_ures.ptr if d_ures else None, d_accepted.ptr, d_tokens.ptr))
 

@@ -19,15 +19,19 @@
 //   i* = k:  inverse CDF of E_x of target k with u_resample[k]
 //   inverse CDF: t = floor(W u) exactly; first x with prefix_sum(w)_x > t.
 //
-// Kernels (one pass over the logits each, chunks of 4096 per workgroup):
-//   stats    per (row, chunk): max over non-NaN and the greedy arg-max
-//   sums     per (row, chunk): S_fix partial (stochastic only)
-//   residual per chunk: decisions (recomputed redundantly per workgroup from
-//            the partials) and, if a draft was rejected, the residual mass
-//   final    one workgroup: emitted tokens, locating the sampled token with
-//            an exact prefix scan inside the selected chunk.
+// Kernels (chunks of 4096 logits per workgroup, coalesced 128-bit loads):
+//   stats    per (row, chunk): max over non-NaN and the greedy arg-max; in
+//            greedy mode the last workgroup emits the tokens.
+//   sums     per (row, chunk): S_fix partials; the last workgroup forms the
+//            row statistics and the decisions, and when every draft was
+//            accepted it samples the bonus token itself.
+//   residual per chunk, only after a rejection: residual mass; the last
+//            workgroup samples the replacement token.
+// Hand-offs inside a kernel use device-coherent stores and a counter; the
+// counters return to zero in the workgroup that finishes the kernel.
 #include <hip/hip_runtime.h>
 
+#include "tqf_device.h"
 #include "tqf_internal.h"
 
 #pragma clang fp contract(off)
@@ -44,6 +48,7 @@ struct AccLayout {
     size_t off_max, off_av, off_ai, off_sum, off_w, off_misc, total;
 };
 
+// misc: [0] i*, [1] counter (sums), [2] counter (residual), [3] counter (stats)
 __host__ __device__ inline AccLayout acc_layout(uint32_t k, uint32_t vocab) {
     AccLayout L;
     L.rows = 2 * k + 1;
@@ -153,14 +158,70 @@ __device__ __forceinline__ uint64_t shfl_up_u64(uint64_t v, int off) {
     const uint32_t hi = __shfl_up((uint32_t)(v >> 32), off);
     return ((uint64_t)hi << 32) | lo;
 }
+__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
+    const uint32_t lo = __shfl((uint32_t)v, src);
+    const uint32_t hi = __shfl((uint32_t)(v >> 32), src);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+    for (int off = 32; off >= 1; off >>= 1) v += shfl_xor_u64(v, off);
+    return v;
+}
+// Inclusive prefix sum over the wavefront (exact integers).
+__device__ __forceinline__ uint64_t wave_scan_u64(uint64_t v, int lane) {
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint64_t o = shfl_up_u64(v, off);
+        if (lane >= off) v += o;
+    }
+    return v;
+}
 
 __device__ uint64_t block_sum_u64(uint64_t v, uint64_t *lds /*[4]*/) {
-    for (int off = 32; off >= 1; off >>= 1) v += shfl_xor_u64(v, off);
+    v = wave_sum_u64(v);
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     __syncthreads();
     if (lane == 0) lds[wave] = v;
     __syncthreads();
     return (lds[0] + lds[1]) + (lds[2] + lds[3]);
+}
+
+__device__ __forceinline__ void store_coherent_u64(uint64_t *p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t load_coherent_u64(const uint64_t *p) {
+    return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_coherent_u32(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t load_coherent_u32(const uint32_t *p) {
+    return __hip_atomic_load(const_cast<uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_coherent_f32(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent_f32(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// Thread 0 arrives on `ctr` after every thread's coherent stores completed;
+// returns (in every thread) whether this workgroup arrived last, and then
+// resets the counter for the next launch.
+__device__ bool arrive_last(uint32_t *ctr, uint32_t expected, int *s_flag) {
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = prev == expected - 1;
+        if (last) store_coherent_u32(ctr, 0u);
+        *s_flag = last ? 1 : 0;
+    }
+    __syncthreads();
+    return *s_flag != 0;
 }
 
 struct AccArgs {
@@ -177,281 +238,162 @@ struct AccArgs {
     uint8_t *scratch;
 };
 
+struct Acc {
+    AccLayout L;
+    float *pmax, *pav;
+    uint32_t *pai;
+    uint64_t *psum, *pw;
+    int32_t *misc;
+    __device__ explicit Acc(const AccArgs &a) : L(acc_layout(a.k, a.vocab)) {
+        pmax = reinterpret_cast<float *>(a.scratch + L.off_max);
+        pav = reinterpret_cast<float *>(a.scratch + L.off_av);
+        pai = reinterpret_cast<uint32_t *>(a.scratch + L.off_ai);
+        psum = reinterpret_cast<uint64_t *>(a.scratch + L.off_sum);
+        pw = reinterpret_cast<uint64_t *>(a.scratch + L.off_w);
+        misc = reinterpret_cast<int32_t *>(a.scratch + L.off_misc);
+    }
+};
+
 __device__ __forceinline__ const float *acc_row(const AccArgs &a, uint32_t r) {
     return r <= a.k ? a.target + (size_t)r * a.vocab : a.draft + (size_t)(r - a.k - 1) * a.vocab;
 }
 
-// ---- kernel 1: per-chunk max and greedy arg-max ---------------------------
-__global__ __launch_bounds__(kAccThreads) void acc_stats_kernel(AccArgs a) {
-    const AccLayout L = acc_layout(a.k, a.vocab);
-    const uint32_t c = blockIdx.x, r = blockIdx.y;
-    if (a.greedy && r > a.k) return;
-    const float *row = acc_row(a, r);
-    float mx = -__builtin_inff();
-    float bv = -__builtin_inff();
-    uint32_t bi = kNone;
-    const uint32_t base = c * kAccChunk + threadIdx.x * kAccPerThread;
-    for (int i = 0; i < kAccPerThread; ++i) {
-        const uint32_t x = base + i;
-        if (x >= a.vocab) break;
-        const float l = row[x];
-        if (l > mx) mx = l;
-        if (l > bv) {
-            bv = l;
-            bi = x;
+// The 16 logits of thread `tid` in chunk c: element i of the thread is
+// x = c*4096 + (i/4)*1024 + tid*4 + i%4, read as four float4 loads when the
+// row allows it (coalesced 1 KiB per wavefront).
+__device__ __forceinline__ void load_chunk(const float *row, uint32_t vocab, uint32_t c, int tid,
+                                           float (&v)[kAccPerThread], uint32_t (&x)[kAccPerThread]) {
+    const uint32_t base = c * kAccChunk;
+    const bool vec = (vocab % 4 == 0) && ((reinterpret_cast<uintptr_t>(row) & 15) == 0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t x0 = base + q * 1024 + tid * 4;
+        if (vec && x0 + 3 < vocab) {
+            const float4 f = *reinterpret_cast<const float4 *>(row + x0);
+            v[q * 4 + 0] = f.x;
+            v[q * 4 + 1] = f.y;
+            v[q * 4 + 2] = f.z;
+            v[q * 4 + 3] = f.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[q * 4 + j] = (x0 + j < vocab) ? row[x0 + j] : __int_as_float(0x7FC00000);
         }
-    }
-    __shared__ float s_mx[4], s_bv[4];
-    __shared__ uint32_t s_bi[4];
-    for (int off = 32; off >= 1; off >>= 1) {
-        mx = fmaxf(mx, __shfl_xor(mx, off));
-        const float ov = __shfl_xor(bv, off);
-        const uint32_t oi = __shfl_xor(bi, off);
-        if (arg_better(ov, oi, bv, bi)) {
-            bv = ov;
-            bi = oi;
-        }
-    }
-    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-    if (lane == 0) {
-        s_mx[wave] = mx;
-        s_bv[wave] = bv;
-        s_bi[wave] = bi;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; ++w) {
-            mx = fmaxf(mx, s_mx[w]);
-            if (arg_better(s_bv[w], s_bi[w], bv, bi)) {
-                bv = s_bv[w];
-                bi = s_bi[w];
-            }
-        }
-        const size_t o = (size_t)r * L.nch + c;
-        reinterpret_cast<float *>(a.scratch + L.off_max)[o] = mx;
-        reinterpret_cast<float *>(a.scratch + L.off_av)[o] = bv;
-        reinterpret_cast<uint32_t *>(a.scratch + L.off_ai)[o] = bi;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[q * 4 + j] = x0 + j;
     }
 }
 
-__device__ __forceinline__ float row_max(const AccArgs &a, const AccLayout &L, uint32_t r) {
-    const float *pm = reinterpret_cast<const float *>(a.scratch + L.off_max) + (size_t)r * L.nch;
-    float M = -__builtin_inff();
-    for (uint32_t c = 0; c < L.nch; ++c) M = fmaxf(M, pm[c]);
-    return M;
-}
-
-__device__ __forceinline__ uint64_t row_sfix(const AccArgs &a, const AccLayout &L, uint32_t r) {
-    const uint64_t *ps =
-        reinterpret_cast<const uint64_t *>(a.scratch + L.off_sum) + (size_t)r * L.nch;
-    uint64_t s = 0;
-    for (uint32_t c = 0; c < L.nch; ++c) s += ps[c];
-    return s;
-}
-
-__device__ __forceinline__ uint32_t row_argmax(const AccArgs &a, const AccLayout &L, uint32_t r) {
-    const float *pv = reinterpret_cast<const float *>(a.scratch + L.off_av) + (size_t)r * L.nch;
-    const uint32_t *pi =
-        reinterpret_cast<const uint32_t *>(a.scratch + L.off_ai) + (size_t)r * L.nch;
-    float bv = -__builtin_inff();
-    uint32_t bi = kNone;
-    for (uint32_t c = 0; c < L.nch; ++c)
-        if (arg_better(pv[c], pi[c], bv, bi)) {
-            bv = pv[c];
-            bi = pi[c];
-        }
-    return bi == kNone ? 0u : bi;
-}
-
-// ---- kernel 2: per-chunk S_fix partials -----------------------------------
-__global__ __launch_bounds__(kAccThreads) void acc_sums_kernel(AccArgs a) {
-    if (a.greedy) return;
-    const AccLayout L = acc_layout(a.k, a.vocab);
-    const uint32_t c = blockIdx.x, r = blockIdx.y;
-    __shared__ float s_M;
-    __shared__ uint64_t s_red[4];
-    if (threadIdx.x == 0) s_M = row_max(a, L, r);
-    __syncthreads();
-    const float M = s_M;
-    const float *row = acc_row(a, r);
-    uint64_t s = 0;
-    const uint32_t base = c * kAccChunk + threadIdx.x * kAccPerThread;
-    for (int i = 0; i < kAccPerThread; ++i) {
-        const uint32_t x = base + i;
-        if (x >= a.vocab) break;
-        s += fix_shift(row_e(row[x], M, a.T), 40);
-    }
-    s = block_sum_u64(s, s_red);
-    if (threadIdx.x == 0)
-        reinterpret_cast<uint64_t *>(a.scratch + L.off_sum)[(size_t)r * L.nch + c] = s;
-}
-
+// ---- row statistics from the per-chunk partials (one wavefront per row) ---
 struct RowStat {
     float M, S;
     uint64_t sfix;
 };
 
-__device__ RowStat row_stat(const AccArgs &a, const AccLayout &L, uint32_t r) {
+__device__ RowStat wave_row_stat(const Acc &A, uint32_t r, bool coherent_sum, int lane) {
+    float M = -__builtin_inff();
+    uint64_t s = 0;
+    for (uint32_t c = lane; c < A.L.nch; c += 64) {
+        const size_t o = (size_t)r * A.L.nch + c;
+        M = fmaxf(M, A.pmax[o]);
+        s += coherent_sum ? load_coherent_u64(&A.psum[o]) : A.psum[o];
+    }
     RowStat st;
-    st.M = row_max(a, L, r);
-    st.sfix = row_sfix(a, L, r);
+    st.M = group_reduce<64>(M, MaxOp());
+    st.sfix = wave_sum_u64(s);
     st.S = u64_to_f32_rn(st.sfix) * 0x1p-40f;
     return st;
 }
 
-// Decision sequence; returns i*.  Called by one thread.
-__device__ uint32_t decide(const AccArgs &a, const AccLayout &L, RowStat &sp_star,
-                           RowStat &sq_star) {
-    for (uint32_t i = 0; i < a.k; ++i) {
-        const RowStat sp = row_stat(a, L, i);
-        const RowStat sq = row_stat(a, L, a.k + 1 + i);
-        const int32_t dt = a.dtok[i];
-        if (dt < 0 || (uint32_t)dt >= a.vocab) {  // out of vocabulary: rejected
-            sp_star = sp;
-            sq_star = sq;
-            return i;
-        }
-        const uint32_t d = (uint32_t)dt;
-        const float p = prob(row_e(a.target[(size_t)i * a.vocab + d], sp.M, a.T), sp.S);
-        const float q = prob(row_e(a.draft[(size_t)i * a.vocab + d], sq.M, a.T), sq.S);
-        const bool acc = (q > 0.0f) ? (a.u[i] < p / q) : (p > 0.0f);
-        if (!acc) {
-            sp_star = sp;
-            sq_star = sq;
-            return i;
+__device__ uint32_t wave_row_argmax(const Acc &A, uint32_t r, bool coherent, int lane) {
+    float bv = -__builtin_inff();
+    uint32_t bi = kNone;
+    for (uint32_t c = lane; c < A.L.nch; c += 64) {
+        const size_t o = (size_t)r * A.L.nch + c;
+        const float v = coherent ? load_coherent_f32(&A.pav[o]) : A.pav[o];
+        const uint32_t i = coherent ? load_coherent_u32(&A.pai[o]) : A.pai[o];
+        if (arg_better(v, i, bv, bi)) {
+            bv = v;
+            bi = i;
         }
     }
-    return a.k;
+    // among lanes with the best value, the lowest index (kNone is largest)
+    const float best = group_reduce<64>(bv, MaxOp());
+    const int cand = (bv == best && bi != kNone) ? (int)bi : 0x7FFFFFFF;
+    const int win = group_reduce<64>(cand, MinOp());
+    return win == 0x7FFFFFFF ? 0u : (uint32_t)win;
 }
 
-__device__ __forceinline__ uint64_t residual_w(const AccArgs &a, uint32_t istar, uint32_t x,
-                                               const RowStat &sp, const RowStat &sq) {
-    const float p = prob(row_e(a.target[(size_t)istar * a.vocab + x], sp.M, a.T), sp.S);
-    const float q = prob(row_e(a.draft[(size_t)istar * a.vocab + x], sq.M, a.T), sq.S);
-    return fix_shift(ftz(fmaxf(0.0f, p - q)), 62);
-}
+// ---- weights of the sampled distribution -----------------------------------
+struct SampleRows {
+    const float *tr;  // target row i*
+    const float *dr;  // draft row i* (residual mode)
+    RowStat sp, sq;
+    bool resid;
+};
 
-// ---- kernel 3: decisions + residual mass per chunk ------------------------
-__global__ __launch_bounds__(kAccThreads) void acc_residual_kernel(AccArgs a) {
-    if (a.greedy) return;
-    const AccLayout L = acc_layout(a.k, a.vocab);
-    __shared__ uint32_t s_istar;
-    __shared__ RowStat s_sp, s_sq;
-    __shared__ uint64_t s_red[4];
-    if (threadIdx.x == 0) {
-        RowStat sp{}, sq{};
-        s_istar = decide(a, L, sp, sq);
-        s_sp = sp;
-        s_sq = sq;
-        if (blockIdx.x == 0) reinterpret_cast<int32_t *>(a.scratch + L.off_misc)[0] = (int32_t)s_istar;
+__device__ __forceinline__ uint64_t sample_w(const SampleRows &s, float l_t, float l_d, float T) {
+    if (s.resid) {
+        const float p = prob(row_e(l_t, s.sp.M, T), s.sp.S);
+        const float q = prob(row_e(l_d, s.sq.M, T), s.sq.S);
+        return fix_shift(ftz(fmaxf(0.0f, p - q)), 62);
     }
-    __syncthreads();
-    const uint32_t istar = s_istar;
-    if (istar >= a.k) return;
-    const RowStat sp = s_sp, sq = s_sq;
-    uint64_t s = 0;
-    const uint32_t base = blockIdx.x * kAccChunk + threadIdx.x * kAccPerThread;
-    for (int i = 0; i < kAccPerThread; ++i) {
-        const uint32_t x = base + i;
-        if (x >= a.vocab) break;
-        s += residual_w(a, istar, x, sp, sq);
-    }
-    s = block_sum_u64(s, s_red);
-    if (threadIdx.x == 0) reinterpret_cast<uint64_t *>(a.scratch + L.off_w)[blockIdx.x] = s;
+    return fix_shift(row_e(l_t, s.sp.M, T), 40);
 }
 
-// ---- kernel 4: emitted tokens ----------------------------------------------
-__global__ __launch_bounds__(kAccThreads) void acc_final_kernel(AccArgs a) {
-    const AccLayout L = acc_layout(a.k, a.vocab);
-    __shared__ int32_t s_token;
-    __shared__ uint32_t s_istar, s_chunk, s_mode;
-    __shared__ uint64_t s_t, s_base;
-    __shared__ RowStat s_sp, s_sq;
+// Inverse CDF over `parts` (per-chunk masses, total W > 0) with uniform u:
+// the whole workgroup finds the first x with prefix(w)_x > floor(W u).
+__device__ int32_t sample_token(const AccArgs &a, const Acc &A, const SampleRows &s,
+                                const uint64_t *parts, bool coherent, uint64_t W, float u) {
     __shared__ uint64_t s_scan[4];
-    const int tid = threadIdx.x;
-    if (a.greedy) {
-        if (tid == 0) {
-            uint32_t i = 0;
-            for (; i < a.k; ++i) {
-                const uint32_t am = row_argmax(a, L, i);
-                if ((int32_t)am != a.dtok[i]) break;
-                a.tokens[i] = a.dtok[i];
+    __shared__ uint32_t s_chunk;
+    __shared__ uint64_t s_base;
+    __shared__ int32_t s_token;
+    const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    const uint64_t t = scale_floor(W, u);
+    if (wave == 0) {
+        uint64_t carry = 0;
+        uint32_t found = kNone;
+        uint64_t before = 0;
+        for (uint32_t c0 = 0; c0 < A.L.nch && found == kNone; c0 += 64) {
+            const uint32_t c = c0 + lane;
+            const uint64_t v = c < A.L.nch ? (coherent ? load_coherent_u64(&parts[c]) : parts[c]) : 0;
+            const uint64_t incl = carry + wave_scan_u64(v, lane);
+            const uint64_t mask = __ballot(c < A.L.nch && incl > t);
+            if (mask) {
+                const int l = __builtin_ctzll(mask);
+                found = c0 + l;
+                before = shfl_u64(incl - v, l);
             }
-            a.tokens[i] = (int32_t)row_argmax(a, L, i);
-            for (uint32_t j = i + 1; j <= a.k; ++j) a.tokens[j] = -1;
-            *a.accepted = (int32_t)i;
+            carry = shfl_u64(incl, 63);
         }
-        return;
-    }
-    // mode 0: residual weights of row pair i*; 1: E of target i*; 2: arg-max
-    if (tid == 0) {
-        const uint32_t istar = (uint32_t)reinterpret_cast<const int32_t *>(a.scratch + L.off_misc)[0];
-        uint32_t mode = 1;
-        uint64_t W = 0;
-        const uint64_t *parts;
-        if (istar < a.k) {
-            parts = reinterpret_cast<const uint64_t *>(a.scratch + L.off_w);
-            for (uint32_t c = 0; c < L.nch; ++c) W += parts[c];
-            if (W > 0) mode = 0;
-        }
-        if (mode == 1) {
-            parts = reinterpret_cast<const uint64_t *>(a.scratch + L.off_sum) + (size_t)istar * L.nch;
-            W = 0;
-            for (uint32_t c = 0; c < L.nch; ++c) W += parts[c];
-            if (W == 0) mode = 2;
-        }
-        s_istar = istar;
-        s_mode = mode;
-        if (mode == 2) {
-            s_token = (int32_t)row_argmax(a, L, istar);
-        } else {
-            const uint64_t t = scale_floor(W, a.ures[istar]);
-            uint64_t cum = 0;
-            uint32_t c = 0;
-            for (; c < L.nch; ++c) {
-                if (cum + parts[c] > t) break;
-                cum += parts[c];
-            }
-            s_chunk = c;
-            s_base = cum;
-            s_t = t;
-            s_sp = row_stat(a, L, istar);
-            s_sq = (mode == 0) ? row_stat(a, L, a.k + 1 + istar) : s_sp;
+        if (lane == 0) {
+            s_chunk = found;
+            s_base = before;
             s_token = -1;
         }
     }
     __syncthreads();
-    const uint32_t istar = s_istar;
-    if (s_mode != 2) {
-        const uint32_t c = s_chunk;
-        const RowStat sp = s_sp, sq = s_sq;
-        const bool resid = (s_mode == 0);
+    const uint32_t c = s_chunk;
+    if (c != kNone) {
+        // exact scan of the chunk in element order: thread tid owns elements
+        // [c*4096 + tid*16, +16)
+        const uint32_t base = c * kAccChunk + tid * kAccPerThread;
         uint64_t w[kAccPerThread];
         uint64_t mine = 0;
-        const uint32_t base = c * kAccChunk + tid * kAccPerThread;
+#pragma unroll
         for (int i = 0; i < kAccPerThread; ++i) {
             const uint32_t x = base + i;
             uint64_t v = 0;
-            if (x < a.vocab) {
-                v = resid ? residual_w(a, istar, x, sp, sq)
-                          : fix_shift(row_e(a.target[(size_t)istar * a.vocab + x], sp.M, a.T), 40);
-            }
+            if (x < a.vocab) v = sample_w(s, s.tr[x], s.resid ? s.dr[x] : 0.0f, a.T);
             w[i] = v;
             mine += v;
         }
-        // exclusive scan of `mine` across the workgroup (exact integers)
-        const int wave = tid / 64, lane = tid % 64;
-        uint64_t incl = mine;
-        for (int off = 1; off < 64; off <<= 1) {
-            const uint64_t o = shfl_up_u64(incl, off);
-            if (lane >= off) incl += o;
-        }
+        const uint64_t incl = wave_scan_u64(mine, lane);
         if (lane == 63) s_scan[wave] = incl;
         __syncthreads();
         uint64_t before = 0;
         for (int wv = 0; wv < wave; ++wv) before += s_scan[wv];
         const uint64_t excl = s_base + before + (incl - mine);
-        const uint64_t t = s_t;
         if (excl <= t && t < excl + mine) {
             uint64_t cum = excl;
             for (int i = 0; i < kAccPerThread; ++i) {
@@ -462,14 +404,219 @@ __global__ __launch_bounds__(kAccThreads) void acc_final_kernel(AccArgs a) {
                 }
             }
         }
-        __syncthreads();
     }
+    __syncthreads();
+    return s_token;
+}
+
+__device__ void emit(const AccArgs &a, uint32_t istar, int32_t token) {
+    for (uint32_t j = threadIdx.x; j <= a.k; j += blockDim.x)
+        a.tokens[j] = j < istar ? a.dtok[j] : (j == istar ? token : -1);
+    if (threadIdx.x == 0) *a.accepted = (int32_t)istar;
+}
+
+// ---- kernel 1: per-chunk max and greedy arg-max ---------------------------
+__global__ __launch_bounds__(kAccThreads) void acc_stats_kernel(AccArgs a) {
+    const Acc A(a);
+    __shared__ float s_mx[4], s_bv[4];
+    __shared__ uint32_t s_bi[4];
+    __shared__ int s_last;
+    const uint32_t c = blockIdx.x, r = blockIdx.y;
+    if (a.greedy && r > a.k) return;
+    const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    float v[kAccPerThread];
+    uint32_t xs[kAccPerThread];
+    load_chunk(acc_row(a, r), a.vocab, c, tid, v, xs);
+    float mx = -__builtin_inff();
+    float bv = -__builtin_inff();
+    uint32_t bi = kNone;
+#pragma unroll
+    for (int i = 0; i < kAccPerThread; ++i) {
+        if (v[i] > mx) mx = v[i];
+        if (arg_better(v[i], xs[i], bv, bi)) {
+            bv = v[i];
+            bi = xs[i];
+        }
+    }
+    mx = group_reduce<64>(mx, MaxOp());
+    {
+        const float best = group_reduce<64>(bv, MaxOp());
+        const int cand = (bv == best && bi != kNone) ? (int)bi : 0x7FFFFFFF;
+        const int win = group_reduce<64>(cand, MinOp());
+        bv = best;
+        bi = win == 0x7FFFFFFF ? kNone : (uint32_t)win;
+    }
+    if (lane == 0) {
+        s_mx[wave] = mx;
+        s_bv[wave] = bv;
+        s_bi[wave] = bi;
+    }
+    __syncthreads();
     if (tid == 0) {
-        for (uint32_t j = 0; j < istar; ++j) a.tokens[j] = a.dtok[j];
-        a.tokens[istar] = s_token;
-        for (uint32_t j = istar + 1; j <= a.k; ++j) a.tokens[j] = -1;
-        *a.accepted = (int32_t)istar;
+        for (int w = 1; w < 4; ++w) {
+            mx = fmaxf(mx, s_mx[w]);
+            if (arg_better(s_bv[w], s_bi[w], bv, bi)) {
+                bv = s_bv[w];
+                bi = s_bi[w];
+            }
+        }
+        const size_t o = (size_t)r * A.L.nch + c;
+        store_coherent_f32(&A.pmax[o], mx);
+        store_coherent_f32(&A.pav[o], bv);
+        store_coherent_u32(&A.pai[o], bi);
     }
+    if (!a.greedy) return;
+    // greedy: the last workgroup decides (runtime/decode.rs:48-64 argmax per
+    // target row; accept while it equals the draft).
+    if (!arrive_last(reinterpret_cast<uint32_t *>(&A.misc[3]), (a.k + 1) * A.L.nch, &s_last)) return;
+    __shared__ uint32_t s_arg[kMaxTokens];
+    for (uint32_t rr = wave; rr <= a.k; rr += 4) {
+        const uint32_t am = wave_row_argmax(A, rr, true, lane);
+        if (lane == 0) s_arg[rr] = am;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t i = 0;
+        while (i < a.k && (int32_t)s_arg[i] == a.dtok[i]) ++i;
+        A.misc[0] = (int32_t)i;
+        s_last = (int)s_arg[i];
+    }
+    __syncthreads();
+    emit(a, (uint32_t)A.misc[0], s_last);
+}
+
+// ---- kernel 2: S_fix partials; the last workgroup decides -----------------
+__global__ __launch_bounds__(kAccThreads) void acc_sums_kernel(AccArgs a) {
+    if (a.greedy) return;
+    const Acc A(a);
+    const uint32_t c = blockIdx.x, r = blockIdx.y;
+    const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    __shared__ float s_M;
+    __shared__ uint64_t s_red[4];
+    __shared__ int s_last;
+    __shared__ RowStat s_st[2 * kMaxTokens];
+    __shared__ float s_lt[kMaxTokens], s_ld[kMaxTokens];
+    __shared__ uint32_t s_istar;
+    __shared__ int32_t s_tok;
+    if (wave == 0) {
+        float M = -__builtin_inff();
+        for (uint32_t cc = lane; cc < A.L.nch; cc += 64) M = fmaxf(M, A.pmax[(size_t)r * A.L.nch + cc]);
+        M = group_reduce<64>(M, MaxOp());
+        if (lane == 0) s_M = M;
+    }
+    float v[kAccPerThread];
+    uint32_t xs[kAccPerThread];
+    load_chunk(acc_row(a, r), a.vocab, c, tid, v, xs);
+    __syncthreads();
+    const float M = s_M;
+    uint64_t s = 0;
+#pragma unroll
+    for (int i = 0; i < kAccPerThread; ++i)
+        if (xs[i] < a.vocab) s += fix_shift(row_e(v[i], M, a.T), 40);
+    s = block_sum_u64(s, s_red);
+    if (tid == 0) store_coherent_u64(&A.psum[(size_t)r * A.L.nch + c], s);
+    if (!arrive_last(reinterpret_cast<uint32_t *>(&A.misc[1]), A.L.rows * A.L.nch, &s_last)) return;
+
+    // ---- last workgroup: row statistics and the decisions ------------------
+    for (uint32_t rr = wave; rr < A.L.rows; rr += 4) {
+        const RowStat st = wave_row_stat(A, rr, true, lane);
+        if (lane == 0) s_st[rr] = st;
+    }
+    if (tid < (int)a.k) {
+        const int32_t dt = a.dtok[tid];
+        const bool ok = dt >= 0 && (uint32_t)dt < a.vocab;
+        s_lt[tid] = ok ? a.target[(size_t)tid * a.vocab + dt] : 0.0f;
+        s_ld[tid] = ok ? a.draft[(size_t)tid * a.vocab + dt] : 0.0f;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t i = 0;
+        for (; i < a.k; ++i) {
+            const int32_t dt = a.dtok[i];
+            if (dt < 0 || (uint32_t)dt >= a.vocab) break;  // out of vocabulary: rejected
+            const RowStat sp = s_st[i], sq = s_st[a.k + 1 + i];
+            const float p = prob(row_e(s_lt[i], sp.M, a.T), sp.S);
+            const float q = prob(row_e(s_ld[i], sq.M, a.T), sq.S);
+            const bool acc = (q > 0.0f) ? (a.u[i] < p / q) : (p > 0.0f);
+            if (!acc) break;
+        }
+        s_istar = i;
+        A.misc[0] = (int32_t)i;
+    }
+    __syncthreads();
+    const uint32_t istar = s_istar;
+    if (istar < a.k) return;  // the residual kernel samples the replacement
+    // every draft accepted: the bonus token from target row k
+    SampleRows srow{a.target + (size_t)a.k * a.vocab, nullptr, s_st[a.k], s_st[a.k], false};
+    int32_t token;
+    if (srow.sp.sfix == 0) {
+        token = (int32_t)wave_row_argmax(A, a.k, false, lane);
+        if (tid == 0) s_tok = token;
+        __syncthreads();
+        token = s_tok;
+    } else {
+        token = sample_token(a, A, srow, A.psum + (size_t)a.k * A.L.nch, true, srow.sp.sfix,
+                             a.ures[a.k]);
+    }
+    emit(a, istar, token);
+}
+
+// ---- kernel 3: residual mass after a rejection; the last workgroup samples -
+__global__ __launch_bounds__(kAccThreads) void acc_residual_kernel(AccArgs a) {
+    if (a.greedy) return;
+    const Acc A(a);
+    const uint32_t istar = (uint32_t)A.misc[0];
+    if (istar >= a.k) return;
+    const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    __shared__ RowStat s_sp, s_sq;
+    __shared__ uint64_t s_red[4];
+    __shared__ int s_last;
+    __shared__ int32_t s_tok;
+    if (wave < 2) {
+        const RowStat st = wave_row_stat(A, wave == 0 ? istar : a.k + 1 + istar, false, lane);
+        if (lane == 0) {
+            if (wave == 0) s_sp = st;
+            else s_sq = st;
+        }
+    }
+    __syncthreads();
+    const SampleRows srow{a.target + (size_t)istar * a.vocab, a.draft + (size_t)istar * a.vocab,
+                          s_sp, s_sq, true};
+    float vt[kAccPerThread], vd[kAccPerThread];
+    uint32_t xs[kAccPerThread];
+    load_chunk(srow.tr, a.vocab, blockIdx.x, tid, vt, xs);
+    load_chunk(srow.dr, a.vocab, blockIdx.x, tid, vd, xs);
+    uint64_t s = 0;
+#pragma unroll
+    for (int i = 0; i < kAccPerThread; ++i)
+        if (xs[i] < a.vocab) s += sample_w(srow, vt[i], vd[i], a.T);
+    s = block_sum_u64(s, s_red);
+    if (tid == 0) store_coherent_u64(&A.pw[blockIdx.x], s);
+    if (!arrive_last(reinterpret_cast<uint32_t *>(&A.misc[2]), A.L.nch, &s_last)) return;
+
+    // ---- last workgroup: W, fallbacks, the replacement token ----------------
+    __shared__ uint64_t s_W;
+    if (wave == 0) {
+        uint64_t w = 0;
+        for (uint32_t c = lane; c < A.L.nch; c += 64) w += load_coherent_u64(&A.pw[c]);
+        w = wave_sum_u64(w);
+        if (lane == 0) s_W = w;
+    }
+    __syncthreads();
+    int32_t token;
+    if (s_W > 0) {
+        token = sample_token(a, A, srow, A.pw, true, s_W, a.ures[istar]);
+    } else if (srow.sp.sfix > 0) {
+        SampleRows e{srow.tr, nullptr, srow.sp, srow.sp, false};
+        token = sample_token(a, A, e, A.psum + (size_t)istar * A.L.nch, false, srow.sp.sfix,
+                             a.ures[istar]);
+    } else {
+        token = (int32_t)wave_row_argmax(A, istar, false, lane);
+        if (tid == 0) s_tok = token;
+        __syncthreads();
+        token = s_tok;
+    }
+    emit(a, istar, token);
 }
 
 hipError_t launch_accept(hipStream_t s, const float *target, const float *draft,
@@ -483,7 +630,6 @@ hipError_t launch_accept(hipStream_t s, const float *target, const float *draft,
     hipLaunchKernelGGL(acc_stats_kernel, dim3(L.nch, L.rows), dim3(kAccThreads), 0, s, a);
     hipLaunchKernelGGL(acc_sums_kernel, dim3(L.nch, L.rows), dim3(kAccThreads), 0, s, a);
     hipLaunchKernelGGL(acc_residual_kernel, dim3(L.nch), dim3(kAccThreads), 0, s, a);
-    hipLaunchKernelGGL(acc_final_kernel, dim3(1), dim3(kAccThreads), 0, s, a);
     if (ev_stop) (void)hipEventRecord(ev_stop, s);
     return hipGetLastError();
 }

@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -138,21 +139,24 @@ int32_t ensure_moe_scratch(tqf_hip_ctx *ctx, uint32_t hidden, uint32_t width, ui
     (void)hipFree(sc.logits);
     (void)hipFree(sc.plan);
     (void)hipFree(sc.partial);
+    (void)hipFree(sc.gu_partial);
     (void)hipFree(sc.counters);
     sc.xprep = sc.hprep = sc.counters = nullptr;
-    sc.logits = sc.partial = nullptr;
+    sc.logits = sc.partial = sc.gu_partial = nullptr;
     sc.plan = nullptr;
     sc.hidden = sc.width = sc.experts = 0;
     const size_t xprep = (size_t)kMaxTokens * (hidden / 32) * kXprepDwords * 4;
-    const size_t hprep = (size_t)kMaxSlots * kMaxTokens * (width / 32) * kXprepDwords * 4;
+    const size_t hprep = (size_t)kMaxSlots * (width / 32) * kXprepDwords * 4;
     const size_t logits = (size_t)kMaxTokens * (experts + 1) * 4;
-    const size_t partial = (size_t)((kMaxSlots + 3) / 4) * kMaxTokens * hidden * 4;
-    const size_t counters = (size_t)(64 + hidden / 64) * 4;
+    const size_t partial = (size_t)kMaxSlots * kMaxTokens * hidden * 4;
+    const size_t gu_partial = (size_t)kMaxSlots * (width / 64) * 4 * 2 * kWave * 4;
+    const size_t counters = counter_count(hidden, width) * 4;
     TQF_HIP(ctx, hipMalloc(&sc.xprep, xprep));
     TQF_HIP(ctx, hipMalloc(&sc.hprep, hprep));
     TQF_HIP(ctx, hipMalloc(&sc.logits, logits));
     TQF_HIP(ctx, hipMalloc(&sc.plan, sizeof(Plan)));
     TQF_HIP(ctx, hipMalloc(&sc.partial, partial));
+    TQF_HIP(ctx, hipMalloc(&sc.gu_partial, gu_partial));
     TQF_HIP(ctx, hipMalloc(&sc.counters, counters));
     TQF_HIP(ctx, hipMemset(sc.xprep, 0, xprep));
     TQF_HIP(ctx, hipMemset(sc.hprep, 0, hprep));
@@ -170,6 +174,7 @@ int32_t ensure_accept_scratch(tqf_hip_ctx *ctx, size_t bytes) {
     TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
     drop_graphs(ctx);
     TQF_HIP(ctx, grow(sc.accept, sc.accept_bytes, bytes));
+    TQF_HIP(ctx, hipMemset(sc.accept, 0, sc.accept_bytes));  // counters start at zero
     return TQF_HIP_OK;
 }
 
@@ -201,7 +206,7 @@ void resolve_profile(tqf_hip_ctx *ctx) {
             ctx->prof_launches[p.kind] += 1;
             ctx->prof_ms[p.kind] += ms;
             double bytes = p.fixed_bytes;
-            if (p.ring_index >= 0) bytes += p.per_slot_bytes * ctx->prof_ring[p.ring_index];
+            if (p.ring_index >= 0) bytes += p.per_slot_bytes * (ctx->prof_ring[p.ring_index] + 1);
             ctx->prof_bytes[p.kind] += bytes;
         }
         ctx->event_pool.push_back(p.start);
@@ -221,7 +226,8 @@ struct Prof {
             if (start) (void)hipEventRecord(start, ctx->stream);
         }
     }
-    // per_slot_bytes > 0 reads plan->n_slots of the launch just made.
+    // per_slot_bytes > 0 is charged once per distinct expert of the launch
+    // just made: (plan->n_union + 1) including the shared expert.
     void end(int kind, double fixed_bytes, double per_slot_bytes, const Plan *plan) {
         if (!start) return;
         hipEvent_t stop = take_event(ctx);
@@ -230,7 +236,7 @@ struct Prof {
         int ring = -1;
         if (per_slot_bytes > 0 && plan) {
             ring = ctx->prof_ring_next++;
-            (void)hipMemcpyAsync(&ctx->prof_ring[ring], &plan->n_slots, sizeof(int32_t),
+            (void)hipMemcpyAsync(&ctx->prof_ring[ring], &plan->n_union, sizeof(int32_t),
                                  hipMemcpyDeviceToHost, ctx->stream);
         }
         ctx->prof_pending.push_back(ProfileSlot{start, stop, kind, fixed_bytes, per_slot_bytes, ring});
@@ -275,13 +281,14 @@ int32_t enqueue_layer(tqf_hip_ctx *ctx, const LayerDev &L, const float *h, const
     return TQF_HIP_OK;
 }
 
-int32_t enqueue_stack(tqf_hip_ctx *ctx, const tqf_hip_stack *st, float *d_h, uint32_t m,
-                      uint16_t *d_ids, float *d_w, int32_t *d_status) {
+int32_t enqueue_stack(tqf_hip_ctx *ctx, const tqf_hip_stack *st, const float *d_h_in, float *d_h,
+                      uint32_t m, uint16_t *d_ids, float *d_w, int32_t *d_status) {
     for (size_t l = 0; l < st->layers.size(); ++l) {
         const LayerDev &L = st->layers[l]->dev;
         uint16_t *ids = d_ids ? d_ids + l * (size_t)m * kTopK : nullptr;
         float *w = d_w ? d_w + l * (size_t)m * kTopK : nullptr;
-        int32_t rc = enqueue_layer(ctx, L, d_h, st->norms[l], m, d_h, d_h, ids, w, d_status);
+        const float *in = (l == 0 && d_h_in) ? d_h_in : d_h;
+        int32_t rc = enqueue_layer(ctx, L, in, st->norms[l], m, in, d_h, ids, w, d_status);
         if (rc) return rc;
     }
     return TQF_HIP_OK;
@@ -301,9 +308,19 @@ int32_t enqueue_accept(tqf_hip_ctx *ctx, const float *t, const float *d, const i
 
 // Runs `enqueue` eagerly, or captures it once per key into a HIP graph and
 // replays it.  Profiling forces eager execution so events bracket kernels.
+// TQF_HIP_GRAPHS=0 in the environment disables capture (eager launches of
+// the same kernels), e.g. under tracing tools that do not follow graphs.
+bool graphs_enabled() {
+    static const bool on = [] {
+        const char *v = std::getenv("TQF_HIP_GRAPHS");
+        return !(v && v[0] == '0');
+    }();
+    return on;
+}
+
 template <typename F>
 int32_t run_graphed(tqf_hip_ctx *ctx, const std::vector<uint64_t> &key, F enqueue) {
-    if (ctx->profiling) return enqueue();
+    if (ctx->profiling || !graphs_enabled()) return enqueue();
     GraphEntry *g = find_graph(ctx, key);
     if (!g) {
         if (ctx->graphs.size() >= kMaxGraphs) {
@@ -393,6 +410,7 @@ extern "C" int32_t tqf_hip_destroy(tqf_hip_ctx *ctx) {
     (void)hipFree(sc.logits);
     (void)hipFree(sc.plan);
     (void)hipFree(sc.partial);
+    (void)hipFree(sc.gu_partial);
     (void)hipFree(sc.counters);
     (void)hipFree(sc.accept);
     (void)hipFree(ctx->d_stage);
@@ -734,10 +752,14 @@ extern "C" int32_t tqf_hip_expert_forward(tqf_hip_ctx *ctx, const tqf_hip_weight
     const uint8_t *mats[3] = {gate->tiles, up->tiles, down->tiles};
     Plan plan;
     std::memset(&plan, 0, sizeof plan);
-    plan.n_slots = 1;
-    plan.slot_expert[0] = 0;
-    plan.slot_mask[0] = (1u << m) - 1u;
-    for (uint32_t t = 0; t < m; ++t) plan.coef[0][t] = 1.0f;
+    plan.n_slots = (int32_t)m;
+    plan.n_union = 0;
+    plan.m = (int32_t)m;
+    for (uint32_t t = 0; t < m; ++t) {
+        plan.slot_expert[t] = 0;
+        plan.slot_token[t] = (int32_t)t;
+        plan.slot_coef[t] = 1.0f;
+    }
     TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
     drop_graphs(ctx);
     TQF_HIP(ctx, hipMemcpy(ctx->d_adhoc_mats, mats, sizeof mats, hipMemcpyHostToDevice));
@@ -910,14 +932,17 @@ extern "C" int32_t tqf_hip_stack_free(tqf_hip_ctx *ctx, tqf_hip_stack *stack) {
 }
 
 extern "C" int32_t tqf_hip_stack_forward_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack,
-                                                float *d_h, uint32_t m, uint16_t *d_ids,
-                                                float *d_w, int32_t *d_status) {
+                                                const float *d_h_in, float *d_h, uint32_t m,
+                                                uint16_t *d_ids, float *d_w, int32_t *d_status) {
     TQF_ENTER(ctx);
     if (!stack || !d_h) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
     if (m == 0 || m > kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "m must be in 1..8");
     if (int32_t rc = ensure_moe_scratch(ctx, stack->hidden, stack->width, stack->experts)) return rc;
-    std::vector<uint64_t> key = {1, k64(stack), k64(d_h), m, k64(d_ids), k64(d_w), k64(d_status)};
-    return run_graphed(ctx, key, [&]() { return enqueue_stack(ctx, stack, d_h, m, d_ids, d_w, d_status); });
+    std::vector<uint64_t> key = {1, k64(stack), k64(d_h_in), k64(d_h), m, k64(d_ids), k64(d_w),
+                                 k64(d_status)};
+    return run_graphed(ctx, key, [&]() {
+        return enqueue_stack(ctx, stack, d_h_in, d_h, m, d_ids, d_w, d_status);
+    });
 }
 
 // ===========================================================================
@@ -1033,7 +1058,8 @@ extern "C" int32_t tqf_hip_top_logit_candidates(tqf_hip_ctx *ctx, const float *l
 // verify step
 // ===========================================================================
 extern "C" int32_t tqf_hip_verify_step_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack,
-                                              float *d_h, uint32_t m, const float *d_target,
+                                              const float *d_h_in, float *d_h, uint32_t m,
+                                              const float *d_target,
                                               const float *d_draft, const int32_t *d_dtok,
                                               uint32_t vocab, float temperature, int32_t greedy,
                                               const float *d_u, const float *d_ures,
@@ -1051,11 +1077,11 @@ extern "C" int32_t tqf_hip_verify_step_device(tqf_hip_ctx *ctx, const tqf_hip_st
     if (int32_t rc = ensure_accept_scratch(ctx, accept_scratch_bytes(k, vocab))) return rc;
     uint32_t tbits;
     std::memcpy(&tbits, &temperature, 4);
-    std::vector<uint64_t> key = {2,          k64(stack), k64(d_h),   m,           k64(d_target),
+    std::vector<uint64_t> key = {2,          k64(stack), k64(d_h_in), k64(d_h), m, k64(d_target),
                                  k64(d_draft), k64(d_dtok), vocab,     tbits,       (uint64_t)greedy,
                                  k64(d_u),   k64(d_ures), k64(d_accepted), k64(d_tokens)};
     return run_graphed(ctx, key, [&]() {
-        if (int32_t rc = enqueue_stack(ctx, stack, d_h, m, nullptr, nullptr, nullptr)) return rc;
+        if (int32_t rc = enqueue_stack(ctx, stack, d_h_in, d_h, m, nullptr, nullptr, nullptr)) return rc;
         return enqueue_accept(ctx, d_target, d_draft, d_dtok, k, vocab, temperature, greedy, d_u,
                               d_ures, d_accepted, d_tokens);
     });

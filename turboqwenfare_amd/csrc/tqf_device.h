@@ -12,6 +12,79 @@ __device__ __forceinline__ float f16_to_f32(uint32_t h16) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(h16 & 0xFFFFu));
 }
 
+// ---- wavefront reductions with DPP (no LDS round trip) ---------------------
+// gfx9 DPP controls: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1]
+// (lane ^ 2), row_half_mirror (lane i <- 7 - i within 8), row_mirror
+// (lane i <- 15 - i within 16).  After the four steps every lane of a 16-lane
+// row holds the row's result; rows are combined through v_readlane.
+constexpr int kDppXor1 = 0xB1;
+constexpr int kDppXor2 = 0x4E;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+
+struct AddOp {
+    __device__ float operator()(float a, float b) const { return a + b; }
+    __device__ int operator()(int a, int b) const { return a + b; }
+};
+struct MaxOp {
+    __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+    __device__ int operator()(int a, int b) const { return a > b ? a : b; }
+};
+struct MinOp {
+    __device__ int operator()(int a, int b) const { return a < b ? a : b; }
+};
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+__device__ __forceinline__ int readlane_i(int v, int lane) {
+    return __builtin_amdgcn_readlane(v, lane);
+}
+
+// All-reduce over aligned groups of LANES lanes (2..64); every lane of a
+// group receives the group's result.  All lanes of a group must be active.
+template <int LANES, typename Op>
+__device__ __forceinline__ float group_reduce(float v, Op op) {
+    if constexpr (LANES >= 2) v = op(v, dpp_f<kDppXor1>(v));
+    if constexpr (LANES >= 4) v = op(v, dpp_f<kDppXor2>(v));
+    if constexpr (LANES >= 8) v = op(v, dpp_f<kDppHalfMirror>(v));
+    if constexpr (LANES >= 16) v = op(v, dpp_f<kDppMirror>(v));
+    if constexpr (LANES >= 32) {
+        const float a = readlane_f(v, 0), b = readlane_f(v, 16);
+        const float c = readlane_f(v, 32), d = readlane_f(v, 48);
+        if constexpr (LANES == 32)
+            v = (threadIdx.x & 32) ? op(c, d) : op(a, b);
+        else
+            v = op(op(a, b), op(c, d));
+    }
+    return v;
+}
+template <int LANES, typename Op>
+__device__ __forceinline__ int group_reduce(int v, Op op) {
+    if constexpr (LANES >= 2) v = op(v, dpp_i<kDppXor1>(v));
+    if constexpr (LANES >= 4) v = op(v, dpp_i<kDppXor2>(v));
+    if constexpr (LANES >= 8) v = op(v, dpp_i<kDppHalfMirror>(v));
+    if constexpr (LANES >= 16) v = op(v, dpp_i<kDppMirror>(v));
+    if constexpr (LANES >= 32) {
+        const int a = readlane_i(v, 0), b = readlane_i(v, 16);
+        const int c = readlane_i(v, 32), d = readlane_i(v, 48);
+        if constexpr (LANES == 32)
+            v = (threadIdx.x & 32) ? op(c, d) : op(a, b);
+        else
+            v = op(op(a, b), op(c, d));
+    }
+    return v;
+}
+
 // Scale of a 32-element activation block: x = X * 2^e with |X| <= 2^22.
 // Returns 2^e; 0 for a block whose max |x| is below 2^-100 (its products are
 // below fp32 resolution of any finite output); NaN if the block holds a
@@ -51,10 +124,9 @@ __device__ __forceinline__ void prep_block(const float (&v)[EPL], int lane_in_gr
         amax = fmaxf(amax, b ? 0.0f : a);
     }
     int badi = bad ? 1 : 0;
-#pragma unroll
-    for (int off = 1; off < LPB; off <<= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, off));
-        badi |= __shfl_xor(badi, off);
+    if constexpr (LPB > 1) {
+        amax = group_reduce<LPB>(amax, MaxOp());
+        badi = group_reduce<LPB>(badi, MaxOp());
     }
     int e;
     float scale = block_scale(amax, badi != 0, e);
@@ -71,11 +143,10 @@ __device__ __forceinline__ void prep_block(const float (&v)[EPL], int lane_in_gr
         pk1[i / 4] |= ((uint32_t)d1 & 0xFFu) << (8 * (i % 4));
         pk2[i / 4] |= ((uint32_t)d2 & 0xFFu) << (8 * (i % 4));
     }
-#pragma unroll
-    for (int off = 1; off < LPB; off <<= 1) {
-        s0 += __shfl_xor(s0, off);
-        s1 += __shfl_xor(s1, off);
-        s2 += __shfl_xor(s2, off);
+    if constexpr (LPB > 1) {
+        s0 = group_reduce<LPB>(s0, AddOp());
+        s1 = group_reduce<LPB>(s1, AddOp());
+        s2 = group_reduce<LPB>(s2, AddOp());
     }
     if constexpr (EPL >= 4) {
 #pragma unroll

@@ -50,7 +50,8 @@ constexpr int kXprepDwords = 32;
 constexpr int kTopK = TQF_HIP_TOP_K;
 constexpr int kMaxTokens = TQF_HIP_MAX_TOKENS;
 constexpr int kMaxExperts = 256;
-constexpr int kMaxSlots = kMaxTokens * kTopK + 1;  // union + shared expert
+// One slot per (expert, token) pair: M shared-expert pairs + 8M routed pairs.
+constexpr int kMaxSlots = kMaxTokens * (kTopK + 1);
 // Algorithmic bytes of one GGML Q4_0 block.
 constexpr int kQ4Block = 18;
 
@@ -73,18 +74,25 @@ inline size_t tile_bytes(const MatrixDims &d) {
 }
 
 // Route plan written by the route kernel and read by the expert kernels.
-// Slot 0 is the shared expert (all tokens); slots 1.. are the distinct routed
-// experts in first-demand order (experts/mod.rs:268-275 BatchExpertPlan).
+// Work is planned per (expert, token) pair so that every workgroup carries
+// the same arithmetic: slots [0, M) are the shared expert for tokens 0..M-1
+// (coefficient sigmoid(shared gate logit), experts/mod.rs:1614-1615); then,
+// for each distinct routed expert in first-demand order (the union of
+// experts/mod.rs:268-275 BatchExpertPlan), one slot per token routed to it
+// (coefficient = that token's route weight).  Slots of one expert are
+// adjacent, so its second reads come from L2 / Infinity Cache.
 struct Plan {
-    int32_t n_slots;
-    int32_t status;  // 0 or TQF_HIP_ERR_ROUTER
-    int32_t pad[2];
-    int32_t slot_expert[kMaxSlots];   // expert index; n_experts = shared
-    uint32_t slot_mask[kMaxSlots];    // bit t: token t uses this slot
-    float coef[kMaxSlots][kMaxTokens];  // combine coefficient per (slot, token)
+    int32_t n_slots;  // 9 * M when routing succeeded, 0 otherwise
+    int32_t status;   // 0 or TQF_HIP_ERR_ROUTER
+    int32_t n_union;  // distinct routed experts (HBM bytes = (n_union + 1) experts)
+    int32_t m;
+    int32_t slot_expert[kMaxSlots];  // expert index; n_experts = shared
+    int32_t slot_token[kMaxSlots];
+    float slot_coef[kMaxSlots];
     uint16_t ids[kMaxTokens][kTopK];
     float weights[kMaxTokens][kTopK];
     float gate_logit[kMaxTokens];
+    int32_t union_ids[kMaxTokens * kTopK];
 };
 
 // Device-side description of one MoE layer (passed by value to kernels).
@@ -102,7 +110,8 @@ struct Scratch {
     float *logits = nullptr;     // [kMaxTokens x (n_experts + 1)]
     Plan *plan = nullptr;
     float *partial = nullptr;    // [slot groups x kMaxTokens x hidden]
-    uint32_t *counters = nullptr;  // [64 + hidden/64] last-arriver counters
+    float *gu_partial = nullptr; // [kMaxSlots x width/64 x 4 x 2 x 64] split-K gate/up
+    uint32_t *counters = nullptr;  // last-arriver counters (see kCounter*)
     void *accept = nullptr;      // acceptance partials
     size_t accept_bytes = 0;
     uint32_t hidden = 0, width = 0, experts = 0;
@@ -184,6 +193,21 @@ struct tqf_hip_ctx {
 };
 
 namespace tqf {
+
+// Counter array layout: [route (1) | pad | down (hidden/64) | gate/up
+// (kMaxSlots * width/64)].  Every counter returns to zero when its kernel ends.
+constexpr int kCounterDown = 64;
+inline size_t counter_gate_up_offset(uint32_t hidden) { return kCounterDown + hidden / 64; }
+inline size_t counter_count(uint32_t hidden, uint32_t width) {
+    return counter_gate_up_offset(hidden) + (size_t)kMaxSlots * (width / 64);
+}
+// Split-K factor of the gate/up kernel for M tokens (keeps >= 256 workgroups).
+inline uint32_t gate_up_kparts(uint32_t m, uint32_t hidden) {
+    const uint32_t chunks = hidden / 256;
+    uint32_t kp = m >= 4 ? 1 : (m >= 2 ? 2 : 4);
+    while (kp > 1 && chunks % kp) kp >>= 1;
+    return kp;
+}
 
 // ---- launchers (defined in the .hip translation units) -------------------
 // All are asynchronous on ctx->stream and return a hipError_t.

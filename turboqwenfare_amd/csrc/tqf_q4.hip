@@ -116,7 +116,8 @@ __global__ __launch_bounds__(512) void gemv_kernel(const uint8_t *const *__restr
                                                    const uint32_t *__restrict__ xprep,
                                                    uint32_t m, float *__restrict__ y) {
     __shared__ float red[8][MT][kWave];
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int lane = threadIdx.x % kWave;
     const int waves = blockDim.x / kWave;
     const uint32_t g = blockIdx.x, mat = blockIdx.y;
     const uint8_t *tiles = tables[mat];
@@ -159,15 +160,39 @@ hipError_t launch_gemv(hipStream_t s, const uint8_t *const *d_tiles, uint32_t co
 }
 
 // ---------------------------------------------------------------------------
+// Cross-workgroup hand-off without whole-L2 write-back/invalidate fences.
+// Values that another workgroup will read are stored with agent-scope
+// atomic stores (coherent at device scope, i.e. not left dirty in one XCD's
+// L2), each thread waits for its stores to complete, and only then is the
+// device-scope counter incremented; the workgroup that sees the final count
+// reads the values back with agent-scope atomic loads.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void store_coherent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_own_stores() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+__device__ __forceinline__ uint32_t counter_arrive(uint32_t *c) {
+    return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void counter_reset(uint32_t *c) {
+    __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
 // Block-wide reduction of N floats per thread (256 threads); result valid in
 // every thread.
 // ---------------------------------------------------------------------------
 template <int N>
 __device__ __forceinline__ void block_sum_256(float (&v)[N], float (*lds)[N]) {
 #pragma unroll
-    for (int i = 0; i < N; ++i)
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) v[i] += __shfl_xor(v[i], off);
+    for (int i = 0; i < N; ++i) v[i] = group_reduce<64>(v[i], AddOp());
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     __syncthreads();
     if (lane == 0)
@@ -185,11 +210,9 @@ __device__ __forceinline__ void block_sum_256(float (&v)[N], float (*lds)[N]) {
 //      (weights.rs:216-239: x * (1/sqrt(mean(x^2) + 1e-6)) * w),
 //   2. writes the xprep records of the blocks assigned to it,
 //   3. computes its router logits (experts/mod.rs:1491 router matvec).
-// The last workgroup to finish (device-scope counter) turns the logits into
-// routes (RouterResult::from_logits, experts/mod.rs:134-167: softmax, stable
-// descending top-8 with ties to the lower id, renormalise) and the slot plan
-// (union in first-demand order, slot 0 = shared expert with coefficient
-// sigmoid(gate logit), routed coefficients = route weights).
+// The last workgroup to finish turns the logits into routes
+// (RouterResult::from_logits, experts/mod.rs:134-167: softmax, stable
+// descending top-8 with ties to the lower id, renormalise) and the pair plan.
 // ---------------------------------------------------------------------------
 constexpr int kRouteRows = 2;
 
@@ -207,9 +230,8 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
     __shared__ float lds_norm[4][MT];
     __shared__ int s_last;
     __shared__ int s_bad;
-    __shared__ uint16_t s_ids[kMaxTokens][kTopK];
-    __shared__ float s_w[kMaxTokens][kTopK];
-    __shared__ int s_slot_of[kMaxExperts];
+    __shared__ int s_ids[kMaxTokens * kTopK];
+    __shared__ float s_w[kMaxTokens * kTopK];
 
     const int tid = threadIdx.x;
     const uint32_t H = L.hidden, E = L.n_experts;
@@ -295,20 +317,18 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
         for (int rr = 0; rr < kRouteRows; ++rr) {
             const uint32_t r = blockIdx.x * kRouteRows + rr;
             if (r <= E)
-                for (int t = 0; t < (int)m; ++t) logits[(size_t)t * (E + 1) + r] = dots[rr * MT + t];
+                for (int t = 0; t < (int)m; ++t)
+                    store_coherent(&logits[(size_t)t * (E + 1) + r], dots[rr * MT + t]);
         }
-        __threadfence();
-        const uint32_t prev = atomicAdd(counter, 1u);
-        s_last = (prev == gridDim.x - 1) ? 1 : 0;
+        wait_own_stores();
+        s_last = (counter_arrive(counter) == gridDim.x - 1) ? 1 : 0;
     }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
 
-    // ---- last workgroup: routes ------------------------------------------
+    // ---- last workgroup: routes and the pair plan --------------------------
     const int wave = tid / kWave, lane = tid % kWave;
     if (tid == 0) s_bad = 0;
-    for (int e = tid; e < kMaxExperts; e += 256) s_slot_of[e] = -1;
     __syncthreads();
     for (int t = wave; t < (int)m; t += 4) {
         const float *lt = logits + (size_t)t * (E + 1);
@@ -317,16 +337,14 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t e = (uint32_t)lane + 64u * i;
-            lv[i] = e < E ? __builtin_nontemporal_load(lt + e) : -INFINITY;
+            lv[i] = e < E ? load_coherent(lt + e) : -INFINITY;
             if (e < E && !(fabsf(lv[i]) <= 3.402823466e38f)) fin = false;
         }
         if (__any(!fin)) {
             if (lane == 0) s_bad = 1;
             continue;
         }
-        float mx = fmaxf(fmaxf(lv[0], lv[1]), fmaxf(lv[2], lv[3]));
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        const float mx = group_reduce<64>(fmaxf(fmaxf(lv[0], lv[1]), fmaxf(lv[2], lv[3])), MaxOp());
         float p[4], ssum = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -334,30 +352,26 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
             p[i] = e < E ? expf(lv[i] - mx) : 0.0f;
             ssum += p[i];
         }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) ssum += __shfl_xor(ssum, off);
+        ssum = group_reduce<64>(ssum, AddOp());
 #pragma unroll
         for (int i = 0; i < 4; ++i) p[i] = ((uint32_t)lane + 64u * i < E) ? p[i] / ssum : -1.0f;
         float psel[kTopK];
         int idsel[kTopK];
+#pragma unroll
         for (int k = 0; k < kTopK; ++k) {
-            // best of this lane: highest p, then lowest id (ids ascend with i)
-            float bp = -1.0f;
-            int bid = 0x7FFFFFFF;
+            // lane's best: highest p, then lowest id (ids ascend with i)
+            float bp = p[0];
+            int bid = lane;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 1; i < 4; ++i)
                 if (p[i] > bp) { bp = p[i]; bid = lane + 64 * i; }
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                const float op = __shfl_xor(bp, off);
-                const int oid = __shfl_xor(bid, off);
-                if (op > bp || (op == bp && oid < bid)) { bp = op; bid = oid; }
-            }
-            psel[k] = bp;
-            idsel[k] = bid;
+            const float best = group_reduce<64>(bp, MaxOp());
+            const int win = group_reduce<64>(bp == best ? bid : 0x7FFFFFFF, MinOp());
+            psel[k] = best;
+            idsel[k] = win;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                if (lane + 64 * i == bid) p[i] = -1.0f;
+                if (lane + 64 * i == win) p[i] = -1.0f;
         }
         if (lane == 0) {
             float total = -0.0f;
@@ -365,57 +379,75 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
             float wsum = 0.0f;
             for (int k = 0; k < kTopK; ++k) {
                 const float wk = psel[k] / total;
-                s_ids[t][k] = (uint16_t)idsel[k];
-                s_w[t][k] = wk;
+                s_ids[t * kTopK + k] = idsel[k];
+                s_w[t * kTopK + k] = wk;
                 wsum += wk;
             }
             if (!(fabsf(wsum - 1.0f) <= 1e-4f)) s_bad = 1;
         }
     }
     __syncthreads();
-    if (tid == 0) {
-        if (s_bad) {
+    const int n = (int)m * kTopK;
+    if (s_bad) {
+        if (tid == 0) {
             plan->n_slots = 0;
+            plan->n_union = 0;
             plan->status = TQF_HIP_ERR_ROUTER;
-        } else {
-            int n = 1;
-            plan->slot_expert[0] = (int)E;
-            plan->slot_mask[0] = (1u << m) - 1u;
-            for (int t = 0; t < kMaxTokens; ++t) {
-                const float gl = (t < (int)m) ? logits[(size_t)t * (E + 1) + E] : 0.0f;
-                plan->gate_logit[t] = gl;
-                plan->coef[0][t] = (t < (int)m) ? 1.0f / (1.0f + expf(-gl)) : 0.0f;
-            }
-            for (int t = 0; t < (int)m; ++t) {
-                for (int k = 0; k < kTopK; ++k) {
-                    const int e = s_ids[t][k];
-                    int s = s_slot_of[e];
-                    if (s < 0) {
-                        s = n++;
-                        s_slot_of[e] = s;
-                        plan->slot_expert[s] = e;
-                        plan->slot_mask[s] = 0;
-                        for (int tt = 0; tt < kMaxTokens; ++tt) plan->coef[s][tt] = 0.0f;
-                    }
-                    plan->slot_mask[s] |= 1u << t;
-                    plan->coef[s][t] = s_w[t][k];
-                    plan->ids[t][k] = (uint16_t)e;
-                    plan->weights[t][k] = s_w[t][k];
-                }
-            }
-            plan->n_slots = n;
-            plan->status = 0;
+            plan->m = (int)m;
+            if (status_out) *status_out = TQF_HIP_ERR_ROUTER;
+            counter_reset(counter);
         }
-        if (status_out && plan->status) *status_out = plan->status;
-        *counter = 0u;
+        return;
     }
-    if (ids_out != nullptr || w_out != nullptr) {
-        __syncthreads();
-        if (!s_bad) {
-            for (int i = tid; i < (int)m * kTopK; i += 256) {
-                if (ids_out) ids_out[i] = s_ids[i / kTopK][i % kTopK];
-                if (w_out) w_out[i] = s_w[i / kTopK][i % kTopK];
+    // Pair plan, one route entry i = (t, k) per lane of wave 0 (n <= 64).
+    if (wave == 0) {
+        const int e_i = lane < n ? s_ids[lane] : -1;
+        int first = lane, cnt = 0, rank = 0;
+        for (int j = 0; j < n; ++j) {
+            const int ej = readlane_i(e_i, j);
+            if (ej == e_i) {
+                ++cnt;
+                if (j < lane) ++rank;
+                if (j < first) first = j;
             }
+        }
+        const bool flag = lane < n && first == lane;
+        const int fc = flag ? cnt : 0;
+        int base = 0, upos = 0;
+        for (int j = 0; j < n; ++j) {
+            const int fcj = readlane_i(fc, j);
+            if (j < first) {
+                base += fcj;
+                upos += fcj ? 1 : 0;
+            }
+        }
+        const int nu = __builtin_popcountll(__ballot(flag));
+        if (lane < n) {
+            const int slot = (int)m + base + rank;
+            const int t = lane / kTopK, k = lane % kTopK;
+            const float wv = s_w[lane];
+            plan->slot_expert[slot] = e_i;
+            plan->slot_token[slot] = t;
+            plan->slot_coef[slot] = wv;
+            plan->ids[t][k] = (uint16_t)e_i;
+            plan->weights[t][k] = wv;
+            if (flag) plan->union_ids[upos] = e_i;
+            if (ids_out) ids_out[lane] = (uint16_t)e_i;
+            if (w_out) w_out[lane] = wv;
+        }
+        if (lane < (int)m) {
+            const float gl = load_coherent(logits + (size_t)lane * (E + 1) + E);
+            plan->gate_logit[lane] = gl;
+            plan->slot_expert[lane] = (int)E;
+            plan->slot_token[lane] = lane;
+            plan->slot_coef[lane] = 1.0f / (1.0f + expf(-gl));
+        }
+        if (lane == 0) {
+            plan->n_union = nu;
+            plan->n_slots = (int)m * (kTopK + 1);
+            plan->status = 0;
+            plan->m = (int)m;
+            counter_reset(counter);
         }
     }
 }
@@ -424,7 +456,7 @@ hipError_t launch_route(hipStream_t s, const LayerDev &L, const float *h, const 
                         uint32_t m, Scratch &sc, uint16_t *ids_out, float *w_out,
                         int32_t *status_out) {
     const uint32_t grid = (L.n_experts + 1 + kRouteRows - 1) / kRouteRows;
-    uint32_t *counter = sc.counters;  // counters[0] belongs to the route kernel
+    uint32_t *counter = sc.counters;
 #define TQF_ROUTE(MT)                                                                        \
     hipLaunchKernelGGL(route_kernel<MT>, dim3(grid), dim3(256), 0, s, L, h, norm, m, sc.xprep, \
                        sc.logits, sc.plan, counter, ids_out, w_out, status_out)
@@ -437,68 +469,94 @@ hipError_t launch_route(hipStream_t s, const LayerDev &L, const float *h, const 
 }
 
 // ---------------------------------------------------------------------------
-// Token list of a slot from its mask (uniform per wavefront).
+// One wavefront's share of a pair slot: chunks [c_begin, c_end) step `step`
+// of one matrix for one token.
 // ---------------------------------------------------------------------------
-template <int MT>
-__device__ __forceinline__ int mask_tokens(uint32_t mask, int (&tok)[MT]) {
-    int n = 0;
-#pragma unroll
-    for (int t = 0; t < MT; ++t) tok[t] = 0;
-    for (int t = 0; t < kMaxTokens; ++t)
-        if ((mask >> t) & 1u) {
-            if (n < MT) tok[n] = t;
-            ++n;
-        }
-    return n;
+__device__ __forceinline__ float slot_dot(const uint8_t *tiles, int lane, uint32_t c_begin,
+                                          uint32_t c_end, uint32_t step,
+                                          const uint32_t *__restrict__ xp_token) {
+    float acc = 0.0f;
+    int tok[1] = {0};
+    float a[1] = {0.0f};
+    for (uint32_t c = c_begin; c < c_end; c += step) {
+        uint4 nib[kChunkBlocks], scl;
+        load_tile(tiles + (size_t)c * kTileBytes, lane, nib, scl);
+        a[0] = 0.0f;
+        tile_accumulate<1>(nib, scl, c, xp_token, 0, tok, 1, a);
+        acc += a[0];
+    }
+    return acc;
 }
 
 // ---------------------------------------------------------------------------
-// Gate/up kernel.  Grid (width/64 row groups, slots); 8 wavefronts per
-// workgroup: waves 0-3 read the gate matrix, 4-7 the up matrix, each a
-// quarter of the hidden dimension.  The epilogue forms
-// h = silu(gate) * up (weights.rs:241-259) for 64 rows x the slot's tokens
-// and writes h as xprep records for the down kernel.
+// Gate/up kernel.  Grid (width/64 row groups, pair slots, K parts).  A
+// workgroup holds 2 * W wavefronts: W read the gate matrix and W the up
+// matrix, each wavefront one 9 KiB tile (64 rows x 256 columns) at a time.
+// Partials meet in LDS; with one K part the workgroup forms
+// h = silu(gate) * up (weights.rs:241-259) for its 64 rows and writes h as
+// xprep records for the down kernel.  With several K parts (small M, so the
+// grid still covers every CU) the parts hand off through device-coherent
+// partials and the last part to finish forms h.
 // ---------------------------------------------------------------------------
-template <int MT>
-__global__ __launch_bounds__(512) void gate_up_kernel(LayerDev L, const Plan *__restrict__ plan,
-                                                      const uint32_t *__restrict__ xprep,
-                                                      uint32_t *__restrict__ hprep) {
-    __shared__ float red[8][MT][kWave];
+__global__ __launch_bounds__(1024) void gate_up_kernel(LayerDev L, const Plan *__restrict__ plan,
+                                                       const uint32_t *__restrict__ xprep,
+                                                       uint32_t *__restrict__ hprep,
+                                                       float *__restrict__ gu_partial,
+                                                       uint32_t *__restrict__ counters) {
+    __shared__ float red[16][kWave];
+    __shared__ int s_last;
     const int slot = blockIdx.y;
     if (slot >= plan->n_slots) return;
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const uint32_t g = blockIdx.x;
-    const int expert = plan->slot_expert[slot];
-    int tok[MT];
-    const int m_tok = mask_tokens<MT>(plan->slot_mask[slot], tok);
-    const int mat = wave >> 2, quarter = wave & 3;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int lane = threadIdx.x % kWave;
+    const int waves = blockDim.x / kWave;
+    const int wpm = waves / 2;
+    const uint32_t g = blockIdx.x, kpart = blockIdx.z, kp = gridDim.z;
+    const uint32_t G = gridDim.x;
+    const int expert = __builtin_amdgcn_readfirstlane(plan->slot_expert[slot]);
+    const int tok = __builtin_amdgcn_readfirstlane(plan->slot_token[slot]);
+    const int mat = wave / wpm, wi = wave % wpm;
     const uint32_t chunks = L.hidden / kChunkCols;
+    const uint32_t cpk = chunks / kp;
     const uint32_t bpt = L.hidden / 32;
     const uint8_t *tiles = L.mats[expert * 3 + mat] + (size_t)g * chunks * kTileBytes;
-
-    float acc[MT];
-#pragma unroll
-    for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
-    for (uint32_t c0 = quarter; c0 < chunks; c0 += 8) {
-        const uint32_t c1 = c0 + 4;
-        uint4 nib0[kChunkBlocks], scl0, nib1[kChunkBlocks], scl1;
-        load_tile(tiles + (size_t)c0 * kTileBytes, lane, nib0, scl0);
-        const bool has1 = c1 < chunks;
-        if (has1) load_tile(tiles + (size_t)c1 * kTileBytes, lane, nib1, scl1);
-        tile_accumulate<MT>(nib0, scl0, c0, xprep, bpt, tok, m_tok, acc);
-        if (has1) tile_accumulate<MT>(nib1, scl1, c1, xprep, bpt, tok, m_tok, acc);
-    }
-#pragma unroll
-    for (int t = 0; t < MT; ++t) red[wave][t][lane] = acc[t];
+    const uint32_t *xp = xprep + (size_t)tok * bpt * kXprepDwords;
+    red[wave][lane] = slot_dot(tiles, lane, kpart * cpk + wi, (kpart + 1) * cpk, wpm, xp);
     __syncthreads();
-    const int ti = wave;
-    if (ti < m_tok && ti < MT) {
-        const float gate = (red[0][ti][lane] + red[1][ti][lane]) + (red[2][ti][lane] + red[3][ti][lane]);
-        const float up = (red[4][ti][lane] + red[5][ti][lane]) + (red[6][ti][lane] + red[7][ti][lane]);
+    float gate = 0.0f, up = 0.0f;
+    if (wave == 0) {
+        for (int w = 0; w < wpm; ++w) {
+            gate += red[w][lane];
+            up += red[wpm + w][lane];
+        }
+    }
+    if (kp > 1) {
+        float *part = gu_partial + ((size_t)(slot * G + g) * 4) * 2 * kWave;
+        if (wave == 0) {
+            store_coherent(&part[(kpart * 2 + 0) * kWave + lane], gate);
+            store_coherent(&part[(kpart * 2 + 1) * kWave + lane], up);
+            wait_own_stores();
+        }
+        __syncthreads();
+        uint32_t *ctr = counters + slot * G + g;
+        if (threadIdx.x == 0) s_last = (counter_arrive(ctr) == kp - 1) ? 1 : 0;
+        __syncthreads();
+        if (!s_last) return;
+        if (wave == 0) {
+            gate = 0.0f;
+            up = 0.0f;
+            for (uint32_t q = 0; q < kp; ++q) {
+                gate += load_coherent(&part[(q * 2 + 0) * kWave + lane]);
+                up += load_coherent(&part[(q * 2 + 1) * kWave + lane]);
+            }
+            if (lane == 0) counter_reset(ctr);
+        }
+    }
+    if (wave == 0) {
         const float hv = (gate / (1.0f + expf(-gate))) * up;
         const uint32_t hb = L.width / 32;
         const uint32_t blk = g * 2 + (uint32_t)(lane >> 5);
-        uint32_t *rec = hprep + (((size_t)slot * kMaxTokens + tok[ti]) * hb + blk) * kXprepDwords;
+        uint32_t *rec = hprep + ((size_t)slot * hb + blk) * kXprepDwords;
         float v1[1] = {hv};
         prep_block<1>(v1, lane & 31, rec);
     }
@@ -506,106 +564,89 @@ __global__ __launch_bounds__(512) void gate_up_kernel(LayerDev L, const Plan *__
 
 hipError_t launch_gate_up(hipStream_t s, const LayerDev &L, uint32_t m, Scratch &sc,
                           const Plan *plan, const uint32_t *xprep) {
-    const uint32_t max_slots = m * kTopK + 1;
-    dim3 grid(L.width / kRowsPerGroup, max_slots), block(8 * kWave);
-    if (m <= 1)
-        hipLaunchKernelGGL(gate_up_kernel<1>, grid, block, 0, s, L, plan, xprep, sc.hprep);
-    else if (m <= 2)
-        hipLaunchKernelGGL(gate_up_kernel<2>, grid, block, 0, s, L, plan, xprep, sc.hprep);
-    else if (m <= 4)
-        hipLaunchKernelGGL(gate_up_kernel<4>, grid, block, 0, s, L, plan, xprep, sc.hprep);
-    else
-        hipLaunchKernelGGL(gate_up_kernel<8>, grid, block, 0, s, L, plan, xprep, sc.hprep);
+    const uint32_t kp = gate_up_kparts(m, L.hidden);
+    const uint32_t cpk = (L.hidden / kChunkCols) / kp;
+    const uint32_t wpm = cpk < 8 ? cpk : 8;
+    dim3 grid(L.width / kRowsPerGroup, m * (kTopK + 1), kp), block(2 * wpm * kWave);
+    hipLaunchKernelGGL(gate_up_kernel, grid, block, 0, s, L, plan, xprep, sc.hprep, sc.gu_partial,
+                       sc.counters + counter_gate_up_offset(L.hidden));
     return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
-// Down kernel.  Grid (hidden/64 row groups, slot groups of 4); wavefront w
-// computes slot 4*sg + w over the whole width.  The workgroup combines its
-// four slots with the plan coefficients (shared: sigmoid gate; routed: the
-// route weight; experts/mod.rs:1609-1630) into one partial per token; the
-// last workgroup of a row group (device-scope counter) sums the partials in
-// slot-group order and adds the residual (runtime.rs:802) when given.
+// Down kernel.  Grid (hidden/64 row groups, slot groups of `spg` pair
+// slots); each wavefront takes one 9 KiB tile (one slot, one 256-column
+// chunk of the width).  The workgroup weights each slot by its coefficient
+// (shared: sigmoid gate; routed: route weight; experts/mod.rs:1609-1630) and
+// sums per token; the last workgroup of a row group sums the slot groups in
+// order and adds the residual (runtime.rs:802) when given.
 // ---------------------------------------------------------------------------
-template <int MT>
-__global__ __launch_bounds__(256) void down_kernel(LayerDev L, const Plan *__restrict__ plan,
-                                                   const uint32_t *__restrict__ hprep,
-                                                   float *__restrict__ partial,
-                                                   uint32_t *__restrict__ counters,
-                                                   const float *resid, float *out, uint32_t m) {
-    __shared__ float red[4][kMaxTokens][kWave];
+__global__ __launch_bounds__(1024) void down_kernel(LayerDev L, const Plan *__restrict__ plan,
+                                                    const uint32_t *__restrict__ hprep,
+                                                    float *__restrict__ partial,
+                                                    uint32_t *__restrict__ counters,
+                                                    const float *resid, float *out, uint32_t m,
+                                                    uint32_t spg) {
+    __shared__ float red[16][kWave];
+    __shared__ int s_tok[16];
     __shared__ int s_last;
     const int n_slots = plan->n_slots;
-    const int n_sg = (n_slots + 3) / 4;
+    const int n_sg = (n_slots + (int)spg - 1) / (int)spg;
     const int sg = blockIdx.y;
     if (sg >= n_sg) return;
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int lane = threadIdx.x % kWave;
+    const int waves = blockDim.x / kWave;
+    const uint32_t chunks = L.width / kChunkCols;
+    const int slot = sg * (int)spg + wave / (int)chunks;
+    const uint32_t c = (uint32_t)wave % chunks;
     const uint32_t g = blockIdx.x;
     const uint32_t H = L.hidden;
-    const int slot = sg * 4 + wave;
-    const bool active = slot < n_slots;
-    for (int t = 0; t < (int)m; ++t) red[wave][t][lane] = 0.0f;
-    if (active) {
-        const int expert = plan->slot_expert[slot];
-        int tok[MT];
-        const int m_tok = mask_tokens<MT>(plan->slot_mask[slot], tok);
-        const uint32_t chunks = L.width / kChunkCols;
-        const uint32_t hb = L.width / 32;
+    const uint32_t hb = L.width / 32;
+    float v = 0.0f;
+    int tok = -1;
+    if (slot < n_slots) {
+        const int expert = __builtin_amdgcn_readfirstlane(plan->slot_expert[slot]);
+        tok = __builtin_amdgcn_readfirstlane(plan->slot_token[slot]);
+        const float coef = plan->slot_coef[slot];
         const uint8_t *tiles = L.mats[expert * 3 + 2] + (size_t)g * chunks * kTileBytes;
-        const uint32_t *hp = hprep + (size_t)slot * kMaxTokens * hb * kXprepDwords;
-        float acc[MT];
-#pragma unroll
-        for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
-        for (uint32_t c0 = 0; c0 < chunks; c0 += 2) {
-            uint4 nib0[kChunkBlocks], scl0, nib1[kChunkBlocks], scl1;
-            load_tile(tiles + (size_t)c0 * kTileBytes, lane, nib0, scl0);
-            const bool has1 = c0 + 1 < chunks;
-            if (has1) load_tile(tiles + (size_t)(c0 + 1) * kTileBytes, lane, nib1, scl1);
-            tile_accumulate<MT>(nib0, scl0, c0, hp, hb, tok, m_tok, acc);
-            if (has1) tile_accumulate<MT>(nib1, scl1, c0 + 1, hp, hb, tok, m_tok, acc);
-        }
-#pragma unroll
-        for (int t = 0; t < MT; ++t)
-            if (t < m_tok) red[wave][tok[t]][lane] = plan->coef[slot][tok[t]] * acc[t];
+        const uint32_t *xp = hprep + (size_t)slot * hb * kXprepDwords;
+        v = coef * slot_dot(tiles, lane, c, c + 1, 1, xp);
     }
+    red[wave][lane] = v;
+    if (lane == 0) s_tok[wave] = tok;
     __syncthreads();
     const uint32_t row = g * kRowsPerGroup + lane;
-    for (int t = wave; t < (int)m; t += 4) {
-        const float p = (red[0][t][lane] + red[1][t][lane]) + (red[2][t][lane] + red[3][t][lane]);
-        partial[((size_t)sg * kMaxTokens + t) * H + row] = p;
+    for (int t = wave; t < (int)m; t += waves) {
+        float p = 0.0f;
+        for (int w = 0; w < waves; ++w)
+            if (s_tok[w] == t) p += red[w][lane];
+        store_coherent(&partial[((size_t)sg * kMaxTokens + t) * H + row], p);
     }
+    wait_own_stores();
     __syncthreads();
-    if (threadIdx.x == 0) {
-        __threadfence();
-        const uint32_t prev = atomicAdd(&counters[g], 1u);
-        s_last = (prev == (uint32_t)n_sg - 1) ? 1 : 0;
-    }
+    if (threadIdx.x == 0) s_last = (counter_arrive(&counters[g]) == (uint32_t)n_sg - 1) ? 1 : 0;
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
-    for (int t = wave; t < (int)m; t += 4) {
+    for (int t = wave; t < (int)m; t += waves) {
         float s = 0.0f;
-        for (int q = 0; q < n_sg; ++q)
-            s += __builtin_nontemporal_load(&partial[((size_t)q * kMaxTokens + t) * H + row]);
+        for (int q = 0; q < n_sg; ++q) s += load_coherent(&partial[((size_t)q * kMaxTokens + t) * H + row]);
         const size_t o = (size_t)t * H + row;
         out[o] = resid ? resid[o] + s : s;
     }
-    if (threadIdx.x == 0) counters[g] = 0u;
+    if (threadIdx.x == 0) counter_reset(&counters[g]);
 }
 
 hipError_t launch_down(hipStream_t s, const LayerDev &L, uint32_t m, Scratch &sc,
                        const Plan *plan, const float *resid, float *out) {
-    const uint32_t max_slots = m * kTopK + 1;
-    dim3 grid(L.hidden / kRowsPerGroup, (max_slots + 3) / 4), block(4 * kWave);
-    uint32_t *counters = sc.counters + 64;  // counters[0..64) belong to the route kernel
-#define TQF_DOWN(MT)                                                                          \
-    hipLaunchKernelGGL(down_kernel<MT>, grid, block, 0, s, L, plan, sc.hprep, sc.partial,     \
-                       counters, resid, out, m)
-    if (m <= 1) TQF_DOWN(1);
-    else if (m <= 2) TQF_DOWN(2);
-    else if (m <= 4) TQF_DOWN(4);
-    else TQF_DOWN(8);
-#undef TQF_DOWN
+    const uint32_t chunks = L.width / kChunkCols;
+    uint32_t spg = 16 / chunks;  // at most 16 wavefronts per workgroup
+    if (spg > m) spg = m;        // M slots per group: 9 groups for any M
+    if (spg == 0) spg = 1;
+    const uint32_t n_sg = (m * (kTopK + 1) + spg - 1) / spg;
+    dim3 grid(L.hidden / kRowsPerGroup, n_sg), block(spg * chunks * kWave);
+    hipLaunchKernelGGL(down_kernel, grid, block, 0, s, L, plan, sc.hprep, sc.partial,
+                       sc.counters + kCounterDown, resid, out, m, spg);
     return hipGetLastError();
 }
 
