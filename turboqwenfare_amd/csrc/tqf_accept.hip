@@ -48,19 +48,21 @@ struct AccLayout {
     size_t off_max, off_av, off_ai, off_sum, off_w, off_misc, total;
 };
 
-// misc: [0] i*, [1] counter (sums), [2] counter (residual), [3] counter (stats)
+// misc (first 64 bytes, the same for every k and vocab so that the counters
+// are never overlaid by another call's partials): [0] i*, [1] counter (sums),
+// [2] counter (residual), [3] counter (stats).  Partials follow.
 __host__ __device__ inline AccLayout acc_layout(uint32_t k, uint32_t vocab) {
     AccLayout L;
     L.rows = 2 * k + 1;
     L.nch = (vocab + kAccChunk - 1) / kAccChunk;
     const size_t n = (size_t)L.rows * L.nch;
-    L.off_max = 0;
+    L.off_misc = 0;
+    L.off_max = 64;
     L.off_av = L.off_max + n * 4;
     L.off_ai = L.off_av + n * 4;
     L.off_sum = (L.off_ai + n * 4 + 7) & ~(size_t)7;
     L.off_w = L.off_sum + n * 8;
-    L.off_misc = L.off_w + (size_t)L.nch * 8;
-    L.total = L.off_misc + 64;
+    L.total = L.off_w + (size_t)L.nch * 8;
     return L;
 }
 

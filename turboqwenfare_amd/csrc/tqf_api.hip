@@ -139,24 +139,22 @@ int32_t ensure_moe_scratch(tqf_hip_ctx *ctx, uint32_t hidden, uint32_t width, ui
     (void)hipFree(sc.logits);
     (void)hipFree(sc.plan);
     (void)hipFree(sc.partial);
-    (void)hipFree(sc.gu_partial);
     (void)hipFree(sc.counters);
     sc.xprep = sc.hprep = sc.counters = nullptr;
-    sc.logits = sc.partial = sc.gu_partial = nullptr;
+    sc.logits = sc.partial = nullptr;
     sc.plan = nullptr;
     sc.hidden = sc.width = sc.experts = 0;
-    const size_t xprep = (size_t)kMaxTokens * (hidden / 32) * kXprepDwords * 4;
-    const size_t hprep = (size_t)kMaxSlots * (width / 32) * kXprepDwords * 4;
+    // padding records stay zero: kernels only write real blocks
+    const size_t xprep = (size_t)kMaxTokens * padded_blocks(hidden / 32) * kXprepDwords * 4;
+    const size_t hprep = (size_t)kMaxSlots * padded_blocks(width / 32) * kXprepDwords * 4;
     const size_t logits = (size_t)kMaxTokens * (experts + 1) * 4;
     const size_t partial = (size_t)kMaxSlots * kMaxTokens * hidden * 4;
-    const size_t gu_partial = (size_t)kMaxSlots * (width / 64) * 4 * 2 * kWave * 4;
-    const size_t counters = counter_count(hidden, width) * 4;
+    const size_t counters = counter_count(hidden) * 4;
     TQF_HIP(ctx, hipMalloc(&sc.xprep, xprep));
     TQF_HIP(ctx, hipMalloc(&sc.hprep, hprep));
     TQF_HIP(ctx, hipMalloc(&sc.logits, logits));
     TQF_HIP(ctx, hipMalloc(&sc.plan, sizeof(Plan)));
     TQF_HIP(ctx, hipMalloc(&sc.partial, partial));
-    TQF_HIP(ctx, hipMalloc(&sc.gu_partial, gu_partial));
     TQF_HIP(ctx, hipMalloc(&sc.counters, counters));
     TQF_HIP(ctx, hipMemset(sc.xprep, 0, xprep));
     TQF_HIP(ctx, hipMemset(sc.hprep, 0, hprep));
@@ -266,14 +264,14 @@ int32_t enqueue_layer(tqf_hip_ctx *ctx, const LayerDev &L, const float *h, const
     }
     {
         Prof p(ctx);
-        hipError_t e = launch_gate_up(ctx->stream, L, m, sc, sc.plan, sc.xprep);
+        hipError_t e = launch_gate_up(ctx->stream, L, m * (kTopK + 1), sc.plan, sc.xprep, sc.hprep);
         if (e != hipSuccess) return hip_fail(ctx, "gate/up kernel launch", e);
         p.end(TQF_HIP_KERNEL_GATE_UP, m * H * 4 + pairs * F * 4, 2 * q4_bytes(L.width, L.hidden),
               sc.plan);
     }
     {
         Prof p(ctx);
-        hipError_t e = launch_down(ctx->stream, L, m, sc, sc.plan, resid, out);
+        hipError_t e = launch_down(ctx->stream, L, m, m * (kTopK + 1), sc, sc.plan, sc.hprep, resid, out);
         if (e != hipSuccess) return hip_fail(ctx, "down kernel launch", e);
         p.end(TQF_HIP_KERNEL_DOWN, pairs * F * 4 + m * H * 4 * (resid ? 2 : 1),
               q4_bytes(L.hidden, L.width), sc.plan);
@@ -410,7 +408,6 @@ extern "C" int32_t tqf_hip_destroy(tqf_hip_ctx *ctx) {
     (void)hipFree(sc.logits);
     (void)hipFree(sc.plan);
     (void)hipFree(sc.partial);
-    (void)hipFree(sc.gu_partial);
     (void)hipFree(sc.counters);
     (void)hipFree(sc.accept);
     (void)hipFree(ctx->d_stage);
@@ -487,13 +484,13 @@ extern "C" int32_t tqf_hip_memcpy_d2h(tqf_hip_ctx *ctx, void *dst, const void *s
 // ===========================================================================
 extern "C" uint64_t tqf_hip_weights_bytes_for(uint32_t rows, uint32_t cols) {
     if (rows == 0 || cols == 0 || cols % 32) return 0;
-    return align_up(tile_bytes(matrix_dims(rows, cols)), kAlign) + kAlign;
+    return align_up(layout_bytes(matrix_dims(rows, cols)), kAlign) + kAlign;
 }
 
 namespace {
 int32_t weights_alloc(tqf_hip_ctx *ctx, uint32_t rows, uint32_t cols, tqf_hip_weights **out) {
     const MatrixDims d = matrix_dims(rows, cols);
-    const size_t bytes = tile_bytes(d);
+    const size_t bytes = layout_bytes(d);
     void *tiles = nullptr, *self = nullptr;
     hipError_t e = arena_alloc(ctx, bytes, &tiles);
     if (e != hipSuccess) return fail(ctx, TQF_HIP_ERR_NOMEM, "weights allocation failed");
@@ -604,14 +601,13 @@ extern "C" int32_t tqf_hip_weights_download(tqf_hip_ctx *ctx, const tqf_hip_weig
     std::vector<uint8_t> tiles(w->bytes);
     TQF_HIP(ctx, hipMemcpyAsync(tiles.data(), w->tiles, w->bytes, hipMemcpyDeviceToHost, ctx->stream));
     TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    const uint8_t *scales = tiles.data() + nibble_plane_bytes(d);
+    const size_t bp = d.blocks_padded;
     for (uint32_t r = 0; r < d.rows; ++r) {
-        const uint32_t g = r / kRowsPerGroup, lane = r % kRowsPerGroup;
         for (uint32_t b = 0; b < blocks; ++b) {
-            const uint8_t *tile = tiles.data() + ((size_t)g * d.chunks + b / kChunkBlocks) * kTileBytes;
-            const uint32_t j = b % kChunkBlocks;
             uint8_t *dst = q4_0 + ((size_t)r * blocks + b) * kQ4Block;
-            std::memcpy(dst, tile + kTileNibbleBytes + lane * 16 + j * 2, 2);
-            std::memcpy(dst + 2, tile + j * 1024 + lane * 16, 16);
+            std::memcpy(dst, scales + ((r / 8) * bp + b) * 16 + (r % 8) * 2, 2);
+            std::memcpy(dst + 2, tiles.data() + (r * bp + b) * 16, 16);
         }
     }
     return TQF_HIP_OK;
@@ -662,7 +658,7 @@ extern "C" int32_t tqf_hip_tensor_free(tqf_hip_ctx *ctx, tqf_hip_tensor *t) {
 namespace {
 int32_t gemv_enqueue(tqf_hip_ctx *ctx, const uint8_t *const *table, uint32_t count,
                      const MatrixDims &d, const float *d_x, uint32_t m, float *d_y) {
-    const uint32_t bp = d.chunks * kChunkBlocks;
+    const uint32_t bp = d.blocks_padded;
     const size_t xb = (size_t)m * bp * kXprepDwords * 4;
     if (!ctx->d_gemv_xprep || ctx->gemv_xprep_bytes < xb) {
         TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -742,8 +738,8 @@ extern "C" int32_t tqf_hip_expert_forward(tqf_hip_ctx *ctx, const tqf_hip_weight
     const uint32_t F = gate->dims.rows, H = gate->dims.cols;
     if (up->dims.rows != F || up->dims.cols != H || down->dims.rows != H || down->dims.cols != F)
         return fail(ctx, TQF_HIP_ERR_INVALID, "expert shapes: gate/up [width x hidden], down [hidden x width]");
-    if (H % 256 || F % 256)
-        return fail(ctx, TQF_HIP_ERR_INVALID, "expert hidden and width must be multiples of 256");
+    if (H % 256 || F % 256 || H > 2048 || F > 2048)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "expert hidden and width must be multiples of 256, at most 2048");
     if (int32_t rc = ensure_moe_scratch(ctx, H, F, 0)) return rc;
     const size_t xb = (size_t)m * H * 4;
     if (int32_t rc = ensure_stage(ctx, 2 * align_up(xb, kAlign))) return rc;
@@ -756,9 +752,8 @@ extern "C" int32_t tqf_hip_expert_forward(tqf_hip_ctx *ctx, const tqf_hip_weight
     plan.n_union = 0;
     plan.m = (int32_t)m;
     for (uint32_t t = 0; t < m; ++t) {
+        plan.slots[t] = SlotRec{{gate->tiles, up->tiles, down->tiles}, (int32_t)t, 1.0f};
         plan.slot_expert[t] = 0;
-        plan.slot_token[t] = (int32_t)t;
-        plan.slot_coef[t] = 1.0f;
     }
     TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
     drop_graphs(ctx);
@@ -767,9 +762,11 @@ extern "C" int32_t tqf_hip_expert_forward(tqf_hip_ctx *ctx, const tqf_hip_weight
     TQF_HIP(ctx, hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream));
     LayerDev L{nullptr, nullptr, ctx->d_adhoc_mats, 0, H, F};
     Scratch &sc = ctx->scratch;
-    hipError_t e = launch_prep(ctx->stream, dx, m, H, H / 32, sc.xprep);
-    if (e == hipSuccess) e = launch_gate_up(ctx->stream, L, m, sc, ctx->d_adhoc_plan, sc.xprep);
-    if (e == hipSuccess) e = launch_down(ctx->stream, L, m, sc, ctx->d_adhoc_plan, nullptr, dy);
+    hipError_t e = launch_prep(ctx->stream, dx, m, H, padded_blocks(H / 32), sc.xprep);
+    if (e == hipSuccess)
+        e = launch_gate_up(ctx->stream, L, m, ctx->d_adhoc_plan, sc.xprep, sc.hprep);
+    if (e == hipSuccess)
+        e = launch_down(ctx->stream, L, m, m, sc, ctx->d_adhoc_plan, sc.hprep, nullptr, dy);
     if (e != hipSuccess) return hip_fail(ctx, "expert kernels", e);
     TQF_HIP(ctx, hipMemcpyAsync(y, dy, xb, hipMemcpyDeviceToHost, ctx->stream));
     TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -787,7 +784,8 @@ extern "C" int32_t tqf_hip_moe_layer_prepare(tqf_hip_ctx *ctx, const tqf_hip_moe
     const uint32_t E = mw->n_experts, H = mw->hidden, F = mw->width;
     if (E != 256) return fail(ctx, TQF_HIP_ERR_INVALID, "router requires n_experts == 256 (experts/mod.rs:135)");
     if (H == 0 || H % 256 || H > 2048) return fail(ctx, TQF_HIP_ERR_INVALID, "hidden must be a multiple of 256, at most 2048");
-    if (F == 0 || F % 256) return fail(ctx, TQF_HIP_ERR_INVALID, "width must be a multiple of 256");
+    if (F == 0 || F % 256 || F > 2048)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "width must be a multiple of 256, at most 2048");
     if (!mw->router || mw->router->count != (size_t)E * H)
         return fail(ctx, TQF_HIP_ERR_INVALID, "router must be f32 [n_experts x hidden]");
     if (!mw->shared_input_gate || mw->shared_input_gate->count != H)

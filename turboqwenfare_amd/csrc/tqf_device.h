@@ -198,15 +198,140 @@ __device__ __forceinline__ float q4_block_dot(const uint4 w, const uint32_t *__r
     return (float)v * __uint_as_float(xp[27]);
 }
 
-// Scale j (0..7) of a tile's per-lane scale vector.
-__device__ __forceinline__ float tile_scale(const uint4 s, int j) {
+// ---- transpose-reduce: per-lane partial sums of NL rows -> one row per lane
+// Lanes are grouped LPR to a matrix row (LPR in {16, 32, 64}); every lane
+// holds NL partials.  Each halving stage pairs value i with value i + K/2;
+// lanes whose stage bit is set keep the second member and add their
+// partner's copy of it, so K halves per stage and no work is wasted.  The
+// cross-row stages use gfx950's v_permlane32_swap / v_permlane16_swap, the
+// in-row stages DPP mirrors.  Result: the sum over the group's LPR lanes of
+// value index (lane % LPR) >> log2(LPR / NL), replicated LPR / NL times.
+constexpr int kDppQuadRev = 0x1B;  // quad_perm [3,2,1,0]
+
+template <int CTRL, int K>
+__device__ __forceinline__ void dpp_stage(float *v, bool hi) {
+    if constexpr (K >= 2) {
+#pragma unroll
+        for (int i = 0; i < K / 2; ++i) {
+            const float a = v[i], b = v[i + K / 2];
+            v[i] = (hi ? b : a) + dpp_f<CTRL>(hi ? a : b);
+        }
+    } else {
+        v[0] = v[0] + dpp_f<CTRL>(v[0]);
+    }
+}
+
+template <int K>
+__device__ __forceinline__ void permlane32_stage(float *v) {
+    if constexpr (K >= 2) {
+#pragma unroll
+        for (int i = 0; i < K / 2; ++i) {
+            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]),
+                                                            __float_as_uint(v[i + K / 2]), false, false);
+            v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[0]), __float_as_uint(v[0]),
+                                                        false, false);
+        v[0] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+}
+
+template <int K>
+__device__ __forceinline__ void permlane16_stage(float *v) {
+    if constexpr (K >= 2) {
+#pragma unroll
+        for (int i = 0; i < K / 2; ++i) {
+            const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]),
+                                                            __float_as_uint(v[i + K / 2]), false, false);
+            v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
+    } else {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[0]), __float_as_uint(v[0]),
+                                                        false, false);
+        v[0] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+}
+
+constexpr int half_or_one(int k) { return k > 1 ? k / 2 : 1; }
+constexpr int ilog2(int v) { return v <= 1 ? 0 : 1 + ilog2(v / 2); }
+
+template <int LPR, int NL>
+__device__ __forceinline__ float transpose_reduce(float (&v)[NL]) {
+    static_assert(LPR == 16 || LPR == 32 || LPR == 64, "lanes per row");
+    static_assert(NL >= 1 && NL <= LPR && (NL & (NL - 1)) == 0, "values per lane");
+    const int lane = threadIdx.x & 63;
+    constexpr int K0 = NL;
+    if constexpr (LPR == 64) permlane32_stage<K0>(v);
+    constexpr int K1 = LPR == 64 ? half_or_one(K0) : K0;
+    if constexpr (LPR >= 32) permlane16_stage<K1>(v);
+    constexpr int K2 = LPR >= 32 ? half_or_one(K1) : K1;
+    dpp_stage<kDppMirror, K2>(v, lane & 8);
+    constexpr int K3 = half_or_one(K2);
+    dpp_stage<kDppHalfMirror, K3>(v, lane & 4);
+    constexpr int K4 = half_or_one(K3);
+    dpp_stage<kDppQuadRev, K4>(v, lane & 2);
+    constexpr int K5 = half_or_one(K4);
+    dpp_stage<kDppXor1, K5>(v, lane & 1);
+    return v[0];
+}
+// Value index a lane holds after transpose_reduce, and whether it is the
+// first of the replicated copies.
+template <int LPR, int NL>
+__device__ __forceinline__ int reduced_index(int lane) {
+    return (lane % LPR) >> (ilog2(LPR) - ilog2(NL));
+}
+template <int LPR, int NL>
+__device__ __forceinline__ bool reduced_first_copy(int lane) {
+    return ((lane % LPR) & ((LPR / NL) - 1)) == 0;
+}
+
+// ---- row-lane matrix access ------------------------------------------------
+struct RowLane {
+    const uint8_t *nib;    // nibble plane
+    const uint8_t *scale;  // scale plane
+    uint32_t bp;           // padded blocks per row
+};
+__device__ __forceinline__ RowLane row_lane(const uint8_t *base, uint32_t rows_padded, uint32_t bp) {
+    RowLane r;
+    r.nib = base;
+    r.scale = base + (size_t)rows_padded * bp * 16;
+    r.bp = bp;
+    return r;
+}
+// Loads from device memory through global (not flat) instructions: the
+// matrix pointers come from tables in memory, which the compiler cannot
+// prove are global.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_global_u4(const void *p) {
+    const u32x4 v = *(const __attribute__((address_space(1))) u32x4 *)(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint4 load_nibbles(const RowLane &m, uint32_t row, uint32_t block) {
+    return load_global_u4(m.nib + ((size_t)row * m.bp + block) * 16);
+}
+// Scales of rows 8*octet .. 8*octet+7 of one block.
+__device__ __forceinline__ uint4 load_scales(const RowLane &m, uint32_t octet, uint32_t block) {
+    return load_global_u4(m.scale + ((size_t)octet * m.bp + block) * 16);
+}
+// One xprep record (28 used dwords) into registers.
+__device__ __forceinline__ void load_xrec(const uint32_t *rec, uint32_t (&x)[28]) {
+#pragma unroll
+    for (int i = 0; i < 7; ++i) {
+        const uint4 q = load_global_u4(rec + 4 * i);
+        x[4 * i + 0] = q.x;
+        x[4 * i + 1] = q.y;
+        x[4 * i + 2] = q.z;
+        x[4 * i + 3] = q.w;
+    }
+}
+
+// Scale j (0..7) of a per-lane vector of eight f16 scales.
+__device__ __forceinline__ float octet_scale(const uint4 s, int j) {
     const uint32_t sv[4] = {s.x, s.y, s.z, s.w};
     const uint32_t word = sv[j >> 1];
     return f16_to_f32((j & 1) ? (word >> 16) : word);
 }
 
-__device__ __forceinline__ uint4 load_u4(const uint8_t *p) {
-    return *reinterpret_cast<const uint4 *>(p);
-}
 
 }  // namespace tqf

@@ -1,18 +1,19 @@
 // tqf_internal.h -- shared definitions of the gfx950 HIP backend (not ABI).
 //
-// Device layout of one Q4_0 matrix ("tile layout").  A GGML Q4_0 matrix is
-// rows x B blocks of 18 bytes (f16 scale d, 16 nibble bytes qs; element j of
-// a block is (qs[j] & 15) - 8, element j + 16 is (qs[j] >> 4) - 8;
-// format/quant/dequant.rs:110-123).  The backend stores it as
-//   row groups of 64 rows  x  chunks of 8 blocks (256 columns)
-// and each (group, chunk) tile is 9216 contiguous bytes:
-//   bytes [j*1024 + lane*16, +16)  qs of block j of row (group*64 + lane)
-//   bytes [8192 + lane*16, +16)    the 8 f16 scales of that row's blocks
-// so lane L of a 64-wide wavefront reads its row's 16 nibble bytes with one
-// 128-bit load and a wavefront reads 1 KiB contiguously.  Rows are padded to
-// 64 and blocks to 8 with zero scales (their products are exactly zero).  The
-// bytes are the GGML bytes moved, never re-encoded: the repack is lossless
-// and tqf_hip_weights_download() inverts it.
+// Device layout of one Q4_0 matrix ("row-lane layout").  A GGML Q4_0 matrix
+// is rows x B blocks of 18 bytes (f16 scale d, 16 nibble bytes qs; element j
+// of a block is (qs[j] & 15) - 8, element j + 16 is (qs[j] >> 4) - 8;
+// format/quant/dequant.rs:110-123).  The backend pads B to Bp (16, 32 or a
+// multiple of 64) and the rows to a multiple of 64, and stores
+//   nibble plane  [Rp rows][Bp blocks][16 bytes]              (row-major)
+//   scale plane   [Rp/8 row octets][Bp blocks][8 rows x f16]
+// A row's blocks are spread across lanes: lane l of a 64-wide wavefront owns
+// block (l mod LPR) (LPR = min(Bp, 64) lanes per row, Bp/LPR blocks per
+// lane), so one 128-bit load per lane reads 64/LPR whole rows = 1 KiB
+// contiguously, and one 16-byte scale load gives a lane the scales of eight
+// rows.  Padding has zero scale (products exactly zero).  The bytes are the
+// GGML bytes moved, never re-encoded: the repack is lossless and
+// tqf_hip_weights_download() inverts it.
 //
 // Activation prep ("xprep").  A Q4_0 dot is evaluated with exact integer
 // arithmetic: each 32-element activation block is written as
@@ -41,11 +42,7 @@
 namespace tqf {
 
 constexpr int kWave = 64;
-constexpr int kRowsPerGroup = 64;
-constexpr int kChunkBlocks = 8;
-constexpr int kChunkCols = kChunkBlocks * 32;  // 256
-constexpr int kTileNibbleBytes = kChunkBlocks * kRowsPerGroup * 16;  // 8192
-constexpr int kTileBytes = kTileNibbleBytes + kRowsPerGroup * 16;    // 9216
+constexpr int kRowsPerGroup = 64;  // row padding unit
 constexpr int kXprepDwords = 32;
 constexpr int kTopK = TQF_HIP_TOP_K;
 constexpr int kMaxTokens = TQF_HIP_MAX_TOKENS;
@@ -57,20 +54,33 @@ constexpr int kQ4Block = 18;
 
 struct MatrixDims {
     uint32_t rows, cols;
-    uint32_t groups;  // ceil(rows / 64)
-    uint32_t chunks;  // ceil(cols / 256)
+    uint32_t rows_padded;    // multiple of 64
+    uint32_t blocks;         // cols / 32
+    uint32_t blocks_padded;  // Bp: 16, 32 or a multiple of 64
+    uint32_t lpr;            // lanes per row: min(Bp, 64)
 };
+
+inline uint32_t padded_blocks(uint32_t blocks) {
+    if (blocks <= 16) return 16;
+    if (blocks <= 32) return 32;
+    return (blocks + 63) / 64 * 64;
+}
 
 inline MatrixDims matrix_dims(uint32_t rows, uint32_t cols) {
     MatrixDims d;
     d.rows = rows;
     d.cols = cols;
-    d.groups = (rows + kRowsPerGroup - 1) / kRowsPerGroup;
-    d.chunks = (cols + kChunkCols - 1) / kChunkCols;
+    d.rows_padded = (rows + kRowsPerGroup - 1) / kRowsPerGroup * kRowsPerGroup;
+    d.blocks = cols / 32;
+    d.blocks_padded = padded_blocks(d.blocks);
+    d.lpr = d.blocks_padded < 64 ? d.blocks_padded : 64;
     return d;
 }
-inline size_t tile_bytes(const MatrixDims &d) {
-    return (size_t)d.groups * d.chunks * kTileBytes;
+inline size_t nibble_plane_bytes(const MatrixDims &d) {
+    return (size_t)d.rows_padded * d.blocks_padded * 16;
+}
+inline size_t layout_bytes(const MatrixDims &d) {
+    return (size_t)d.rows_padded * d.blocks_padded * kQ4Block;
 }
 
 // Route plan written by the route kernel and read by the expert kernels.
@@ -81,14 +91,31 @@ inline size_t tile_bytes(const MatrixDims &d) {
 // experts/mod.rs:268-275 BatchExpertPlan), one slot per token routed to it
 // (coefficient = that token's route weight).  Slots of one expert are
 // adjacent, so its second reads come from L2 / Infinity Cache.
+// One pair slot as the expert kernels read it: a single 32-byte scalar load.
+struct SlotRec {
+    const uint8_t *mat[3];  // gate, up, down matrices of the slot's expert
+    int32_t token;          // < 0: no work (routing failed)
+    float coef;
+};
+static_assert(sizeof(SlotRec) == 32, "slot record is one s_load_dwordx8");
+
+#if defined(__HIP_DEVICE_COMPILE__)
+// Reads a slot record with one 32-byte load, ahead of any use of its fields.
+__device__ __forceinline__ SlotRec load_slot(const SlotRec *p) {
+    typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+    const u32x8 v = *reinterpret_cast<const u32x8 *>(p);
+    return __builtin_bit_cast(SlotRec, v);
+}
+#endif
+
 struct Plan {
     int32_t n_slots;  // 9 * M when routing succeeded, 0 otherwise
     int32_t status;   // 0 or TQF_HIP_ERR_ROUTER
     int32_t n_union;  // distinct routed experts (HBM bytes = (n_union + 1) experts)
     int32_t m;
+    int32_t pad[4];
+    SlotRec slots[kMaxSlots];
     int32_t slot_expert[kMaxSlots];  // expert index; n_experts = shared
-    int32_t slot_token[kMaxSlots];
-    float slot_coef[kMaxSlots];
     uint16_t ids[kMaxTokens][kTopK];
     float weights[kMaxTokens][kTopK];
     float gate_logit[kMaxTokens];
@@ -105,12 +132,11 @@ struct LayerDev {
 
 // Per-context device scratch (allocated once, grown on demand).
 struct Scratch {
-    uint32_t *xprep = nullptr;   // [kMaxTokens x hidden/32 x 32]
-    uint32_t *hprep = nullptr;   // [kMaxSlots x kMaxTokens x width/32 x 32]
+    uint32_t *xprep = nullptr;   // [kMaxTokens x padded(hidden/32) x 32]
+    uint32_t *hprep = nullptr;   // [kMaxSlots x padded(width/32) x 32]
     float *logits = nullptr;     // [kMaxTokens x (n_experts + 1)]
     Plan *plan = nullptr;
     float *partial = nullptr;    // [slot groups x kMaxTokens x hidden]
-    float *gu_partial = nullptr; // [kMaxSlots x width/64 x 4 x 2 x 64] split-K gate/up
     uint32_t *counters = nullptr;  // last-arriver counters (see kCounter*)
     void *accept = nullptr;      // acceptance partials
     size_t accept_bytes = 0;
@@ -136,7 +162,7 @@ struct Slab {
 
 struct tqf_hip_weights {
     tqf::MatrixDims dims;
-    uint8_t *tiles;              // device
+    uint8_t *tiles;              // device: nibble plane, then scale plane
     size_t bytes;
     const uint8_t **d_self;      // device: one-entry table {tiles}
 };
@@ -194,20 +220,11 @@ struct tqf_hip_ctx {
 
 namespace tqf {
 
-// Counter array layout: [route (1) | pad | down (hidden/64) | gate/up
-// (kMaxSlots * width/64)].  Every counter returns to zero when its kernel ends.
+// Counter array layout: [route (1) | pad | down (one per row group, at most
+// hidden / 16)].  Every counter returns to zero in the workgroup that
+// finishes its kernel.
 constexpr int kCounterDown = 64;
-inline size_t counter_gate_up_offset(uint32_t hidden) { return kCounterDown + hidden / 64; }
-inline size_t counter_count(uint32_t hidden, uint32_t width) {
-    return counter_gate_up_offset(hidden) + (size_t)kMaxSlots * (width / 64);
-}
-// Split-K factor of the gate/up kernel for M tokens (keeps >= 256 workgroups).
-inline uint32_t gate_up_kparts(uint32_t m, uint32_t hidden) {
-    const uint32_t chunks = hidden / 256;
-    uint32_t kp = m >= 4 ? 1 : (m >= 2 ? 2 : 4);
-    while (kp > 1 && chunks % kp) kp >>= 1;
-    return kp;
-}
+inline size_t counter_count(uint32_t hidden) { return kCounterDown + hidden / 16; }
 
 // ---- launchers (defined in the .hip translation units) -------------------
 // All are asynchronous on ctx->stream and return a hipError_t.
@@ -224,10 +241,15 @@ hipError_t launch_gemv(hipStream_t s, const uint8_t *const *d_tiles, uint32_t co
 hipError_t launch_route(hipStream_t s, const LayerDev &L, const float *h, const float *norm,
                         uint32_t m, Scratch &sc, uint16_t *ids_out, float *w_out,
                         int32_t *status_out);
-hipError_t launch_gate_up(hipStream_t s, const LayerDev &L, uint32_t m, Scratch &sc,
-                          const Plan *plan, const uint32_t *xprep);
-hipError_t launch_down(hipStream_t s, const LayerDev &L, uint32_t m, Scratch &sc,
-                       const Plan *plan, const float *resid, float *out);
+// gate/up needs the gate/up matrices' padded block count (hidden / 32) and the
+// down matrix's (width / 32) in {16, 32, 64}; other shapes return
+// hipErrorInvalidValue (callers validate first).
+// `slots` is the number of pair slots the grid covers (9 M for a MoE layer);
+// a slot whose record has token < 0 does no work.
+hipError_t launch_gate_up(hipStream_t s, const LayerDev &L, uint32_t slots, const Plan *plan,
+                          const uint32_t *xprep, uint32_t *hprep);
+hipError_t launch_down(hipStream_t s, const LayerDev &L, uint32_t m, uint32_t slots, Scratch &sc,
+                       const Plan *plan, const uint32_t *hprep, const float *resid, float *out);
 size_t accept_scratch_bytes(uint32_t k, uint32_t vocab);
 hipError_t launch_accept(hipStream_t s, const float *target, const float *draft,
                          const int32_t *dtok, uint32_t k, uint32_t vocab, float temperature,

@@ -1,12 +1,12 @@
-// tqf_q4.hip -- Q4_0 tile layout, activation prep, GEMV and the three MoE
+// tqf_q4.hip -- Q4_0 row-lane layout, activation prep, GEMV and the three MoE
 // layer kernels (route, gate/up + SwiGLU, down + weighted combine) for gfx950.
 //
-// The matrix tile layout and the integer-dot activation format are described
-// in tqf_internal.h.  Every kernel here is HBM-bound: the weight bytes are
-// read exactly once with 128-bit loads (one row per lane, 1 KiB per
-// wavefront load), all of a wavefront's loads are issued before any math,
-// and partial sums are combined through LDS in a fixed order, so results are
-// deterministic run to run.
+// The matrix layout and the integer-dot activation format are described in
+// tqf_internal.h.  Every kernel here is HBM-bound: the weight bytes are read
+// exactly once with 128-bit loads (a row's blocks spread over the lanes, 1 KiB
+// per wavefront load), all of a wavefront's loads are issued before any
+// math, and partial sums are combined in a fixed order (DPP / permlane
+// transposes, then LDS), so results are deterministic run to run.
 #include <hip/hip_runtime.h>
 
 #include "tqf_device.h"
@@ -15,34 +15,32 @@
 namespace tqf {
 
 // ---------------------------------------------------------------------------
-// Repack: GGML Q4_0 (rows x B x 18 bytes) -> tile layout.  One thread per
+// Repack: GGML Q4_0 (rows x B x 18 bytes) -> row-lane layout.  One thread per
 // block; the destination was zero-filled (padding rows/blocks keep scale 0).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__ aos,
                                                      uint32_t rows, uint32_t blocks,
-                                                     uint32_t chunks,
-                                                     uint8_t *__restrict__ tiles) {
+                                                     uint32_t rows_padded, uint32_t bp,
+                                                     uint8_t *__restrict__ dst) {
     const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (uint64_t)rows * blocks) return;
     const uint32_t r = (uint32_t)(idx / blocks), b = (uint32_t)(idx % blocks);
     const uint8_t *src = aos + idx * kQ4Block;
-    uint8_t *tile = tiles + ((size_t)(r / kRowsPerGroup) * chunks + b / kChunkBlocks) * kTileBytes;
-    const uint32_t lane = r % kRowsPerGroup, j = b % kChunkBlocks;
-    uint8_t *nib = tile + j * 1024 + lane * 16;
+    uint8_t *nib = dst + ((size_t)r * bp + b) * 16;
 #pragma unroll
     for (int i = 0; i < 16; ++i) nib[i] = src[2 + i];
-    uint8_t *sc = tile + kTileNibbleBytes + lane * 16 + j * 2;
+    uint8_t *sc = dst + (size_t)rows_padded * bp * 16 + ((size_t)(r / 8) * bp + b) * 16 + (r % 8) * 2;
     sc[0] = src[0];
     sc[1] = src[1];
 }
 
 hipError_t launch_repack(hipStream_t s, const uint8_t *d_aos, const MatrixDims &d,
-                         uint8_t *tiles) {
-    const uint64_t n = (uint64_t)d.rows * (d.cols / 32);
+                         uint8_t *dst) {
+    const uint64_t n = (uint64_t)d.rows * d.blocks;
     if (n == 0) return hipSuccess;
     const uint32_t grid = (uint32_t)((n + 255) / 256);
-    hipLaunchKernelGGL(repack_kernel, dim3(grid), dim3(256), 0, s, d_aos, d.rows, d.cols / 32,
-                       d.chunks, tiles);
+    hipLaunchKernelGGL(repack_kernel, dim3(grid), dim3(256), 0, s, d_aos, d.rows, d.blocks,
+                       d.rows_padded, d.blocks_padded, dst);
     return hipGetLastError();
 }
 
@@ -73,90 +71,86 @@ hipError_t launch_prep(hipStream_t s, const float *x, uint32_t m, uint32_t cols,
 }
 
 // ---------------------------------------------------------------------------
-// Shared wavefront body: one tile (64 rows x 8 blocks) of one matrix against
-// up to MT tokens.  acc[t] accumulates for token tok[t] (t < m_tok).
+// Standalone GEMV / small-M GEMM: y[mat][t][row] for `count` matrices of one
+// shape.  Grid (row groups, count), four wavefronts per workgroup.  Lane
+// group j (LPR lanes) of a wavefront owns NL consecutive rows; lane b of the
+// group reads block b (+ LPR, + 2 LPR, ... for long rows) of each of them, so
+// one wavefront load covers 64/LPR rows with 16 bytes per lane.  Every load
+// of a chunk is issued before any arithmetic; the row sums come out of
+// transpose_reduce, one row per lane.
 // ---------------------------------------------------------------------------
-template <int MT>
-__device__ __forceinline__ void tile_accumulate(const uint4 (&nib)[kChunkBlocks], const uint4 scl,
-                                                uint32_t chunk, const uint32_t *__restrict__ xprep,
-                                                uint32_t blocks_per_token,
-                                                const int (&tok)[MT], int m_tok,
-                                                float (&acc)[MT]) {
+constexpr int kGemvWaves = 4;
+
+template <int LPR, int NL, int MT>
+__global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(
+    const uint8_t *const *__restrict__ tables, MatrixDims d, const uint32_t *__restrict__ xprep,
+    uint32_t m, float *__restrict__ y) {
+    constexpr int G = kWave / LPR;
+    constexpr int RW = NL * G;  // rows per wavefront
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int lane = threadIdx.x % kWave;
+    const uint32_t j = (uint32_t)lane / LPR, b = (uint32_t)lane % LPR;
+    const uint32_t mat = blockIdx.y;
+    const uint32_t r0 = (blockIdx.x * kGemvWaves + wave) * RW;
+    if (r0 >= d.rows_padded) return;
+    const RowLane W = row_lane(tables[mat], d.rows_padded, d.blocks_padded);
+    const uint32_t rl = r0 + j * NL;
+    float acc[MT][NL];
 #pragma unroll
-    for (int j = 0; j < kChunkBlocks; ++j) {
-        const float d = tile_scale(scl, j);
-        const uint32_t kb = chunk * kChunkBlocks + j;
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int n = 0; n < NL; ++n) acc[t][n] = 0.0f;
+    const uint32_t chunks = d.blocks_padded / LPR;
+    for (uint32_t c = 0; c < chunks; ++c) {
+        const uint32_t blk = c * LPR + b;
+        uint4 nib[NL], sc[NL / 8];
+#pragma unroll
+        for (int n = 0; n < NL; ++n) nib[n] = load_nibbles(W, rl + n, blk);
+#pragma unroll
+        for (int o = 0; o < NL / 8; ++o) sc[o] = load_scales(W, rl / 8 + o, blk);
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-            if (t < m_tok) {
-                const uint32_t *xp =
-                    xprep + ((size_t)tok[t] * blocks_per_token + kb) * kXprepDwords;
-                acc[t] = fmaf(d, q4_block_dot(nib[j], xp), acc[t]);
+            if (t < (int)m) {
+                uint32_t x[28];
+                load_xrec(xprep + ((size_t)t * d.blocks_padded + blk) * kXprepDwords, x);
+#pragma unroll
+                for (int n = 0; n < NL; ++n)
+                    acc[t][n] = fmaf(octet_scale(sc[n / 8], n % 8), q4_block_dot(nib[n], x), acc[t][n]);
             }
+        }
+    }
+    const uint32_t row = rl + reduced_index<LPR, NL>(lane);
+    const bool writer = reduced_first_copy<LPR, NL>(lane) && row < d.rows;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        if (t < (int)m) {
+            const float s = transpose_reduce<LPR, NL>(acc[t]);
+            if (writer) y[((size_t)mat * m + t) * d.rows + row] = s;
         }
     }
 }
 
-__device__ __forceinline__ void load_tile(const uint8_t *tile, int lane,
-                                          uint4 (&nib)[kChunkBlocks], uint4 &scl) {
-    const uint8_t *p = tile + lane * 16;
-#pragma unroll
-    for (int j = 0; j < kChunkBlocks; ++j) nib[j] = load_u4(p + j * 1024);
-    scl = load_u4(p + kTileNibbleBytes);
-}
-
-// ---------------------------------------------------------------------------
-// Standalone GEMV / small-M GEMM: y[mat][t][row] for `count` matrices of one
-// shape.  Grid (row groups, count); block = W wavefronts, wavefront w takes
-// chunks w, w + W, ...; partials meet in LDS and are summed in wave order.
-// ---------------------------------------------------------------------------
-template <int MT>
-__global__ __launch_bounds__(512) void gemv_kernel(const uint8_t *const *__restrict__ tables,
-                                                   MatrixDims d,
-                                                   const uint32_t *__restrict__ xprep,
-                                                   uint32_t m, float *__restrict__ y) {
-    __shared__ float red[8][MT][kWave];
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int lane = threadIdx.x % kWave;
-    const int waves = blockDim.x / kWave;
-    const uint32_t g = blockIdx.x, mat = blockIdx.y;
-    const uint8_t *tiles = tables[mat];
-    const uint32_t bpt = d.chunks * kChunkBlocks;
-    int tok[MT];
-#pragma unroll
-    for (int t = 0; t < MT; ++t) tok[t] = t;
-    float acc[MT];
-#pragma unroll
-    for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
-    for (uint32_t c = wave; c < d.chunks; c += waves) {
-        uint4 nib[kChunkBlocks], scl;
-        load_tile(tiles + ((size_t)g * d.chunks + c) * kTileBytes, lane, nib, scl);
-        tile_accumulate<MT>(nib, scl, c, xprep, bpt, tok, (int)m, acc);
-    }
-#pragma unroll
-    for (int t = 0; t < MT; ++t) red[wave][t][lane] = acc[t];
-    __syncthreads();
-    const uint32_t row = g * kRowsPerGroup + lane;
-    for (int t = wave; t < (int)m; t += waves) {
-        float s = red[0][t][lane];
-        for (int w = 1; w < waves; ++w) s += red[w][t][lane];
-        if (row < d.rows) y[((size_t)mat * m + t) * d.rows + row] = s;
-    }
-}
-
-hipError_t launch_gemv(hipStream_t s, const uint8_t *const *d_tiles, uint32_t count,
-                       const MatrixDims &d, const uint32_t *xprep, uint32_t m, float *y) {
-    const uint32_t waves = d.chunks < 8 ? d.chunks : 8;
-    dim3 grid(d.groups, count), block(waves * kWave);
-    if (m <= 1)
-        hipLaunchKernelGGL(gemv_kernel<1>, grid, block, 0, s, d_tiles, d, xprep, m, y);
-    else if (m <= 2)
-        hipLaunchKernelGGL(gemv_kernel<2>, grid, block, 0, s, d_tiles, d, xprep, m, y);
-    else if (m <= 4)
-        hipLaunchKernelGGL(gemv_kernel<4>, grid, block, 0, s, d_tiles, d, xprep, m, y);
-    else
-        hipLaunchKernelGGL(gemv_kernel<8>, grid, block, 0, s, d_tiles, d, xprep, m, y);
+template <int LPR>
+hipError_t launch_gemv_lpr(hipStream_t s, const uint8_t *const *d_tables, uint32_t count,
+                           const MatrixDims &d, const uint32_t *xprep, uint32_t m, float *y) {
+    auto go = [&](auto kernel, int rows_per_wave) {
+        const uint32_t rows_per_group = kGemvWaves * rows_per_wave;
+        dim3 grid((d.rows_padded + rows_per_group - 1) / rows_per_group, count);
+        hipLaunchKernelGGL(kernel, grid, dim3(kGemvWaves * kWave), 0, s, d_tables, d, xprep, m, y);
+    };
+    constexpr int G = kWave / LPR;
+    if (m <= 1) go(gemv_kernel<LPR, 16, 1>, 16 * G);
+    else if (m <= 2) go(gemv_kernel<LPR, 8, 2>, 8 * G);
+    else if (m <= 4) go(gemv_kernel<LPR, 8, 4>, 8 * G);
+    else go(gemv_kernel<LPR, 8, 8>, 8 * G);
     return hipGetLastError();
+}
+
+hipError_t launch_gemv(hipStream_t s, const uint8_t *const *d_tables, uint32_t count,
+                       const MatrixDims &d, const uint32_t *xprep, uint32_t m, float *y) {
+    if (d.lpr == 16) return launch_gemv_lpr<16>(s, d_tables, count, d, xprep, m, y);
+    if (d.lpr == 32) return launch_gemv_lpr<32>(s, d_tables, count, d, xprep, m, y);
+    return launch_gemv_lpr<64>(s, d_tables, count, d, xprep, m, y);
 }
 
 // ---------------------------------------------------------------------------
@@ -219,7 +213,7 @@ constexpr int kRouteRows = 2;
 template <int MT>
 __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__restrict__ h,
                                                     const float *__restrict__ norm, uint32_t m,
-                                                    uint32_t *__restrict__ xprep,
+                                                    uint32_t bp, uint32_t *__restrict__ xprep,
                                                     float *__restrict__ logits,
                                                     Plan *__restrict__ plan,
                                                     uint32_t *__restrict__ counter,
@@ -265,14 +259,15 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
         }
     }
 
-    // 2. xprep of block kb is held by threads [kb * 32/vpt, (kb+1) * 32/vpt).
+    // 2. xprep of block kb is held by threads [kb * 32/vpt, (kb+1) * 32/vpt);
+    //    records are strided by the gate/up matrices' padded block count bp.
     const uint32_t KB = H / 32;
     for (uint32_t kb = blockIdx.x; kb < KB; kb += gridDim.x) {
         const int lpb = 32 / vpt;
         const int first = (int)kb * lpb;
         if (tid >= first && tid < first + lpb) {
             for (int t = 0; t < (int)m; ++t) {
-                uint32_t *rec = xprep + ((size_t)t * KB + kb) * kXprepDwords;
+                uint32_t *rec = xprep + ((size_t)t * bp + kb) * kXprepDwords;
                 if (vpt == 8) {
                     float v8[8];
 #pragma unroll
@@ -389,6 +384,8 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
     __syncthreads();
     const int n = (int)m * kTopK;
     if (s_bad) {
+        if (wave == 0)
+            for (int i = lane; i < (int)m * (kTopK + 1); i += kWave) plan->slots[i].token = -1;
         if (tid == 0) {
             plan->n_slots = 0;
             plan->n_union = 0;
@@ -426,9 +423,14 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
             const int slot = (int)m + base + rank;
             const int t = lane / kTopK, k = lane % kTopK;
             const float wv = s_w[lane];
+            SlotRec rec;
+            rec.mat[0] = L.mats[e_i * 3 + 0];
+            rec.mat[1] = L.mats[e_i * 3 + 1];
+            rec.mat[2] = L.mats[e_i * 3 + 2];
+            rec.token = t;
+            rec.coef = wv;
+            plan->slots[slot] = rec;
             plan->slot_expert[slot] = e_i;
-            plan->slot_token[slot] = t;
-            plan->slot_coef[slot] = wv;
             plan->ids[t][k] = (uint16_t)e_i;
             plan->weights[t][k] = wv;
             if (flag) plan->union_ids[upos] = e_i;
@@ -438,9 +440,14 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
         if (lane < (int)m) {
             const float gl = load_coherent(logits + (size_t)lane * (E + 1) + E);
             plan->gate_logit[lane] = gl;
+            SlotRec rec;
+            rec.mat[0] = L.mats[E * 3 + 0];
+            rec.mat[1] = L.mats[E * 3 + 1];
+            rec.mat[2] = L.mats[E * 3 + 2];
+            rec.token = lane;
+            rec.coef = 1.0f / (1.0f + expf(-gl));
+            plan->slots[lane] = rec;
             plan->slot_expert[lane] = (int)E;
-            plan->slot_token[lane] = lane;
-            plan->slot_coef[lane] = 1.0f / (1.0f + expf(-gl));
         }
         if (lane == 0) {
             plan->n_union = nu;
@@ -456,9 +463,10 @@ hipError_t launch_route(hipStream_t s, const LayerDev &L, const float *h, const 
                         uint32_t m, Scratch &sc, uint16_t *ids_out, float *w_out,
                         int32_t *status_out) {
     const uint32_t grid = (L.n_experts + 1 + kRouteRows - 1) / kRouteRows;
+    const uint32_t bp = padded_blocks(L.hidden / 32);
     uint32_t *counter = sc.counters;
 #define TQF_ROUTE(MT)                                                                        \
-    hipLaunchKernelGGL(route_kernel<MT>, dim3(grid), dim3(256), 0, s, L, h, norm, m, sc.xprep, \
+    hipLaunchKernelGGL(route_kernel<MT>, dim3(grid), dim3(256), 0, s, L, h, norm, m, bp, sc.xprep, \
                        sc.logits, sc.plan, counter, ids_out, w_out, status_out)
     if (m <= 1) TQF_ROUTE(1);
     else if (m <= 2) TQF_ROUTE(2);
@@ -469,184 +477,187 @@ hipError_t launch_route(hipStream_t s, const LayerDev &L, const float *h, const 
 }
 
 // ---------------------------------------------------------------------------
-// One wavefront's share of a pair slot: chunks [c_begin, c_end) step `step`
-// of one matrix for one token.
+// Gate/up kernel.  Grid (width / (64 G) row groups, pair slots), eight
+// wavefronts per workgroup; G = 64 / LPR lane groups per wavefront, LPR =
+// the gate/up matrices' padded block count (hidden / 32 <= 64).  Lane group
+// j of a wavefront owns 8 rows of both matrices: lane b loads block b of each
+// row (16 nibble loads), the scales of its block for the 8 rows (one 16-byte
+// load per matrix) and the activation record of block b of the slot's token,
+// then reduces the 16 block products across the group (value 2n + u: row n,
+// u = 0 gate, 1 up).  h = silu(gate) * up (weights.rs:241-259) meets in LDS
+// and the first G wavefronts write it as xprep records for the down kernel.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float slot_dot(const uint8_t *tiles, int lane, uint32_t c_begin,
-                                          uint32_t c_end, uint32_t step,
-                                          const uint32_t *__restrict__ xp_token) {
-    float acc = 0.0f;
-    int tok[1] = {0};
-    float a[1] = {0.0f};
-    for (uint32_t c = c_begin; c < c_end; c += step) {
-        uint4 nib[kChunkBlocks], scl;
-        load_tile(tiles + (size_t)c * kTileBytes, lane, nib, scl);
-        a[0] = 0.0f;
-        tile_accumulate<1>(nib, scl, c, xp_token, 0, tok, 1, a);
-        acc += a[0];
-    }
-    return acc;
-}
+constexpr int kGateUpWaves = 8;
+constexpr int kGateUpRows = 8;  // rows per lane group per matrix
 
-// ---------------------------------------------------------------------------
-// Gate/up kernel.  Grid (width/64 row groups, pair slots, K parts).  A
-// workgroup holds 2 * W wavefronts: W read the gate matrix and W the up
-// matrix, each wavefront one 9 KiB tile (64 rows x 256 columns) at a time.
-// Partials meet in LDS; with one K part the workgroup forms
-// h = silu(gate) * up (weights.rs:241-259) for its 64 rows and writes h as
-// xprep records for the down kernel.  With several K parts (small M, so the
-// grid still covers every CU) the parts hand off through device-coherent
-// partials and the last part to finish forms h.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void gate_up_kernel(LayerDev L, const Plan *__restrict__ plan,
-                                                       const uint32_t *__restrict__ xprep,
-                                                       uint32_t *__restrict__ hprep,
-                                                       float *__restrict__ gu_partial,
-                                                       uint32_t *__restrict__ counters) {
-    __shared__ float red[16][kWave];
-    __shared__ int s_last;
+template <int LPR>
+__global__ __launch_bounds__(kGateUpWaves * kWave) void gate_up_kernel(
+    LayerDev L, const Plan *__restrict__ plan, const uint32_t *__restrict__ xprep,
+    uint32_t *__restrict__ hprep, uint32_t rows_padded, uint32_t bp_down) {
+    constexpr int G = kWave / LPR;
+    constexpr int RW = kGateUpRows * G;  // rows per wavefront per matrix
+    constexpr int R = LPR / 16;          // copies of each reduced value
+    __shared__ float s_h[kGateUpWaves * RW];
     const int slot = blockIdx.y;
-    if (slot >= plan->n_slots) return;
+    const SlotRec rec = load_slot(&plan->slots[slot]);
+    if (rec.token < 0) return;  // routing failed: no work
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x % kWave;
-    const int waves = blockDim.x / kWave;
-    const int wpm = waves / 2;
-    const uint32_t g = blockIdx.x, kpart = blockIdx.z, kp = gridDim.z;
-    const uint32_t G = gridDim.x;
-    const int expert = __builtin_amdgcn_readfirstlane(plan->slot_expert[slot]);
-    const int tok = __builtin_amdgcn_readfirstlane(plan->slot_token[slot]);
-    const int mat = wave / wpm, wi = wave % wpm;
-    const uint32_t chunks = L.hidden / kChunkCols;
-    const uint32_t cpk = chunks / kp;
-    const uint32_t bpt = L.hidden / 32;
-    const uint8_t *tiles = L.mats[expert * 3 + mat] + (size_t)g * chunks * kTileBytes;
-    const uint32_t *xp = xprep + (size_t)tok * bpt * kXprepDwords;
-    red[wave][lane] = slot_dot(tiles, lane, kpart * cpk + wi, (kpart + 1) * cpk, wpm, xp);
+    const uint32_t j = (uint32_t)lane / LPR, b = (uint32_t)lane % LPR;
+    const int tok = rec.token;
+    const uint32_t r0 = (blockIdx.x * kGateUpWaves + wave) * RW;
+    if (r0 < rows_padded) {
+        const RowLane Wg = row_lane(rec.mat[0], rows_padded, LPR);
+        const RowLane Wu = row_lane(rec.mat[1], rows_padded, LPR);
+        const uint32_t rl = r0 + j * kGateUpRows;
+        uint4 ng[kGateUpRows], nu[kGateUpRows];
+#pragma unroll
+        for (int n = 0; n < kGateUpRows; ++n) {
+            ng[n] = load_nibbles(Wg, rl + n, b);
+            nu[n] = load_nibbles(Wu, rl + n, b);
+        }
+        const uint4 sg = load_scales(Wg, rl / 8, b), su = load_scales(Wu, rl / 8, b);
+        uint32_t x[28];
+        load_xrec(xprep + ((size_t)tok * LPR + b) * kXprepDwords, x);
+        __builtin_amdgcn_sched_barrier(0);  // every load in flight before any math
+        float v[2 * kGateUpRows];
+#pragma unroll
+        for (int n = 0; n < kGateUpRows; ++n) {
+            v[2 * n] = octet_scale(sg, n) * q4_block_dot(ng[n], x);
+            v[2 * n + 1] = octet_scale(su, n) * q4_block_dot(nu[n], x);
+        }
+        const float gate = transpose_reduce<LPR, 2 * kGateUpRows>(v);
+        const float up = dpp_f<0x100 + R>(gate);  // row_shl:R -> the up value
+        const uint32_t q = (uint32_t)lane % LPR;
+        if (q % (2 * R) == 0)
+            s_h[wave * RW + j * kGateUpRows + q / (2 * R)] = (gate / (1.0f + expf(-gate))) * up;
+    }
     __syncthreads();
-    float gate = 0.0f, up = 0.0f;
-    if (wave == 0) {
-        for (int w = 0; w < wpm; ++w) {
-            gate += red[w][lane];
-            up += red[wpm + w][lane];
+    if (wave < G) {
+        const uint32_t blk = blockIdx.x * (2 * G) + 2 * wave + (uint32_t)(lane >> 5);
+        if (blk < L.width / 32) {
+            float hv[1] = {s_h[(2 * wave + (lane >> 5)) * 32 + (lane & 31)]};
+            prep_block<1>(hv, lane & 31, hprep + ((size_t)slot * bp_down + blk) * kXprepDwords);
         }
-    }
-    if (kp > 1) {
-        float *part = gu_partial + ((size_t)(slot * G + g) * 4) * 2 * kWave;
-        if (wave == 0) {
-            store_coherent(&part[(kpart * 2 + 0) * kWave + lane], gate);
-            store_coherent(&part[(kpart * 2 + 1) * kWave + lane], up);
-            wait_own_stores();
-        }
-        __syncthreads();
-        uint32_t *ctr = counters + slot * G + g;
-        if (threadIdx.x == 0) s_last = (counter_arrive(ctr) == kp - 1) ? 1 : 0;
-        __syncthreads();
-        if (!s_last) return;
-        if (wave == 0) {
-            gate = 0.0f;
-            up = 0.0f;
-            for (uint32_t q = 0; q < kp; ++q) {
-                gate += load_coherent(&part[(q * 2 + 0) * kWave + lane]);
-                up += load_coherent(&part[(q * 2 + 1) * kWave + lane]);
-            }
-            if (lane == 0) counter_reset(ctr);
-        }
-    }
-    if (wave == 0) {
-        const float hv = (gate / (1.0f + expf(-gate))) * up;
-        const uint32_t hb = L.width / 32;
-        const uint32_t blk = g * 2 + (uint32_t)(lane >> 5);
-        uint32_t *rec = hprep + ((size_t)slot * hb + blk) * kXprepDwords;
-        float v1[1] = {hv};
-        prep_block<1>(v1, lane & 31, rec);
     }
 }
 
-hipError_t launch_gate_up(hipStream_t s, const LayerDev &L, uint32_t m, Scratch &sc,
-                          const Plan *plan, const uint32_t *xprep) {
-    const uint32_t kp = gate_up_kparts(m, L.hidden);
-    const uint32_t cpk = (L.hidden / kChunkCols) / kp;
-    const uint32_t wpm = cpk < 8 ? cpk : 8;
-    dim3 grid(L.width / kRowsPerGroup, m * (kTopK + 1), kp), block(2 * wpm * kWave);
-    hipLaunchKernelGGL(gate_up_kernel, grid, block, 0, s, L, plan, xprep, sc.hprep, sc.gu_partial,
-                       sc.counters + counter_gate_up_offset(L.hidden));
+hipError_t launch_gate_up(hipStream_t s, const LayerDev &L, uint32_t slots, const Plan *plan,
+                          const uint32_t *xprep, uint32_t *hprep) {
+    const MatrixDims g = matrix_dims(L.width, L.hidden);
+    const MatrixDims dn = matrix_dims(L.hidden, L.width);
+    const uint32_t G = kWave / g.lpr;
+    const uint32_t rows_per_group = kGateUpWaves * kGateUpRows * G;
+    dim3 grid((g.rows_padded + rows_per_group - 1) / rows_per_group, slots);
+    dim3 block(kGateUpWaves * kWave);
+#define TQF_GU(LPR)                                                                         \
+    hipLaunchKernelGGL(gate_up_kernel<LPR>, grid, block, 0, s, L, plan, xprep, hprep,          \
+                       g.rows_padded, dn.blocks_padded)
+    if (g.blocks_padded == 16) TQF_GU(16);
+    else if (g.blocks_padded == 32) TQF_GU(32);
+    else if (g.blocks_padded == 64) TQF_GU(64);
+    else return hipErrorInvalidValue;
+#undef TQF_GU
     return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
-// Down kernel.  Grid (hidden/64 row groups, slot groups of `spg` pair
-// slots); each wavefront takes one 9 KiB tile (one slot, one 256-column
-// chunk of the width).  The workgroup weights each slot by its coefficient
-// (shared: sigmoid gate; routed: route weight; experts/mod.rs:1609-1630) and
-// sums per token; the last workgroup of a row group sums the slot groups in
-// order and adds the residual (runtime.rs:802) when given.
+// Down kernel.  Grid (hidden / (16 G) row groups, slot groups of four pair
+// slots), one wavefront per slot.  Lane group j owns 16 consecutive rows of
+// the slot's down matrix; lane b reads block b of each (LPR = the padded
+// block count of the width, <= 64) against block b of the slot's h records.
+// The workgroup weights each slot by its coefficient (shared: sigmoid gate;
+// routed: route weight; experts/mod.rs:1609-1630) and sums per token in slot
+// order; the last workgroup of a row group sums the slot groups in order and
+// adds the residual (runtime.rs:802) when given.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void down_kernel(LayerDev L, const Plan *__restrict__ plan,
-                                                    const uint32_t *__restrict__ hprep,
-                                                    float *__restrict__ partial,
-                                                    uint32_t *__restrict__ counters,
-                                                    const float *resid, float *out, uint32_t m,
-                                                    uint32_t spg) {
-    __shared__ float red[16][kWave];
-    __shared__ int s_tok[16];
+constexpr int kDownSlots = 4;
+constexpr int kDownRows = 16;  // rows per lane group
+
+template <int LPR>
+__global__ __launch_bounds__(kDownSlots * kWave) void down_kernel(
+    LayerDev L, const Plan *__restrict__ plan, const uint32_t *__restrict__ hprep,
+    uint32_t rows_padded, float *__restrict__ partial, uint32_t *__restrict__ counters,
+    const float *resid, float *out, uint32_t m, int n_slots) {
+    constexpr int G = kWave / LPR;
+    constexpr int RW = kDownRows * G;  // rows per workgroup
+    __shared__ float red[kDownSlots][RW];
+    __shared__ int s_tok[kDownSlots];
     __shared__ int s_last;
-    const int n_slots = plan->n_slots;
-    const int n_sg = (n_slots + (int)spg - 1) / (int)spg;
+    const int n_sg = gridDim.y;  // every workgroup arrives, with or without work
     const int sg = blockIdx.y;
-    if (sg >= n_sg) return;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x % kWave;
-    const int waves = blockDim.x / kWave;
-    const uint32_t chunks = L.width / kChunkCols;
-    const int slot = sg * (int)spg + wave / (int)chunks;
-    const uint32_t c = (uint32_t)wave % chunks;
-    const uint32_t g = blockIdx.x;
+    const uint32_t j = (uint32_t)lane / LPR, b = (uint32_t)lane % LPR;
+    const int slot = sg * kDownSlots + wave;
+    const uint32_t r0 = blockIdx.x * RW;
     const uint32_t H = L.hidden;
-    const uint32_t hb = L.width / 32;
     float v = 0.0f;
-    int tok = -1;
-    if (slot < n_slots) {
-        const int expert = __builtin_amdgcn_readfirstlane(plan->slot_expert[slot]);
-        tok = __builtin_amdgcn_readfirstlane(plan->slot_token[slot]);
-        const float coef = plan->slot_coef[slot];
-        const uint8_t *tiles = L.mats[expert * 3 + 2] + (size_t)g * chunks * kTileBytes;
-        const uint32_t *xp = hprep + (size_t)slot * hb * kXprepDwords;
-        v = coef * slot_dot(tiles, lane, c, c + 1, 1, xp);
+    const SlotRec rec = load_slot(&plan->slots[slot < n_slots ? slot : 0]);
+    const int tok = slot < n_slots ? rec.token : -1;
+    if (tok >= 0) {
+        const float coef = rec.coef;
+        const RowLane W = row_lane(rec.mat[2], rows_padded, LPR);
+        const uint32_t rl = r0 + j * kDownRows;
+        uint4 nib[kDownRows];
+#pragma unroll
+        for (int n = 0; n < kDownRows; ++n) nib[n] = load_nibbles(W, rl + n, b);
+        const uint4 s0 = load_scales(W, rl / 8, b), s1 = load_scales(W, rl / 8 + 1, b);
+        uint32_t x[28];
+        load_xrec(hprep + ((size_t)slot * LPR + b) * kXprepDwords, x);
+        __builtin_amdgcn_sched_barrier(0);  // every load in flight before any math
+        float a[kDownRows];
+#pragma unroll
+        for (int n = 0; n < kDownRows; ++n)
+            a[n] = octet_scale(n < 8 ? s0 : s1, n % 8) * q4_block_dot(nib[n], x);
+        v = coef * transpose_reduce<LPR, kDownRows>(a);
     }
-    red[wave][lane] = v;
+    if (reduced_first_copy<LPR, kDownRows>(lane))
+        red[wave][j * kDownRows + reduced_index<LPR, kDownRows>(lane)] = v;
     if (lane == 0) s_tok[wave] = tok;
     __syncthreads();
-    const uint32_t row = g * kRowsPerGroup + lane;
-    for (int t = wave; t < (int)m; t += waves) {
+    for (int i = threadIdx.x; i < (int)m * RW; i += kDownSlots * kWave) {
+        const int t = i / RW, r = i % RW;
         float p = 0.0f;
-        for (int w = 0; w < waves; ++w)
-            if (s_tok[w] == t) p += red[w][lane];
-        store_coherent(&partial[((size_t)sg * kMaxTokens + t) * H + row], p);
+#pragma unroll
+        for (int w = 0; w < kDownSlots; ++w)
+            if (s_tok[w] == t) p += red[w][r];
+        if (r0 + r < H) store_coherent(&partial[((size_t)sg * kMaxTokens + t) * H + r0 + r], p);
     }
     wait_own_stores();
     __syncthreads();
-    if (threadIdx.x == 0) s_last = (counter_arrive(&counters[g]) == (uint32_t)n_sg - 1) ? 1 : 0;
+    if (threadIdx.x == 0)
+        s_last = (counter_arrive(&counters[blockIdx.x]) == (uint32_t)n_sg - 1) ? 1 : 0;
     __syncthreads();
     if (!s_last) return;
-    for (int t = wave; t < (int)m; t += waves) {
-        float s = 0.0f;
-        for (int q = 0; q < n_sg; ++q) s += load_coherent(&partial[((size_t)q * kMaxTokens + t) * H + row]);
-        const size_t o = (size_t)t * H + row;
-        out[o] = resid ? resid[o] + s : s;
+    for (int i = threadIdx.x; i < (int)m * RW; i += kDownSlots * kWave) {
+        const int t = i / RW, r = i % RW;
+        if (r0 + r >= H) continue;
+        float sum = 0.0f;
+        for (int q = 0; q < n_sg; ++q)
+            sum += load_coherent(&partial[((size_t)q * kMaxTokens + t) * H + r0 + r]);
+        const size_t o = (size_t)t * H + r0 + r;
+        out[o] = resid ? resid[o] + sum : sum;
     }
-    if (threadIdx.x == 0) counter_reset(&counters[g]);
+    if (threadIdx.x == 0) counter_reset(&counters[blockIdx.x]);
 }
 
-hipError_t launch_down(hipStream_t s, const LayerDev &L, uint32_t m, Scratch &sc,
-                       const Plan *plan, const float *resid, float *out) {
-    const uint32_t chunks = L.width / kChunkCols;
-    uint32_t spg = 16 / chunks;  // at most 16 wavefronts per workgroup
-    if (spg > m) spg = m;        // M slots per group: 9 groups for any M
-    if (spg == 0) spg = 1;
-    const uint32_t n_sg = (m * (kTopK + 1) + spg - 1) / spg;
-    dim3 grid(L.hidden / kRowsPerGroup, n_sg), block(spg * chunks * kWave);
-    hipLaunchKernelGGL(down_kernel, grid, block, 0, s, L, plan, sc.hprep, sc.partial,
-                       sc.counters + kCounterDown, resid, out, m, spg);
+hipError_t launch_down(hipStream_t s, const LayerDev &L, uint32_t m, uint32_t slots, Scratch &sc,
+                       const Plan *plan, const uint32_t *hprep, const float *resid, float *out) {
+    const MatrixDims dn = matrix_dims(L.hidden, L.width);
+    const uint32_t G = kWave / dn.lpr;
+    const uint32_t rows_per_group = kDownRows * G;
+    const uint32_t n_sg = (slots + kDownSlots - 1) / kDownSlots;
+    dim3 grid((dn.rows_padded + rows_per_group - 1) / rows_per_group, n_sg);
+    dim3 block(kDownSlots * kWave);
+#define TQF_DOWN(LPR)                                                                      \
+    hipLaunchKernelGGL(down_kernel<LPR>, grid, block, 0, s, L, plan, hprep, dn.rows_padded, \
+                       sc.partial, sc.counters + kCounterDown, resid, out, m, (int)slots)
+    if (dn.blocks_padded == 16) TQF_DOWN(16);
+    else if (dn.blocks_padded == 32) TQF_DOWN(32);
+    else if (dn.blocks_padded == 64) TQF_DOWN(64);
+    else return hipErrorInvalidValue;
+#undef TQF_DOWN
     return hipGetLastError();
 }
 

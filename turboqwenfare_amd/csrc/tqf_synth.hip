@@ -37,7 +37,8 @@ __device__ __forceinline__ void philox4x32_10(uint32_t c[4], uint32_t k0, uint32
 }
 
 __global__ __launch_bounds__(256) void synth_q4_0_kernel(uint32_t rows, uint32_t blocks,
-                                                         uint32_t chunks, uint32_t key0,
+                                                         uint32_t rows_padded, uint32_t bp,
+                                                         uint32_t key0,
                                                          uint32_t key1,
                                                          uint8_t *__restrict__ tiles) {
     const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -50,10 +51,9 @@ __global__ __launch_bounds__(256) void synth_q4_0_kernel(uint32_t rows, uint32_t
     const float u = (float)(s[0] >> 8) * 0x1p-24f;
     const float d = 0.005f + 0.015f * u;
     const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)d);
-    uint8_t *tile = tiles + ((size_t)(r / kRowsPerGroup) * chunks + b / kChunkBlocks) * kTileBytes;
-    const uint32_t lane = r % kRowsPerGroup, j = b % kChunkBlocks;
-    *reinterpret_cast<uint4 *>(tile + j * 1024 + lane * 16) = make_uint4(q[0], q[1], q[2], q[3]);
-    *reinterpret_cast<uint16_t *>(tile + kTileNibbleBytes + lane * 16 + j * 2) = h;
+    *reinterpret_cast<uint4 *>(tiles + ((size_t)r * bp + b) * 16) = make_uint4(q[0], q[1], q[2], q[3]);
+    *reinterpret_cast<uint16_t *>(tiles + (size_t)rows_padded * bp * 16 +
+                                  ((size_t)(r / 8) * bp + b) * 16 + (r % 8) * 2) = h;
 }
 
 hipError_t launch_synth_q4_0(hipStream_t s, const MatrixDims &d, uint32_t tensor_id,
@@ -61,7 +61,7 @@ hipError_t launch_synth_q4_0(hipStream_t s, const MatrixDims &d, uint32_t tensor
     const uint64_t n = (uint64_t)d.rows * (d.cols / 32);
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(synth_q4_0_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s,
-                       d.rows, d.cols / 32, d.chunks, tensor_id, seed, tiles);
+                       d.rows, d.blocks, d.rows_padded, d.blocks_padded, tensor_id, seed, tiles);
     return hipGetLastError();
 }
 
