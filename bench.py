@@ -133,7 +133,21 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--gemv-pool", type=int, default=2048,
                     help="distinct 512x2048 matrices in the config-1 GEMV bandwidth pool")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 5 plain device copies of MIB MiB (torch) and exit: the "
+                         "known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"bench: copied {args.copy_calibration} MiB x 5 (read + write per copy)")
+        return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

@@ -174,3 +174,22 @@ def test_device_entry_point_matches_host(backend):
         assert (a, tk) == orc.accept(target, draft, dtok, 0.7, False, u, ur)
     for b in bufs + [acc, toks]:
         backend.free(b)
+
+
+def test_matches_committed_golden(backend):
+    """The committed oracle outcomes (tests/golden/oracle_vectors.npz) for
+    seeds 0..63, greedy and stochastic, at V = 1000, k = 3."""
+    import sys
+    from pathlib import Path
+
+    golden = Path(__file__).resolve().parent / "golden"
+    sys.path.insert(0, str(golden))
+    from golden_inputs import accept_inputs
+
+    g = np.load(golden / "oracle_vectors.npz")
+    for gi, greedy in enumerate((True, False)):
+        for seed in range(64):
+            target, draft, dtok, u, ur = accept_inputs(seed)
+            a, toks = backend.accept(target, draft, dtok, 0.7, greedy, u, ur)
+            assert a == g["accept_len"][gi, seed], (greedy, seed)
+            assert toks == list(g["accept_tokens"][gi, seed, : a + 1]), (greedy, seed)

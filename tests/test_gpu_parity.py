@@ -136,6 +136,21 @@ def test_gemv_batched_matches_single(backend):
         backend.free_weights(w)
 
 
+def test_gemv_config1_matches_committed_golden(backend):
+    import sys
+    from pathlib import Path
+
+    golden = Path(__file__).resolve().parent / "golden"
+    sys.path.insert(0, str(golden))
+    from golden_inputs import gemv_inputs
+
+    w, x = gemv_inputs()
+    dev = backend.upload_q4_0(w, 512, 2048)
+    want = np.load(golden / "oracle_vectors.npz")["gemv_y"]
+    assert rel_err(backend.q4_gemv(dev, x), want) < 1e-5
+    backend.free_weights(dev)
+
+
 # ---- a10: one expert --------------------------------------------------------
 @pytest.mark.parametrize("m", [1, 4])
 def test_expert_forward_parity(backend, m):
@@ -323,3 +338,32 @@ def test_top_logit_candidates_parity(backend):
         tc, vc = orc.top_logit_candidates(lg[r])
         assert list(toks[r]) == list(tc)
         assert np.array_equal(vals[r], vc)
+
+
+def test_small_geometry_layer_matches_committed_golden(backend):
+    """hidden 256, width 256 (padded block counts: the 16-lane row layout with
+    zero-scale padding blocks) against the committed oracle outputs."""
+    import sys
+    from pathlib import Path
+
+    golden = Path(__file__).resolve().parent / "golden"
+    sys.path.insert(0, str(golden))
+    from golden_inputs import SMALL, small_layer_inputs
+
+    router, gate, x, mats = small_layer_inputs()
+    E, H, F = SMALL["experts"], SMALL["hidden"], SMALL["width"]
+    dev = [(backend.upload_q4_0(g, F, H), backend.upload_q4_0(u, F, H), backend.upload_q4_0(d, H, F))
+           for g, u, d in mats]
+    layer = backend.prepare_moe_layer(backend.upload_f32(router), backend.upload_f32(gate), dev[E],
+                                      [m[0] for m in dev[:E]], [m[1] for m in dev[:E]],
+                                      [m[2] for m in dev[:E]])
+    g = np.load(golden / "oracle_vectors.npz")
+    for m in (1, 4):
+        y, ids, w = backend.moe_forward_batch(layer, x[:m])
+        assert np.array_equal(ids, g[f"moe_ids{m}"])
+        assert rel_err(w, g[f"moe_w{m}"]) < 1e-5
+        assert rel_err(y, g[f"moe_y{m}"]) < FFN_TOL
+    backend.free_moe_layer(layer)
+    for t in dev:
+        for wt in t:
+            backend.free_weights(wt)

@@ -1,0 +1,129 @@
+"""CPU tests of the host-side logic: MTP accounting (runtime/mtp.rs), the
+union golden from the reference's committed real router trace, and the
+synthetic-weight generator shared by the device kernel and the host."""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import cpu_oracle as orc
+from turboqwenfare_amd import mtp, synth
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def test_verify_pair_kat():
+    # mtp.rs:212-221
+    assert mtp.verify_pair(42, 42) == mtp.VerifyOutcome(True, 2)
+    assert mtp.verify_pair(42, 7) == mtp.VerifyOutcome(False, 1)
+
+
+def test_statistics_kat():
+    # mtp.rs:224-235
+    s = mtp.MtpStatistics()
+    s.record(True, 2, 1)
+    s.record(False, 1, 1)
+    s.record(True, 2, 1)
+    assert (s.drafted_tokens, s.accepted_tokens, s.emitted_tokens, s.target_backbone_passes) == (3, 2, 5, 3)
+    assert abs(s.acceptance_rate() - 2 / 3) < 1e-9
+    assert abs(s.emitted_tokens_per_target_pass() - 5 / 3) < 1e-9
+    assert mtp.MtpStatistics().acceptance_rate() == 0.0
+
+
+def test_statistics_k_draft_verify():
+    s = mtp.MtpStatistics()
+    s.record_verify(3, 2)  # two of three drafts accepted, 3 tokens emitted
+    s.record_verify(3, 3)
+    assert (s.drafted_tokens, s.accepted_tokens, s.emitted_tokens, s.target_backbone_passes) == (6, 5, 7, 2)
+
+
+def test_controller_hysteresis_kats():
+    # mtp.rs:238-266
+    c = mtp.MtpController(4)
+    assert not c.enabled
+    c.record_and_decide(2)
+    assert not c.enabled
+    for _ in range(4):
+        c.record_and_decide(2)
+    assert c.enabled
+    for _ in range(4):
+        c.record_and_decide(0)
+    assert not c.enabled
+
+
+def test_union_bandwidth_kat():
+    # mtp.rs:269-298
+    r = mtp.union_bandwidth([1, 2, 3, 4, 5, 6, 7, 8], [1, 2, 3, 4, 9, 10, 11, 12])
+    assert r.union_experts == 12 and r.separate_experts_sum == 16
+    assert r.saved_bytes > 0 and r.union_bytes + r.saved_bytes == r.separate_bytes_sum
+
+
+def test_expert_bytes():
+    # mtp.rs:38-42 with spec section 117 geometry: 1,769,472 B per expert,
+    # equal for Q4_K (144 B / 256) and Q4_0 (18 B / 32)
+    assert mtp.expert_bytes() == 1_769_472 == mtp.expert_bytes_q4_0()
+
+
+def test_real_trace_union_savings_golden():
+    # mtp.rs:310-343 over docs/research/qualification/raw-a-128-route-trace.json
+    # (ids extracted by tests/golden/make_golden.py); the figures are the ones
+    # the reference records in docs/research/phase-33-mtp.md:57
+    ids = np.load(GOLDEN / "route_trace_ids.npy")
+    union = separate = pairs = 0
+    for s in range(ids.shape[0] - 1):
+        for layer in range(ids.shape[1]):
+            r = mtp.union_bandwidth(ids[s, layer], ids[s + 1, layer])
+            union += r.union_bytes
+            separate += r.separate_bytes_sum
+            pairs += 1
+    assert pairs == 5_080
+    assert separate == 143_822_684_160
+    assert union == 113_892_065_280
+    assert round((separate - union) / separate * 100, 2) == 20.81
+
+
+def test_routes_union_is_first_demand_order():
+    routes = [[5, 3, 9, 1, 2, 4, 6, 7], [3, 8, 5, 10, 11, 12, 13, 14]]
+    assert mtp.routes_union(routes) == [5, 3, 9, 1, 2, 4, 6, 7, 8, 10, 11, 12, 13, 14]
+    assert mtp.routes_union(routes) == orc.batch_union(np.array(routes, np.uint16))
+    bw = mtp.routes_union_bandwidth(routes)
+    assert bw.union_experts == 14 and bw.separate_experts_sum == 16
+
+
+def test_expected_tokens_per_step():
+    # E[tokens / step] = (1 - a^(k+1)) / (1 - a) for k = 3
+    assert abs(mtp.expected_tokens_per_step(0.6, 3) - 2.176) < 1e-12
+    assert abs(mtp.expected_tokens_per_step(0.8, 3) - 2.952) < 1e-12
+
+
+def test_synthetic_q4_0_definition():
+    # the generator's definition: nibbles are Philox words, scales
+    # 0.005 + 0.015 u rounded to binary16
+    q = synth.q4_0_synthetic(3, 64, 17, 4).reshape(-1, 18)
+    for b in range(q.shape[0]):
+        words = orc.philox4x32_10([b, 0, 0, 0], [17, 4])
+        assert q[b, 2:].tobytes() == words.astype("<u4").tobytes()
+        w0 = orc.philox4x32_10([b, 0, 1, 0], [17, 4])[0]
+        d = np.float32(0.005) + np.float32(0.015) * (np.float32(w0 >> 8) * np.float32(2 ** -24))
+        assert q[b, 0:2].tobytes() == np.float16(d).tobytes()
+    scales = q[:, 0:2].copy().view(np.float16).astype(np.float32)
+    assert np.all((scales >= 0.00499) & (scales <= 0.02001))
+
+
+def test_philox_uniforms_definition():
+    u = synth.philox_uniforms(9, 1, 5)
+    for i in range(5):
+        w = orc.philox4x32_10([i, 1, 0, 0], [9, 0x243F6A88])[0]
+        assert u[i] == np.float32(w >> 8) * np.float32(2 ** -24)
+    assert np.all((u >= 0) & (u < 1))
+
+
+@pytest.mark.parametrize("bad", [31, 48])
+def test_synthetic_rejects_bad_cols(bad):
+    if bad % 32:
+        with pytest.raises(ValueError):
+            synth.q4_0_synthetic(2, bad, 0, 0)
+    else:
+        assert synth.q4_0_synthetic(2, bad, 0, 0).size == 2 * (bad // 32) * 18

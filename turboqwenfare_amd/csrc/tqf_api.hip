@@ -601,13 +601,11 @@ extern "C" int32_t tqf_hip_weights_download(tqf_hip_ctx *ctx, const tqf_hip_weig
     std::vector<uint8_t> tiles(w->bytes);
     TQF_HIP(ctx, hipMemcpyAsync(tiles.data(), w->tiles, w->bytes, hipMemcpyDeviceToHost, ctx->stream));
     TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    const uint8_t *scales = tiles.data() + nibble_plane_bytes(d);
-    const size_t bp = d.blocks_padded;
     for (uint32_t r = 0; r < d.rows; ++r) {
         for (uint32_t b = 0; b < blocks; ++b) {
             uint8_t *dst = q4_0 + ((size_t)r * blocks + b) * kQ4Block;
-            std::memcpy(dst, scales + ((r / 8) * bp + b) * 16 + (r % 8) * 2, 2);
-            std::memcpy(dst + 2, tiles.data() + (r * bp + b) * 16, 16);
+            std::memcpy(dst, tiles.data() + scale_offset(d, r, b), 2);
+            std::memcpy(dst + 2, tiles.data() + nibble_offset(d, r, b), 16);
         }
     }
     return TQF_HIP_OK;

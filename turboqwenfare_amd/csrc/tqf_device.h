@@ -108,11 +108,19 @@ __device__ __forceinline__ void split_digits(float x, int e, float scale, int &d
     d2 = (X1 - d1) >> 8;
 }
 
+// Address of dword `dw` (0..27) of the record of block b in one activation
+// row's record planes (layout in tqf_internal.h: plane dw/4, block b, word
+// dw%4).
+__device__ __forceinline__ uint32_t *rec_dw(uint32_t *row, uint32_t bp, uint32_t b, int dw) {
+    return row + (size_t)(dw >> 2) * 4 * bp + 4 * b + (dw & 3);
+}
+
 // Writes one xprep record for a 32-element block held by a group of
 // 32/EPL lanes (EPL consecutive elements per lane, group-aligned lanes).
 template <int EPL>
 __device__ __forceinline__ void prep_block(const float (&v)[EPL], int lane_in_group,
-                                           uint32_t *__restrict__ rec) {
+                                           uint32_t *__restrict__ row, uint32_t bp,
+                                           uint32_t block) {
     constexpr int LPB = 32 / EPL;
     float amax = 0.0f;
     bool bad = false;
@@ -151,30 +159,28 @@ __device__ __forceinline__ void prep_block(const float (&v)[EPL], int lane_in_gr
     if constexpr (EPL >= 4) {
 #pragma unroll
         for (int q = 0; q < EPL / 4; ++q) {
-            int dw = lane_in_group * (EPL / 4) + q;
-            rec[dw] = pk0[q];
-            rec[8 + dw] = pk1[q];
-            rec[16 + dw] = pk2[q];
+            const int dw = lane_in_group * (EPL / 4) + q;
+            *rec_dw(row, bp, block, dw) = pk0[q];
+            *rec_dw(row, bp, block, 8 + dw) = pk1[q];
+            *rec_dw(row, bp, block, 16 + dw) = pk2[q];
         }
     } else {
-        uint8_t *b = reinterpret_cast<uint8_t *>(rec);
 #pragma unroll
         for (int i = 0; i < EPL; ++i) {
-            int j = lane_in_group * EPL + i;
-            b[j] = (uint8_t)(pk0[0] >> (8 * i));
-            b[32 + j] = (uint8_t)(pk1[0] >> (8 * i));
-            b[64 + j] = (uint8_t)(pk2[0] >> (8 * i));
+            const int j = lane_in_group * EPL + i;  // element 0..31 -> byte j of a digit
+            reinterpret_cast<uint8_t *>(rec_dw(row, bp, block, j >> 2))[j & 3] =
+                (uint8_t)(pk0[0] >> (8 * i));
+            reinterpret_cast<uint8_t *>(rec_dw(row, bp, block, 8 + (j >> 2)))[j & 3] =
+                (uint8_t)(pk1[0] >> (8 * i));
+            reinterpret_cast<uint8_t *>(rec_dw(row, bp, block, 16 + (j >> 2)))[j & 3] =
+                (uint8_t)(pk2[0] >> (8 * i));
         }
     }
     if (lane_in_group == 0) {
-        rec[24] = (uint32_t)(-8 * s0);
-        rec[25] = (uint32_t)(-8 * s1);
-        rec[26] = (uint32_t)(-8 * s2);
-        rec[27] = __float_as_uint(scale);
-        rec[28] = 0;
-        rec[29] = 0;
-        rec[30] = 0;
-        rec[31] = 0;
+        *rec_dw(row, bp, block, 24) = (uint32_t)(-8 * s0);
+        *rec_dw(row, bp, block, 25) = (uint32_t)(-8 * s1);
+        *rec_dw(row, bp, block, 26) = (uint32_t)(-8 * s2);
+        *rec_dw(row, bp, block, 27) = __float_as_uint(scale);
     }
 }
 
@@ -287,15 +293,16 @@ __device__ __forceinline__ bool reduced_first_copy(int lane) {
 }
 
 // ---- row-lane matrix access ------------------------------------------------
+// Octet-chunk layout (tqf_internal.h): rows 8o..8o+7 are one contiguous chunk
+// of 9 * Bp * 16 bytes: their nibble rows, then one 16-byte scale vector per
+// block.
 struct RowLane {
-    const uint8_t *nib;    // nibble plane
-    const uint8_t *scale;  // scale plane
-    uint32_t bp;           // padded blocks per row
+    const uint8_t *base;
+    uint32_t bp;  // padded blocks per row
 };
-__device__ __forceinline__ RowLane row_lane(const uint8_t *base, uint32_t rows_padded, uint32_t bp) {
+__device__ __forceinline__ RowLane row_lane(const uint8_t *base, uint32_t bp) {
     RowLane r;
-    r.nib = base;
-    r.scale = base + (size_t)rows_padded * bp * 16;
+    r.base = base;
     r.bp = bp;
     return r;
 }
@@ -308,17 +315,19 @@ __device__ __forceinline__ uint4 load_global_u4(const void *p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ uint4 load_nibbles(const RowLane &m, uint32_t row, uint32_t block) {
-    return load_global_u4(m.nib + ((size_t)row * m.bp + block) * 16);
+    return load_global_u4(m.base + (((size_t)(row >> 3) * 9 + (row & 7)) * m.bp + block) * 16);
 }
 // Scales of rows 8*octet .. 8*octet+7 of one block.
 __device__ __forceinline__ uint4 load_scales(const RowLane &m, uint32_t octet, uint32_t block) {
-    return load_global_u4(m.scale + ((size_t)octet * m.bp + block) * 16);
+    return load_global_u4(m.base + (((size_t)octet * 9 + 8) * m.bp + block) * 16);
 }
-// One xprep record (28 used dwords) into registers.
-__device__ __forceinline__ void load_xrec(const uint32_t *rec, uint32_t (&x)[28]) {
+// The record of block b of one activation row into registers: seven 16-byte
+// loads, each part of a contiguous 1 KiB wavefront access when lane = block.
+__device__ __forceinline__ void load_xrec(const uint32_t *row, uint32_t bp, uint32_t b,
+                                          uint32_t (&x)[28]) {
 #pragma unroll
     for (int i = 0; i < 7; ++i) {
-        const uint4 q = load_global_u4(rec + 4 * i);
+        const uint4 q = load_global_u4(row + (size_t)i * 4 * bp + 4 * b);
         x[4 * i + 0] = q.x;
         x[4 * i + 1] = q.y;
         x[4 * i + 2] = q.z;

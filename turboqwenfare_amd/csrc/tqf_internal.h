@@ -4,16 +4,17 @@
 // is rows x B blocks of 18 bytes (f16 scale d, 16 nibble bytes qs; element j
 // of a block is (qs[j] & 15) - 8, element j + 16 is (qs[j] >> 4) - 8;
 // format/quant/dequant.rs:110-123).  The backend pads B to Bp (16, 32 or a
-// multiple of 64) and the rows to a multiple of 64, and stores
-//   nibble plane  [Rp rows][Bp blocks][16 bytes]              (row-major)
-//   scale plane   [Rp/8 row octets][Bp blocks][8 rows x f16]
+// multiple of 64) and the rows to a multiple of 64, and stores every octet of
+// rows 8o..8o+7 as one contiguous chunk of 9 * Bp * 16 bytes:
+//   [8 rows][Bp blocks][16 nibble bytes]   then   [Bp blocks][8 rows x f16]
 // A row's blocks are spread across lanes: lane l of a 64-wide wavefront owns
 // block (l mod LPR) (LPR = min(Bp, 64) lanes per row, Bp/LPR blocks per
 // lane), so one 128-bit load per lane reads 64/LPR whole rows = 1 KiB
-// contiguously, and one 16-byte scale load gives a lane the scales of eight
-// rows.  Padding has zero scale (products exactly zero).  The bytes are the
-// GGML bytes moved, never re-encoded: the repack is lossless and
-// tqf_hip_weights_download() inverts it.
+// contiguously, one 16-byte scale load gives a lane the scales of eight rows,
+// and a wavefront that owns whole octets reads one contiguous 9 KiB stretch
+// per octet (DRAM-page friendly).  Padding has zero scale (products exactly
+// zero).  The bytes are the GGML bytes moved, never re-encoded: the repack is
+// lossless and tqf_hip_weights_download() inverts it.
 //
 // Activation prep ("xprep").  A Q4_0 dot is evaluated with exact integer
 // arithmetic: each 32-element activation block is written as
@@ -24,10 +25,16 @@
 // the block contributes d * 2^e * (float)that.  The representation keeps 22
 // bits of every block relative to its largest element, so the only rounding
 // beyond the fp32 accumulation is 2^-23 of each block's max |x|.  One xprep
-// record per (token, block) is 32 dwords:
+// record per (token, block) is 28 dwords:
 //   dw[0..8)   digit 0 (byte j of dword i = element 4i + j)
 //   dw[8..16)  digit 1,  dw[16..24) digit 2
-//   dw[24..27) -8 * sum of digit k (int32),  dw[27] 2^e (float),  dw[28..32) 0
+//   dw[24..27) -8 * sum of digit k (int32),  dw[27] 2^e (float)
+// The records of one activation row (a token, or a pair slot's h) are stored
+// as 7 planes of 16 bytes per block: plane q = [Bp blocks][dwords 4q..4q+3],
+// so the seven loads of a wavefront whose lane b needs block b are each one
+// contiguous 1 KiB access.  Row stride: 28 * Bp dwords.  Records of padding
+// blocks are never written; readers zero their scale word (dw 27), so a
+// padding block contributes exactly 0 whatever the scratch held before.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -43,7 +50,7 @@ namespace tqf {
 
 constexpr int kWave = 64;
 constexpr int kRowsPerGroup = 64;  // row padding unit
-constexpr int kXprepDwords = 32;
+constexpr int kXprepDwords = 28;  // per block
 constexpr int kTopK = TQF_HIP_TOP_K;
 constexpr int kMaxTokens = TQF_HIP_MAX_TOKENS;
 constexpr int kMaxExperts = 256;
@@ -76,8 +83,12 @@ inline MatrixDims matrix_dims(uint32_t rows, uint32_t cols) {
     d.lpr = d.blocks_padded < 64 ? d.blocks_padded : 64;
     return d;
 }
-inline size_t nibble_plane_bytes(const MatrixDims &d) {
-    return (size_t)d.rows_padded * d.blocks_padded * 16;
+// Byte offsets of nibble (row, block) and of the f16 scale of (row, block).
+__host__ __device__ inline size_t nibble_offset(const MatrixDims &d, size_t row, size_t block) {
+    return (((row >> 3) * 9 + (row & 7)) * d.blocks_padded + block) * 16;
+}
+__host__ __device__ inline size_t scale_offset(const MatrixDims &d, size_t row, size_t block) {
+    return (((row >> 3) * 9 + 8) * d.blocks_padded + block) * 16 + (row & 7) * 2;
 }
 inline size_t layout_bytes(const MatrixDims &d) {
     return (size_t)d.rows_padded * d.blocks_padded * kQ4Block;
@@ -99,14 +110,12 @@ struct SlotRec {
 };
 static_assert(sizeof(SlotRec) == 32, "slot record is one s_load_dwordx8");
 
-#if defined(__HIP_DEVICE_COMPILE__)
 // Reads a slot record with one 32-byte load, ahead of any use of its fields.
 __device__ __forceinline__ SlotRec load_slot(const SlotRec *p) {
     typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
     const u32x8 v = *reinterpret_cast<const u32x8 *>(p);
     return __builtin_bit_cast(SlotRec, v);
 }
-#endif
 
 struct Plan {
     int32_t n_slots;  // 9 * M when routing succeeded, 0 otherwise

@@ -19,17 +19,15 @@ namespace tqf {
 // block; the destination was zero-filled (padding rows/blocks keep scale 0).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__ aos,
-                                                     uint32_t rows, uint32_t blocks,
-                                                     uint32_t rows_padded, uint32_t bp,
-                                                     uint8_t *__restrict__ dst) {
+                                                     MatrixDims d, uint8_t *__restrict__ dst) {
     const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (uint64_t)rows * blocks) return;
-    const uint32_t r = (uint32_t)(idx / blocks), b = (uint32_t)(idx % blocks);
+    if (idx >= (uint64_t)d.rows * d.blocks) return;
+    const uint32_t r = (uint32_t)(idx / d.blocks), b = (uint32_t)(idx % d.blocks);
     const uint8_t *src = aos + idx * kQ4Block;
-    uint8_t *nib = dst + ((size_t)r * bp + b) * 16;
+    uint8_t *nib = dst + nibble_offset(d, r, b);
 #pragma unroll
     for (int i = 0; i < 16; ++i) nib[i] = src[2 + i];
-    uint8_t *sc = dst + (size_t)rows_padded * bp * 16 + ((size_t)(r / 8) * bp + b) * 16 + (r % 8) * 2;
+    uint8_t *sc = dst + scale_offset(d, r, b);
     sc[0] = src[0];
     sc[1] = src[1];
 }
@@ -39,8 +37,7 @@ hipError_t launch_repack(hipStream_t s, const uint8_t *d_aos, const MatrixDims &
     const uint64_t n = (uint64_t)d.rows * d.blocks;
     if (n == 0) return hipSuccess;
     const uint32_t grid = (uint32_t)((n + 255) / 256);
-    hipLaunchKernelGGL(repack_kernel, dim3(grid), dim3(256), 0, s, d_aos, d.rows, d.blocks,
-                       d.rows_padded, d.blocks_padded, dst);
+    hipLaunchKernelGGL(repack_kernel, dim3(grid), dim3(256), 0, s, d_aos, d, dst);
     return hipGetLastError();
 }
 
@@ -58,7 +55,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ x, 
     const uint32_t j = threadIdx.x & 31;
     const uint32_t col = kb * 32 + j;
     float v[1] = {col < cols ? x[(size_t)t * cols + col] : 0.0f};
-    prep_block<1>(v, (int)j, xprep + ((size_t)t * blocks_padded + kb) * kXprepDwords);
+    prep_block<1>(v, (int)j, xprep + (size_t)t * blocks_padded * kXprepDwords, blocks_padded, kb);
 }
 
 hipError_t launch_prep(hipStream_t s, const float *x, uint32_t m, uint32_t cols,
@@ -72,60 +69,66 @@ hipError_t launch_prep(hipStream_t s, const float *x, uint32_t m, uint32_t cols,
 
 // ---------------------------------------------------------------------------
 // Standalone GEMV / small-M GEMM: y[mat][t][row] for `count` matrices of one
-// shape.  Grid (row groups, count), four wavefronts per workgroup.  Lane
-// group j (LPR lanes) of a wavefront owns NL consecutive rows; lane b of the
-// group reads block b (+ LPR, + 2 LPR, ... for long rows) of each of them, so
-// one wavefront load covers 64/LPR rows with 16 bytes per lane.  Every load
-// of a chunk is issued before any arithmetic; the row sums come out of
-// transpose_reduce, one row per lane.
+// shape.  Grid (row groups, count), eight wavefronts per workgroup.  Lane
+// group j (LPR lanes) of a wavefront owns 8 consecutive rows (one octet);
+// lane b reads block b (+ LPR, + 2 LPR, ... for long rows) of each of them.
+// Per chunk of LPR blocks, every load (8 nibble vectors, the octet's scales
+// and the activation records of up to four tokens) is issued before any
+// arithmetic; the row sums come out of transpose_reduce, one row per lane.
+// Tokens beyond four reuse the weights held in registers.
 // ---------------------------------------------------------------------------
-constexpr int kGemvWaves = 4;
+constexpr int kGemvWaves = 8;
+constexpr int kGemvRows = 8;  // rows per lane group
 
-template <int LPR, int NL, int MT>
+template <int LPR, int TG>
 __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(
     const uint8_t *const *__restrict__ tables, MatrixDims d, const uint32_t *__restrict__ xprep,
     uint32_t m, float *__restrict__ y) {
     constexpr int G = kWave / LPR;
-    constexpr int RW = NL * G;  // rows per wavefront
+    constexpr int RW = kGemvRows * G;  // rows per wavefront
+    constexpr int NL = kGemvRows;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x % kWave;
     const uint32_t j = (uint32_t)lane / LPR, b = (uint32_t)lane % LPR;
     const uint32_t mat = blockIdx.y;
     const uint32_t r0 = (blockIdx.x * kGemvWaves + wave) * RW;
     if (r0 >= d.rows_padded) return;
-    const RowLane W = row_lane(tables[mat], d.rows_padded, d.blocks_padded);
+    const RowLane W = row_lane(tables[mat], d.blocks_padded);
     const uint32_t rl = r0 + j * NL;
-    float acc[MT][NL];
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-        for (int n = 0; n < NL; ++n) acc[t][n] = 0.0f;
-    const uint32_t chunks = d.blocks_padded / LPR;
-    for (uint32_t c = 0; c < chunks; ++c) {
-        const uint32_t blk = c * LPR + b;
-        uint4 nib[NL], sc[NL / 8];
-#pragma unroll
-        for (int n = 0; n < NL; ++n) nib[n] = load_nibbles(W, rl + n, blk);
-#pragma unroll
-        for (int o = 0; o < NL / 8; ++o) sc[o] = load_scales(W, rl / 8 + o, blk);
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            if (t < (int)m) {
-                uint32_t x[28];
-                load_xrec(xprep + ((size_t)t * d.blocks_padded + blk) * kXprepDwords, x);
-#pragma unroll
-                for (int n = 0; n < NL; ++n)
-                    acc[t][n] = fmaf(octet_scale(sc[n / 8], n % 8), q4_block_dot(nib[n], x), acc[t][n]);
-            }
-        }
-    }
     const uint32_t row = rl + reduced_index<LPR, NL>(lane);
     const bool writer = reduced_first_copy<LPR, NL>(lane) && row < d.rows;
+    const uint32_t chunks = d.blocks_padded / LPR;
+    const size_t xstride = (size_t)d.blocks_padded * kXprepDwords;
+    for (uint32_t t0 = 0; t0 < m; t0 += TG) {
+        float acc[TG][NL];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-        if (t < (int)m) {
+        for (int t = 0; t < TG; ++t)
+#pragma unroll
+            for (int n = 0; n < NL; ++n) acc[t][n] = 0.0f;
+        for (uint32_t c = 0; c < chunks; ++c) {
+            const uint32_t blk = c * LPR + b;
+            uint4 nib[NL];
+#pragma unroll
+            for (int n = 0; n < NL; ++n) nib[n] = load_nibbles(W, rl + n, blk);
+            const uint4 sc = load_scales(W, rl / 8, blk);
+            uint32_t x[TG][28];
+#pragma unroll
+            for (int t = 0; t < TG; ++t) {
+                const uint32_t tt = t0 + t < m ? t0 + t : 0;  // loads stay unconditional
+                load_xrec(xprep + tt * xstride, d.blocks_padded, blk, x[t]);
+                if (blk >= d.blocks) x[t][27] = 0;  // padding: exactly 0 whatever it holds
+            }
+            __builtin_amdgcn_sched_barrier(0);  // every load in flight before any math
+#pragma unroll
+            for (int t = 0; t < TG; ++t)
+#pragma unroll
+                for (int n = 0; n < NL; ++n)
+                    acc[t][n] = fmaf(octet_scale(sc, n), q4_block_dot(nib[n], x[t]), acc[t][n]);
+        }
+#pragma unroll
+        for (int t = 0; t < TG; ++t) {
             const float s = transpose_reduce<LPR, NL>(acc[t]);
-            if (writer) y[((size_t)mat * m + t) * d.rows + row] = s;
+            if (writer && t0 + t < m) y[((size_t)mat * m + t0 + t) * d.rows + row] = s;
         }
     }
 }
@@ -133,16 +136,12 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(
 template <int LPR>
 hipError_t launch_gemv_lpr(hipStream_t s, const uint8_t *const *d_tables, uint32_t count,
                            const MatrixDims &d, const uint32_t *xprep, uint32_t m, float *y) {
-    auto go = [&](auto kernel, int rows_per_wave) {
-        const uint32_t rows_per_group = kGemvWaves * rows_per_wave;
-        dim3 grid((d.rows_padded + rows_per_group - 1) / rows_per_group, count);
-        hipLaunchKernelGGL(kernel, grid, dim3(kGemvWaves * kWave), 0, s, d_tables, d, xprep, m, y);
-    };
-    constexpr int G = kWave / LPR;
-    if (m <= 1) go(gemv_kernel<LPR, 16, 1>, 16 * G);
-    else if (m <= 2) go(gemv_kernel<LPR, 8, 2>, 8 * G);
-    else if (m <= 4) go(gemv_kernel<LPR, 8, 4>, 8 * G);
-    else go(gemv_kernel<LPR, 8, 8>, 8 * G);
+    constexpr uint32_t rows_per_group = kGemvWaves * kGemvRows * (kWave / LPR);
+    const dim3 grid((d.rows_padded + rows_per_group - 1) / rows_per_group, count);
+    const dim3 block(kGemvWaves * kWave);
+    if (m <= 1) hipLaunchKernelGGL((gemv_kernel<LPR, 1>), grid, block, 0, s, d_tables, d, xprep, m, y);
+    else if (m <= 2) hipLaunchKernelGGL((gemv_kernel<LPR, 2>), grid, block, 0, s, d_tables, d, xprep, m, y);
+    else hipLaunchKernelGGL((gemv_kernel<LPR, 4>), grid, block, 0, s, d_tables, d, xprep, m, y);
     return hipGetLastError();
 }
 
@@ -267,23 +266,23 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
         const int first = (int)kb * lpb;
         if (tid >= first && tid < first + lpb) {
             for (int t = 0; t < (int)m; ++t) {
-                uint32_t *rec = xprep + ((size_t)t * bp + kb) * kXprepDwords;
+                uint32_t *rec = xprep + (size_t)t * bp * kXprepDwords;
                 if (vpt == 8) {
                     float v8[8];
 #pragma unroll
                     for (int v = 0; v < 8; ++v) v8[v] = x[t][v];
-                    prep_block<8>(v8, tid - first, rec);
+                    prep_block<8>(v8, tid - first, rec, bp, kb);
                 } else if (vpt == 4) {
                     float v4[4];
 #pragma unroll
                     for (int v = 0; v < 4; ++v) v4[v] = x[t][v];
-                    prep_block<4>(v4, tid - first, rec);
+                    prep_block<4>(v4, tid - first, rec, bp, kb);
                 } else if (vpt == 2) {
                     float v2[2] = {x[t][0], x[t][1]};
-                    prep_block<2>(v2, tid - first, rec);
+                    prep_block<2>(v2, tid - first, rec, bp, kb);
                 } else {
                     float v1[1] = {x[t][0]};
-                    prep_block<1>(v1, tid - first, rec);
+                    prep_block<1>(v1, tid - first, rec, bp, kb);
                 }
             }
         }
@@ -507,8 +506,8 @@ __global__ __launch_bounds__(kGateUpWaves * kWave) void gate_up_kernel(
     const int tok = rec.token;
     const uint32_t r0 = (blockIdx.x * kGateUpWaves + wave) * RW;
     if (r0 < rows_padded) {
-        const RowLane Wg = row_lane(rec.mat[0], rows_padded, LPR);
-        const RowLane Wu = row_lane(rec.mat[1], rows_padded, LPR);
+        const RowLane Wg = row_lane(rec.mat[0], LPR);
+        const RowLane Wu = row_lane(rec.mat[1], LPR);
         const uint32_t rl = r0 + j * kGateUpRows;
         uint4 ng[kGateUpRows], nu[kGateUpRows];
 #pragma unroll
@@ -518,7 +517,8 @@ __global__ __launch_bounds__(kGateUpWaves * kWave) void gate_up_kernel(
         }
         const uint4 sg = load_scales(Wg, rl / 8, b), su = load_scales(Wu, rl / 8, b);
         uint32_t x[28];
-        load_xrec(xprep + ((size_t)tok * LPR + b) * kXprepDwords, x);
+        load_xrec(xprep + (size_t)tok * LPR * kXprepDwords, LPR, b, x);
+        if (b >= L.hidden / 32) x[27] = 0;  // padding block: contributes exactly 0
         __builtin_amdgcn_sched_barrier(0);  // every load in flight before any math
         float v[2 * kGateUpRows];
 #pragma unroll
@@ -537,7 +537,8 @@ __global__ __launch_bounds__(kGateUpWaves * kWave) void gate_up_kernel(
         const uint32_t blk = blockIdx.x * (2 * G) + 2 * wave + (uint32_t)(lane >> 5);
         if (blk < L.width / 32) {
             float hv[1] = {s_h[(2 * wave + (lane >> 5)) * 32 + (lane & 31)]};
-            prep_block<1>(hv, lane & 31, hprep + ((size_t)slot * bp_down + blk) * kXprepDwords);
+            prep_block<1>(hv, lane & 31, hprep + (size_t)slot * bp_down * kXprepDwords, bp_down,
+                          blk);
         }
     }
 }
@@ -597,14 +598,15 @@ __global__ __launch_bounds__(kDownSlots * kWave) void down_kernel(
     const int tok = slot < n_slots ? rec.token : -1;
     if (tok >= 0) {
         const float coef = rec.coef;
-        const RowLane W = row_lane(rec.mat[2], rows_padded, LPR);
+        const RowLane W = row_lane(rec.mat[2], LPR);
         const uint32_t rl = r0 + j * kDownRows;
         uint4 nib[kDownRows];
 #pragma unroll
         for (int n = 0; n < kDownRows; ++n) nib[n] = load_nibbles(W, rl + n, b);
         const uint4 s0 = load_scales(W, rl / 8, b), s1 = load_scales(W, rl / 8 + 1, b);
         uint32_t x[28];
-        load_xrec(hprep + ((size_t)slot * LPR + b) * kXprepDwords, x);
+        load_xrec(hprep + (size_t)slot * LPR * kXprepDwords, LPR, b, x);
+        if (b >= L.width / 32) x[27] = 0;  // padding block: contributes exactly 0
         __builtin_amdgcn_sched_barrier(0);  // every load in flight before any math
         float a[kDownRows];
 #pragma unroll

@@ -36,14 +36,12 @@ __device__ __forceinline__ void philox4x32_10(uint32_t c[4], uint32_t k0, uint32
     }
 }
 
-__global__ __launch_bounds__(256) void synth_q4_0_kernel(uint32_t rows, uint32_t blocks,
-                                                         uint32_t rows_padded, uint32_t bp,
-                                                         uint32_t key0,
+__global__ __launch_bounds__(256) void synth_q4_0_kernel(MatrixDims dims, uint32_t key0,
                                                          uint32_t key1,
                                                          uint8_t *__restrict__ tiles) {
     const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (uint64_t)rows * blocks) return;
-    const uint32_t r = (uint32_t)(idx / blocks), b = (uint32_t)(idx % blocks);
+    if (idx >= (uint64_t)dims.rows * dims.blocks) return;
+    const uint32_t r = (uint32_t)(idx / dims.blocks), b = (uint32_t)(idx % dims.blocks);
     uint32_t q[4] = {(uint32_t)idx, (uint32_t)(idx >> 32), 0u, 0u};
     philox4x32_10(q, key0, key1);
     uint32_t s[4] = {(uint32_t)idx, (uint32_t)(idx >> 32), 1u, 0u};
@@ -51,9 +49,8 @@ __global__ __launch_bounds__(256) void synth_q4_0_kernel(uint32_t rows, uint32_t
     const float u = (float)(s[0] >> 8) * 0x1p-24f;
     const float d = 0.005f + 0.015f * u;
     const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)d);
-    *reinterpret_cast<uint4 *>(tiles + ((size_t)r * bp + b) * 16) = make_uint4(q[0], q[1], q[2], q[3]);
-    *reinterpret_cast<uint16_t *>(tiles + (size_t)rows_padded * bp * 16 +
-                                  ((size_t)(r / 8) * bp + b) * 16 + (r % 8) * 2) = h;
+    *reinterpret_cast<uint4 *>(tiles + nibble_offset(dims, r, b)) = make_uint4(q[0], q[1], q[2], q[3]);
+    *reinterpret_cast<uint16_t *>(tiles + scale_offset(dims, r, b)) = h;
 }
 
 hipError_t launch_synth_q4_0(hipStream_t s, const MatrixDims &d, uint32_t tensor_id,
@@ -61,7 +58,7 @@ hipError_t launch_synth_q4_0(hipStream_t s, const MatrixDims &d, uint32_t tensor
     const uint64_t n = (uint64_t)d.rows * (d.cols / 32);
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(synth_q4_0_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s,
-                       d.rows, d.blocks, d.rows_padded, d.blocks_padded, tensor_id, seed, tiles);
+                       d, tensor_id, seed, tiles);
     return hipGetLastError();
 }
 
