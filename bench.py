@@ -187,7 +187,7 @@ def main():
     steps_per_s = args.steps / elapsed
     log(f"bench: graph-replayed verify step {elapsed / args.steps * 1e3:.3f} ms")
 
-    # Kernel timing with HIP events (eager launches on the same stream).
+    # Kernel timing with HIP events on the library stream (eager launches).
     be.profile_enable(True)
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -195,12 +195,33 @@ def main():
     be.synchronize()
     eager_ms = (time.perf_counter() - t0) / args.steps * 1e3
     prof = {}
-    for kind, nm in ((_lib.KERNEL_ROUTE, "route"), (_lib.KERNEL_GATE_UP, "gate_up"),
-                     (_lib.KERNEL_DOWN, "down"), (_lib.KERNEL_ACCEPT, "accept")):
+    for kind, nm in ((_lib.KERNEL_STACK, "stack"), (_lib.KERNEL_ROUTE, "route"),
+                     (_lib.KERNEL_GATE_UP, "gate_up"), (_lib.KERNEL_DOWN, "down"),
+                     (_lib.KERNEL_ACCEPT, "accept")):
         n, ms, by = be.profile_read(kind)
-        prof[nm] = dict(launches=n, avg_us=ms / max(n, 1) * 1e3,
-                        gbs=(by / (ms * 1e-3) / 1e9) if ms > 0 else 0.0, bytes_per_launch=by / max(n, 1))
+        if n:
+            prof[nm] = dict(launches=n, avg_us=ms / n * 1e3, bytes_per_launch=by / n,
+                            gbs=by / (ms * 1e-3) / 1e9 if ms > 0 else 0.0)
     be.profile_enable(False)
+
+    # Algorithmic HBM bytes of one stack pass: every layer's router (f32
+    # [E+1 x H] incl. the shared input gate), RMSNorm weight and the Q4_0
+    # bytes of its (union + shared) experts, from the routes of the same input.
+    d_ids = be.alloc(args.layers * M * 8 * 2)
+    d_tmp = be.alloc(M * H * 4)
+    be.stack_forward_device(st, d_tmp, M, d_ids, d_h_in=d["h0"])
+    ids = be.read(d_ids, np.uint16, (args.layers, M, 8))
+    unions = [len(mtp.routes_union(ids[l])) for l in range(args.layers)]
+    stack_bytes = sum((u + 1) * mtp.expert_bytes_q4_0() + (E + 1) * H * 4 + H * 4
+                      for u in unions) + 2 * M * H * 4
+    accept_bytes = (2 * K + 1) * V * 4
+    if "stack" in prof:
+        prof["stack"]["bytes_per_launch"] = stack_bytes
+        prof["stack"]["gbs"] = stack_bytes / (prof["stack"]["avg_us"] * 1e-6) / 1e9
+    if "accept" in prof:
+        prof["accept"]["bytes_per_launch"] = accept_bytes
+        prof["accept"]["gbs"] = accept_bytes / (prof["accept"]["avg_us"] * 1e-6) / 1e9
+    log(f"bench: mean expert union {np.mean(unions):.2f} (min {min(unions)}, max {max(unions)})")
     log("bench: kernel profile " + json.dumps(prof))
 
     # Config-1 GEMV bandwidth: a rotating pool of distinct 512x2048 matrices
@@ -233,11 +254,11 @@ def main():
                    single_thread_value=res[1])
 
     traffic = None
-    tfile = ROOT / "profiles" / "gate_up_verify_traffic.json"
+    tfile = ROOT / "profiles" / "stack_verify_traffic.json"
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
 
-    gu = prof["gate_up"]
+    dom = prof.get("stack") or prof.get("gate_up")
     line = {
         "metric": "MTP k=3 verify steps/sec + Q4 expert GEMV HBM GB/s (% of peak), 1 GPU",
         "value": steps_per_s,
@@ -260,10 +281,13 @@ def main():
                    "resident_weight_gb": round(args.layers * (E + 1) * 3 * 589824 / 1e9, 2)},
         "effective_tokens_per_s": {str(a): steps_per_s * mtp.expected_tokens_per_step(a, K)
                                    for a in (0.6, 0.8)},
-        "roofline": {"bound": "hbm", "achieved": gu["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": gu["gbs"] / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel": "gate_up_kernel (union-expert gate/up GEMV + SwiGLU)",
-                     "avg_us": gu["avg_us"], "algorithmic_bytes_per_launch": gu["bytes_per_launch"]},
+        "roofline": {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": dom["gbs"] / HBM_PEAK_GBS, "traffic": traffic,
+                     "kernel": "stack_kernel (persistent 40-layer MoE stack: router, union-expert "
+                               "gate/up + SwiGLU, down + combine)",
+                     "avg_us": dom["avg_us"], "algorithmic_bytes_per_launch": dom["bytes_per_launch"]},
+        "expert_union": {"mean": float(np.mean(unions)), "min": int(min(unions)),
+                         "max": int(max(unions))},
         "kernels": prof,
         "gemv_config1": gemv,
         "eager_profiled_ms_per_step": eager_ms,

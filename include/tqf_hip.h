@@ -168,7 +168,11 @@ int32_t tqf_hip_stack_free(tqf_hip_ctx *ctx, tqf_hip_stack *stack);
  * equal d_h to update d_h in place.  d_ids/d_w ([n_layers x m x 8], may be
  * NULL) receive every layer's route; *d_status (may be NULL, zeroed by the
  * caller) is set to TQF_HIP_ERR_ROUTER if any layer's routing fails.
- * Captured once into a HIP graph per argument set and replayed afterwards. */
+ * For m <= 4 on the model geometry (hidden 2048, width <= 2048, <= 256
+ * experts) the whole stack runs as one persistent cooperative launch (a
+ * failed co-scheduling wait reports TQF_HIP_ERR_DEVICE in *d_status);
+ * otherwise the per-layer kernels are captured once into a HIP graph per
+ * argument set and replayed. */
 int32_t tqf_hip_stack_forward_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack,
                                      const float *d_h_in, float *d_h, uint32_t m,
                                      uint16_t *d_ids, float *d_w, int32_t *d_status);
@@ -216,7 +220,8 @@ int32_t tqf_hip_verify_step_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack,
 #define TQF_HIP_KERNEL_DOWN 2     /* union-expert down GEMV + weighted combine */
 #define TQF_HIP_KERNEL_GEMV 3     /* standalone Q4_0 GEMV                     */
 #define TQF_HIP_KERNEL_ACCEPT 4   /* the acceptance kernels, summed           */
-#define TQF_HIP_KERNEL_KINDS 5
+#define TQF_HIP_KERNEL_STACK 5    /* the persistent whole-stack MoE kernel     */
+#define TQF_HIP_KERNEL_KINDS 6
 /* While enabled, eager (non-graph) launches of each kind are bracketed by HIP
  * events on the context stream.  Enabling clears the totals. */
 int32_t tqf_hip_profile_enable(tqf_hip_ctx *ctx, int32_t enable);

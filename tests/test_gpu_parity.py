@@ -367,3 +367,61 @@ def test_small_geometry_layer_matches_committed_golden(backend):
     for t in dev:
         for wt in t:
             backend.free_weights(wt)
+
+
+# ---- the persistent whole-stack kernel ----------------------------------------
+def _stack_run(backend, st, h0, m, n_layers, persistent, with_w=False):
+    import os
+
+    old = os.environ.get("TQF_HIP_PERSISTENT")
+    os.environ["TQF_HIP_PERSISTENT"] = "1" if persistent else "0"
+    try:
+        dh = backend.to_device(h0[:m])
+        dids = backend.alloc(n_layers * m * 8 * 2)
+        dw = backend.alloc(n_layers * m * 8 * 4)
+        dst = backend.to_device(np.zeros(1, np.int32))
+        backend.stack_forward_device(st, dh, m, dids, dw, dst)
+        out = (backend.read(dh, np.float32, (m, 2048)), backend.read(dids, np.uint16, (n_layers, m, 8)),
+               backend.read(dw, np.float32, (n_layers, m, 8)), int(backend.read(dst, np.int32, (1,))[0]))
+        for b in (dh, dids, dw, dst):
+            backend.free(b)
+        return out
+    finally:
+        if old is None:
+            del os.environ["TQF_HIP_PERSISTENT"]
+        else:
+            os.environ["TQF_HIP_PERSISTENT"] = old
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+def test_persistent_stack_matches_oracle_and_layer_kernels(backend, stack3, m):
+    layers, norms, st = stack3
+    h0 = synth.normal((4, 2048), seed=300 + m)
+    h_p, ids_p, w_p, s_p = _stack_run(backend, st, h0, m, 3, True)
+    h_k, ids_k, w_k, s_k = _stack_run(backend, st, h0, m, 3, False)
+    assert s_p == 0 and s_k == 0
+    assert np.array_equal(ids_p, ids_k)
+    assert rel_err(w_p, w_k) < 1e-5
+    assert rel_err(h_p, h_k) < 1e-4
+    hc, routes = oracle_stack(layers, norms, h0[:m])
+    for l in range(3):
+        assert np.array_equal(ids_p[l], routes[l])
+    assert rel_err(h_p, hc) < FFN_TOL
+
+
+def test_persistent_stack_repeats_bit_identically(backend, stack3):
+    """Barrier and team counters return to zero at the end of every launch."""
+    _, _, st = stack3
+    h0 = synth.normal((4, 2048), seed=411)
+    first = _stack_run(backend, st, h0, 4, 3, True)
+    for _ in range(4):
+        again = _stack_run(backend, st, h0, 4, 3, True)
+        assert np.array_equal(again[0], first[0]) and np.array_equal(again[1], first[1])
+
+
+def test_persistent_stack_reports_router_error(backend, stack3):
+    _, _, st = stack3
+    h0 = synth.normal((4, 2048), seed=412)
+    h0[2, 100] = np.inf
+    _, _, _, status = _stack_run(backend, st, h0, 4, 3, True)
+    assert status == ERR_ROUTER

@@ -24,7 +24,8 @@ KERNEL_GATE_UP = 1
 KERNEL_DOWN = 2
 KERNEL_GEMV = 3
 KERNEL_ACCEPT = 4
-KERNEL_KINDS = 5
+KERNEL_STACK = 5
+KERNEL_KINDS = 6
 
 _vp = C.c_void_p
 _i32 = C.c_int32

@@ -176,6 +176,38 @@ int32_t ensure_accept_scratch(tqf_hip_ctx *ctx, size_t bytes) {
     return TQF_HIP_OK;
 }
 
+// Scratch of the persistent stack kernel (sized for kStackMT tokens).
+int32_t ensure_stack_scratch(tqf_hip_ctx *ctx, uint32_t experts, uint32_t bp_down,
+                             uint32_t members) {
+    StackScratch &sc = ctx->stack;
+    if (sc.sync && experts <= sc.experts && bp_down <= sc.bp_down && members <= sc.members)
+        return TQF_HIP_OK;
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    drop_graphs(ctx);
+    experts = std::max(experts, sc.experts);
+    bp_down = std::max(bp_down, sc.bp_down);
+    members = std::max(members, sc.members);
+    (void)hipFree(sc.sync);
+    (void)hipFree(sc.logits);
+    (void)hipFree(sc.xprep);
+    (void)hipFree(sc.hprep);
+    (void)hipFree(sc.partial);
+    (void)hipFree(sc.ssq);
+    sc = StackScratch();
+    TQF_HIP(ctx, hipMalloc(&sc.sync, sizeof(StackSync)));
+    TQF_HIP(ctx, hipMemset(sc.sync, 0, sizeof(StackSync)));
+    TQF_HIP(ctx, hipMalloc(&sc.logits, (size_t)kStackMT * (experts + 1) * 4));
+    TQF_HIP(ctx, hipMalloc(&sc.xprep, (size_t)kStackMT * (kStackHidden / 32) * kXprepDwords * 4));
+    TQF_HIP(ctx, hipMalloc(&sc.hprep, (size_t)kStackMT * (kTopK + 1) * bp_down * kXprepDwords * 4));
+    TQF_HIP(ctx, hipMalloc(&sc.partial, (size_t)kStackTeams * members * kStackMT * 64 * 4));
+    TQF_HIP(ctx, hipMalloc(&sc.ssq, (size_t)kStackTeams * kStackMT * 4));
+    TQF_HIP(ctx, hipMemset(sc.ssq, 0, (size_t)kStackTeams * kStackMT * 4));
+    sc.experts = experts;
+    sc.bp_down = bp_down;
+    sc.members = members;
+    return TQF_HIP_OK;
+}
+
 int32_t ensure_stage(tqf_hip_ctx *ctx, size_t bytes) {
     if (ctx->d_stage && ctx->stage_bytes >= bytes) return TQF_HIP_OK;
     TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -289,6 +321,52 @@ int32_t enqueue_stack(tqf_hip_ctx *ctx, const tqf_hip_stack *st, const float *d_
         int32_t rc = enqueue_layer(ctx, L, in, st->norms[l], m, in, d_h, ids, w, d_status);
         if (rc) return rc;
     }
+    return TQF_HIP_OK;
+}
+
+// The persistent path: model geometry, m <= kStackMT, a device that can
+// co-schedule one workgroup per CU.
+bool stack_persistent_ok(tqf_hip_ctx *ctx, const tqf_hip_stack *st, uint32_t m) {
+    if (std::getenv("TQF_HIP_PERSISTENT") && std::string(std::getenv("TQF_HIP_PERSISTENT")) == "0")
+        return false;
+    if (!st->d_layers || m > (uint32_t)kStackMT || st->hidden != (uint32_t)kStackHidden ||
+        st->experts == 0 || st->experts > 256 || st->width % 256 || st->width > 2048)
+        return false;
+    const uint32_t bp_down = padded_blocks(st->width / 32);
+    if (ctx->stack_grid == 0) ctx->stack_grid = stack_grid(ctx->device, bp_down);
+    return ctx->stack_grid >= (uint32_t)kStackTeams;
+}
+
+int32_t enqueue_stack_persistent(tqf_hip_ctx *ctx, const tqf_hip_stack *st, const float *d_h_in,
+                                 float *d_h, uint32_t m, uint16_t *d_ids, float *d_w,
+                                 int32_t *d_status) {
+    const uint32_t bp_down = padded_blocks(st->width / 32);
+    const uint32_t grid = ctx->stack_grid;
+    const uint32_t members = grid / kStackTeams;
+    if (int32_t rc = ensure_stack_scratch(ctx, st->experts, bp_down, members)) return rc;
+    const StackScratch &sc = ctx->stack;
+    StackArgs a;
+    a.layers = st->d_layers;
+    a.n_layers = (uint32_t)st->layers.size();
+    a.E = st->experts;
+    a.F = st->width;
+    a.m = m;
+    a.h_in = d_h_in ? d_h_in : d_h;
+    a.h = d_h;
+    a.ids_out = d_ids;
+    a.w_out = d_w;
+    a.status = d_status;
+    a.logits = sc.logits;
+    a.xprep = sc.xprep;
+    a.hprep = sc.hprep;
+    a.partial = sc.partial;
+    a.ssq = sc.ssq;
+    a.sync = sc.sync;
+    a.members = members;
+    Prof p(ctx);
+    hipError_t e = launch_stack(ctx->stream, a, grid, bp_down);
+    if (e != hipSuccess) return hip_fail(ctx, "persistent stack kernel launch", e);
+    p.end(TQF_HIP_KERNEL_STACK, 0.0, 0.0, nullptr);
     return TQF_HIP_OK;
 }
 
@@ -410,6 +488,12 @@ extern "C" int32_t tqf_hip_destroy(tqf_hip_ctx *ctx) {
     (void)hipFree(sc.partial);
     (void)hipFree(sc.counters);
     (void)hipFree(sc.accept);
+    (void)hipFree(ctx->stack.sync);
+    (void)hipFree(ctx->stack.logits);
+    (void)hipFree(ctx->stack.xprep);
+    (void)hipFree(ctx->stack.hprep);
+    (void)hipFree(ctx->stack.partial);
+    (void)hipFree(ctx->stack.ssq);
     (void)hipFree(ctx->d_stage);
     (void)hipFree(ctx->d_table);
     (void)hipFree(ctx->d_gemv_xprep);
@@ -914,6 +998,18 @@ extern "C" int32_t tqf_hip_stack_prepare(tqf_hip_ctx *ctx, const tqf_hip_layer *
         st->layers.push_back(L);
         st->norms.push_back(nw->data);
     }
+    std::vector<StackLayer> table(n_layers);
+    for (uint32_t l = 0; l < n_layers; ++l)
+        table[l] = StackLayer{st->layers[l]->dev.router, st->layers[l]->dev.shared_input_gate,
+                              st->norms[l], st->layers[l]->dev.mats};
+    hipError_t e = hipMalloc(&st->d_layers, n_layers * sizeof(StackLayer));
+    if (e == hipSuccess)
+        e = hipMemcpy(st->d_layers, table.data(), n_layers * sizeof(StackLayer), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(st->d_layers);
+        delete st;
+        return hip_fail(ctx, "stack layer table", e);
+    }
     *out = st;
     return TQF_HIP_OK;
 }
@@ -923,6 +1019,7 @@ extern "C" int32_t tqf_hip_stack_free(tqf_hip_ctx *ctx, tqf_hip_stack *stack) {
     if (!stack) return TQF_HIP_OK;
     TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
     drop_graphs(ctx);
+    (void)hipFree(stack->d_layers);
     delete stack;
     return TQF_HIP_OK;
 }
@@ -933,6 +1030,8 @@ extern "C" int32_t tqf_hip_stack_forward_device(tqf_hip_ctx *ctx, const tqf_hip_
     TQF_ENTER(ctx);
     if (!stack || !d_h) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
     if (m == 0 || m > kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "m must be in 1..8");
+    if (stack_persistent_ok(ctx, stack, m))
+        return enqueue_stack_persistent(ctx, stack, d_h_in, d_h, m, d_ids, d_w, d_status);
     if (int32_t rc = ensure_moe_scratch(ctx, stack->hidden, stack->width, stack->experts)) return rc;
     std::vector<uint64_t> key = {1, k64(stack), k64(d_h_in), k64(d_h), m, k64(d_ids), k64(d_w),
                                  k64(d_status)};
@@ -1069,8 +1168,14 @@ extern "C" int32_t tqf_hip_verify_step_device(tqf_hip_ctx *ctx, const tqf_hip_st
     if (int32_t rc = check_accept(ctx, k, vocab, temperature, greedy, d_draft != nullptr,
                                   d_u != nullptr && d_ures != nullptr))
         return rc;
-    if (int32_t rc = ensure_moe_scratch(ctx, stack->hidden, stack->width, stack->experts)) return rc;
     if (int32_t rc = ensure_accept_scratch(ctx, accept_scratch_bytes(k, vocab))) return rc;
+    if (stack_persistent_ok(ctx, stack, m)) {
+        if (int32_t rc = enqueue_stack_persistent(ctx, stack, d_h_in, d_h, m, nullptr, nullptr, nullptr))
+            return rc;
+        return enqueue_accept(ctx, d_target, d_draft, d_dtok, k, vocab, temperature, greedy, d_u,
+                              d_ures, d_accepted, d_tokens);
+    }
+    if (int32_t rc = ensure_moe_scratch(ctx, stack->hidden, stack->width, stack->experts)) return rc;
     uint32_t tbits;
     std::memcpy(&tbits, &temperature, 4);
     std::vector<uint64_t> key = {2,          k64(stack), k64(d_h_in), k64(d_h), m, k64(d_target),

@@ -97,16 +97,23 @@ __device__ __forceinline__ float block_scale(float amax, bool bad, int &e) {
     return __uint_as_float((uint32_t)(e + 127) << 23);
 }
 
-// Balanced base-256 digits of X = rint(x * 2^-e): X = d0 + 256 d1 + 65536 d2.
-__device__ __forceinline__ void split_digits(float x, int e, float scale, int &d0, int &d1,
-                                             int &d2) {
+// X = rint(x * 2^-e) as six balanced base-16 digits d_k in [-8, 7]:
+// X = sum_k d_k 16^k (|X| <= 2^22 < 7 (16^6 - 1) / 15, so six digits suffice).
+__device__ __forceinline__ void split_digits16(float x, int e, float scale, int (&d)[6]) {
     int X = 0;
     if (scale > 0.0f) X = (int)__builtin_rintf(__builtin_ldexpf(x, -e));
-    d0 = (int)(int8_t)(X & 0xFF);
-    int X1 = (X - d0) >> 8;
-    d1 = (int)(int8_t)(X1 & 0xFF);
-    d2 = (X1 - d1) >> 8;
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+        d[k] = ((X + 8) & 15) - 8;
+        X = (X - d[k]) >> 4;
+    }
 }
+// Nibble position of block element j (0..31) in the record's digit dwords:
+// it mirrors the Q4_0 byte order (element j < 16 is the low nibble of qs[j],
+// element j + 16 the high nibble), so dword i of a digit plane pairs with
+// bytes 4i..4i+3 of qs nibble for nibble.
+__device__ __forceinline__ int rec_dword_of(int j) { return (j & 15) >> 2; }
+__device__ __forceinline__ int rec_shift_of(int j) { return 4 * (2 * (j & 3) + (j >> 4)); }
 
 // Address of dword `dw` (0..27) of the record of block b in one activation
 // row's record planes (layout in tqf_internal.h: plane dw/4, block b, word
@@ -117,6 +124,9 @@ __device__ __forceinline__ uint32_t *rec_dw(uint32_t *row, uint32_t bp, uint32_t
 
 // Writes one xprep record for a 32-element block held by a group of
 // 32/EPL lanes (EPL consecutive elements per lane, group-aligned lanes).
+struct OrOp {
+    __device__ int operator()(int a, int b) const { return a | b; }
+};
 template <int EPL>
 __device__ __forceinline__ void prep_block(const float (&v)[EPL], int lane_in_group,
                                            uint32_t *__restrict__ row, uint32_t bp,
@@ -137,71 +147,124 @@ __device__ __forceinline__ void prep_block(const float (&v)[EPL], int lane_in_gr
         badi = group_reduce<LPB>(badi, MaxOp());
     }
     int e;
-    float scale = block_scale(amax, badi != 0, e);
-    int s0 = 0, s1 = 0, s2 = 0;
-    uint32_t pk0[(EPL + 3) / 4] = {}, pk1[(EPL + 3) / 4] = {}, pk2[(EPL + 3) / 4] = {};
+    const float scale = block_scale(amax, badi != 0, e);
+    int part[24];
+#pragma unroll
+    for (int q = 0; q < 24; ++q) part[q] = 0;
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
-        int d0, d1, d2;
-        split_digits(v[i], e, scale, d0, d1, d2);
-        s0 += d0;
-        s1 += d1;
-        s2 += d2;
-        pk0[i / 4] |= ((uint32_t)d0 & 0xFFu) << (8 * (i % 4));
-        pk1[i / 4] |= ((uint32_t)d1 & 0xFFu) << (8 * (i % 4));
-        pk2[i / 4] |= ((uint32_t)d2 & 0xFFu) << (8 * (i % 4));
+        const int j = lane_in_group * EPL + i;
+        int d[6];
+        split_digits16(v[i], e, scale, d);
+        const int dw = rec_dword_of(j), sh = rec_shift_of(j);
+#pragma unroll
+        for (int k = 0; k < 6; ++k)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                part[4 * k + q] |= (q == dw) ? (int)(((uint32_t)d[k] & 15u) << sh) : 0;
     }
     if constexpr (LPB > 1) {
-        s0 = group_reduce<LPB>(s0, AddOp());
-        s1 = group_reduce<LPB>(s1, AddOp());
-        s2 = group_reduce<LPB>(s2, AddOp());
-    }
-    if constexpr (EPL >= 4) {
 #pragma unroll
-        for (int q = 0; q < EPL / 4; ++q) {
-            const int dw = lane_in_group * (EPL / 4) + q;
-            *rec_dw(row, bp, block, dw) = pk0[q];
-            *rec_dw(row, bp, block, 8 + dw) = pk1[q];
-            *rec_dw(row, bp, block, 16 + dw) = pk2[q];
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) {
-            const int j = lane_in_group * EPL + i;  // element 0..31 -> byte j of a digit
-            reinterpret_cast<uint8_t *>(rec_dw(row, bp, block, j >> 2))[j & 3] =
-                (uint8_t)(pk0[0] >> (8 * i));
-            reinterpret_cast<uint8_t *>(rec_dw(row, bp, block, 8 + (j >> 2)))[j & 3] =
-                (uint8_t)(pk1[0] >> (8 * i));
-            reinterpret_cast<uint8_t *>(rec_dw(row, bp, block, 16 + (j >> 2)))[j & 3] =
-                (uint8_t)(pk2[0] >> (8 * i));
-        }
+        for (int q = 0; q < 24; ++q) part[q] = group_reduce<LPB>(part[q], OrOp());
     }
     if (lane_in_group == 0) {
-        *rec_dw(row, bp, block, 24) = (uint32_t)(-8 * s0);
-        *rec_dw(row, bp, block, 25) = (uint32_t)(-8 * s1);
-        *rec_dw(row, bp, block, 26) = (uint32_t)(-8 * s2);
-        *rec_dw(row, bp, block, 27) = __float_as_uint(scale);
+#pragma unroll
+        for (int q = 0; q < 24; ++q) *rec_dw(row, bp, block, q) = (uint32_t)part[q];
+        *rec_dw(row, bp, block, 24) = __float_as_uint(scale);
     }
 }
 
-// sum_j (q_j - 8) * x_j of one Q4_0 block against one xprep record, in fp32.
-// `w` is the block's 16 nibble bytes.  The integer part is exact.
-__device__ __forceinline__ float q4_block_dot(const uint4 w, const uint32_t *__restrict__ xp) {
-    int a0 = (int)xp[24], a1 = (int)xp[25], a2 = (int)xp[26];
-    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t lo = wv[i] & 0x0F0F0F0Fu;
-        const uint32_t hi = (wv[i] >> 4) & 0x0F0F0F0Fu;
-        a0 = __builtin_amdgcn_sdot4((int)lo, (int)xp[i], a0, false);
-        a0 = __builtin_amdgcn_sdot4((int)hi, (int)xp[4 + i], a0, false);
-        a1 = __builtin_amdgcn_sdot4((int)lo, (int)xp[8 + i], a1, false);
-        a1 = __builtin_amdgcn_sdot4((int)hi, (int)xp[12 + i], a1, false);
-        a2 = __builtin_amdgcn_sdot4((int)lo, (int)xp[16 + i], a2, false);
-        a2 = __builtin_amdgcn_sdot4((int)hi, (int)xp[20 + i], a2, false);
+// Store policies for prep_block32: plain stores (the writer's own later
+// kernels read the record) or device-coherent stores (another workgroup of
+// the same persistent kernel reads it after a grid barrier).
+struct PlainStore {
+    __device__ void operator()(uint32_t *p, uint32_t v) const { *p = v; }
+};
+struct CoherentStore {
+    __device__ void operator()(uint32_t *p, uint32_t v) const {
+        __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    const int v = a0 + a1 * 256 + a2 * 65536;
-    return (float)v * __uint_as_float(xp[27]);
+};
+
+// prep_block for one element per lane over an aligned half-wavefront (j =
+// lane & 31); the digit nibbles of the eight elements that share a record
+// dword (a quad and the quad 16 lanes away) are OR-combined across lanes so
+// that the record is written with dword stores only.  `active` (uniform per
+// half) suppresses the stores of a half that carries no block.
+template <typename Store>
+__device__ __forceinline__ void prep_block32(float v, int j, bool active, uint32_t *row,
+                                             uint32_t bp, uint32_t block, Store st) {
+    const float a = fabsf(v);
+    const bool bad = !(a <= 3.402823466e38f);
+    const float amax = group_reduce<32>(bad ? 0.0f : a, MaxOp());
+    const int badi = group_reduce<32>(bad ? 1 : 0, MaxOp());
+    int e;
+    const float scale = block_scale(amax, badi != 0, e);
+    int d[6];
+    split_digits16(v, e, scale, d);
+    const int sh = rec_shift_of(j);
+    int p[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+        p[k] = (int)(((uint32_t)d[k] & 15u) << sh);
+        p[k] |= dpp_i<kDppXor1>(p[k]);
+        p[k] |= dpp_i<kDppXor2>(p[k]);
+        p[k] |= __shfl_xor(p[k], 16);
+    }
+    if (active && (j & 19) == 0) {  // j in {0, 4, 8, 12}: dword j / 4 of every digit
+#pragma unroll
+        for (int k = 0; k < 6; ++k) st(rec_dw(row, bp, block, 4 * k + (j >> 2)), (uint32_t)p[k]);
+    }
+    if (active && j == 0) st(rec_dw(row, bp, block, 24), __float_as_uint(scale));
+}
+
+// Device-coherent 32/64-bit accesses for data exchanged between workgroups
+// of one launch (agent scope: not left in, or served from, one XCD's L2).
+__device__ __forceinline__ void store_coherent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t load_coherent_u64(const uint64_t *p) {
+    return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_own_stores() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+__device__ __forceinline__ uint32_t counter_arrive(uint32_t *c) {
+    return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void counter_reset(uint32_t *c) {
+    __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The 16 nibble bytes of a Q4_0 block as signed int4 (q - 8): q ^ 8 is the
+// 4-bit two's complement of q - 8 for q in 0..15.
+__device__ __forceinline__ uint4 q4_signed(const uint4 w) {
+    return make_uint4(w.x ^ 0x88888888u, w.y ^ 0x88888888u, w.z ^ 0x88888888u, w.w ^ 0x88888888u);
+}
+
+// sum_j (q_j - 8) * x_j of one Q4_0 block against one xprep record, in fp32.
+// `ws` is the block's nibbles after q4_signed: six independent chains of
+// four v_dot8_i32_i4 (one per activation digit), recombined exactly in int32
+// (|sum| <= 32 * 8 * 2^22 = 2^30), then scaled by the record's 2^e.
+__device__ __forceinline__ float q4_block_dot(const uint4 ws, const uint32_t *__restrict__ xp) {
+    const int w4[4] = {(int)ws.x, (int)ws.y, (int)ws.z, (int)ws.w};
+    int acc[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s = __builtin_amdgcn_sdot8(w4[i], (int)xp[4 * k + i], s, false);
+        acc[k] = s;
+    }
+    int v = acc[5];
+#pragma unroll
+    for (int k = 4; k >= 0; --k) v = v * 16 + acc[k];
+    return (float)v * __uint_as_float(xp[24]);
 }
 
 // ---- transpose-reduce: per-lane partial sums of NL rows -> one row per lane
@@ -313,6 +376,18 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 load_global_u4(const void *p) {
     const u32x4 v = *(const __attribute__((address_space(1))) u32x4 *)(p);
     return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float4 load_global_f4(const float *p) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const f32x4 v = *(const __attribute__((address_space(1))) f32x4 *)(p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float load_global_f(const float *p) {
+    return *(const __attribute__((address_space(1))) float *)(p);
+}
+template <typename T>
+__device__ __forceinline__ T load_global_ptr(T const *p) {
+    return *(T const __attribute__((address_space(1))) *)(p);
 }
 __device__ __forceinline__ uint4 load_nibbles(const RowLane &m, uint32_t row, uint32_t block) {
     return load_global_u4(m.base + (((size_t)(row >> 3) * 9 + (row & 7)) * m.bp + block) * 16);

@@ -19,21 +19,23 @@
 // Activation prep ("xprep").  A Q4_0 dot is evaluated with exact integer
 // arithmetic: each 32-element activation block is written as
 //   x_j = X_j * 2^e,  |X_j| <= 2^22,  e chosen per block from max |x_j|
-// and X_j is split into three signed base-256 digits D0 + 256 D1 + 65536 D2.
-// With q_j the nibbles, sum_j (q_j - 8) X_j is three v_dot4_i32_i8 chains
-// (nibbles 0..15 are non-negative int8 lanes) seeded with -8 * sum_j D_kj, and
-// the block contributes d * 2^e * (float)that.  The representation keeps 22
-// bits of every block relative to its largest element, so the only rounding
-// beyond the fp32 accumulation is 2^-23 of each block's max |x|.  One xprep
-// record per (token, block) is 28 dwords:
-//   dw[0..8)   digit 0 (byte j of dword i = element 4i + j)
-//   dw[8..16)  digit 1,  dw[16..24) digit 2
-//   dw[24..27) -8 * sum of digit k (int32),  dw[27] 2^e (float)
+// and X_j is split into six balanced base-16 digits D_kj in [-8, 7]
+// (X = sum_k D_k 16^k).  The weights enter as signed nibbles q - 8 (q ^ 8 is
+// their 4-bit two's complement), so sum_j (q_j - 8) X_j is six chains of
+// four v_dot8_i32_i4, recombined exactly in int32, and the block contributes
+// d * 2^e * (float)that.  The representation keeps 22 bits of every block
+// relative to its largest element, so the only rounding beyond the fp32
+// accumulation is 2^-23 of each block's max |x|.  One xprep record per
+// (token, block) is 28 dwords:
+//   dw[4k .. 4k+4)  digit k (k < 6): the nibble of element j sits in dword
+//                   (j mod 16) / 4 at bit 4 (2 (j mod 4) + j / 16), mirroring
+//                   the Q4_0 nibble order of qs
+//   dw[24]          2^e (float);  dw[25..28) unused
 // The records of one activation row (a token, or a pair slot's h) are stored
 // as 7 planes of 16 bytes per block: plane q = [Bp blocks][dwords 4q..4q+3],
 // so the seven loads of a wavefront whose lane b needs block b are each one
 // contiguous 1 KiB access.  Row stride: 28 * Bp dwords.  Records of padding
-// blocks are never written; readers zero their scale word (dw 27), so a
+// blocks are never written; readers zero their scale word (dw 24), so a
 // padding block contributes exactly 0 whatever the scratch held before.
 #pragma once
 
@@ -186,10 +188,70 @@ struct tqf_hip_layer {
     const uint8_t **d_mats;  // device array owned by the layer
 };
 
+namespace tqf {
+// ---- persistent stack kernel (tqf_stack.hip) -------------------------------
+// One launch runs every layer of a stack: per layer three grid-wide phases
+// (A: RMSNorm + router logits + activation records; B: routing, computed
+// identically by every workgroup, then gate/up per (expert, 32-row block)
+// for all of that expert's tokens; C: down per 64-row team with a
+// deterministic in-team combine and the residual), separated by grid
+// barriers whose waits are time-bounded (a timeout sets `abort`, every
+// workgroup then leaves and the launch reports TQF_HIP_ERR_DEVICE).
+struct StackLayer {
+    const float *router;         // [E x H]
+    const float *gate_vec;       // [H]
+    const float *norm;           // [H]
+    const uint8_t *const *mats;  // [(E + 1) x 3]
+};
+constexpr int kStackMT = 4;        // tokens of one persistent launch (k <= 3)
+constexpr int kStackHidden = 2048; // the persistent kernel's hidden size
+constexpr int kStackTeams = kStackHidden / 64;
+struct StackSync {
+    uint32_t barrier;  // arrivals (atomic adds only)
+    uint32_t exit;
+    uint32_t pad0[30];
+    uint32_t release;  // epoch released by the last arrival, and the abort flag:
+    uint32_t abort;    // one 64-bit poll load, on its own cache line
+    uint32_t pad1[30];
+    uint32_t team[kStackTeams];
+};
+struct StackArgs {
+    const StackLayer *layers;
+    uint32_t n_layers, E, F, m;
+    const float *h_in;
+    float *h;
+    uint16_t *ids_out;
+    float *w_out;
+    int32_t *status;
+    float *logits;      // [kStackMT x (E + 1)]
+    uint32_t *xprep;    // [kStackMT rows of 28 x 64 dwords]
+    uint32_t *hprep;    // [9 kStackMT pair rows of 28 x bp_down dwords]
+    float *partial;     // [teams x members x kStackMT x 64]
+    float *ssq;         // [teams x kStackMT]
+    StackSync *sync;
+    uint32_t members;   // workgroups per 64-row team in phase C
+};
+struct StackScratch {
+    StackSync *sync = nullptr;
+    float *logits = nullptr;
+    uint32_t *xprep = nullptr;
+    uint32_t *hprep = nullptr;
+    float *partial = nullptr;
+    float *ssq = nullptr;
+    uint32_t experts = 0, bp_down = 0, members = 0;
+};
+// Workgroups of a persistent launch (0 if the device cannot co-schedule it)
+// and the launcher; `grid` workgroups must be co-resident (cooperative launch).
+uint32_t stack_grid(int device, uint32_t bp_down);
+hipError_t launch_stack(hipStream_t s, const StackArgs &a, uint32_t grid, uint32_t bp_down);
+size_t stack_lds_bytes(uint32_t bp_down, uint32_t members);
+}  // namespace tqf
+
 struct tqf_hip_stack {
     std::vector<const tqf_hip_layer *> layers;
     std::vector<const float *> norms;
     uint32_t hidden, width, experts;
+    tqf::StackLayer *d_layers = nullptr;  // device copy for the persistent kernel
 };
 
 namespace tqf {
@@ -225,6 +287,9 @@ struct tqf_hip_ctx {
     // one-matrix / one-expert layer tables reused by the non-MoE entry points
     const uint8_t **d_adhoc_mats = nullptr;
     tqf::Plan *d_adhoc_plan = nullptr;
+    // persistent stack kernel
+    tqf::StackScratch stack;
+    uint32_t stack_grid = 0;  // 0: not determined yet
 };
 
 namespace tqf {

@@ -109,14 +109,14 @@ __global__ __launch_bounds__(kGemvWaves * kWave) void gemv_kernel(
             const uint32_t blk = c * LPR + b;
             uint4 nib[NL];
 #pragma unroll
-            for (int n = 0; n < NL; ++n) nib[n] = load_nibbles(W, rl + n, blk);
+            for (int n = 0; n < NL; ++n) nib[n] = q4_signed(load_nibbles(W, rl + n, blk));
             const uint4 sc = load_scales(W, rl / 8, blk);
             uint32_t x[TG][28];
 #pragma unroll
             for (int t = 0; t < TG; ++t) {
                 const uint32_t tt = t0 + t < m ? t0 + t : 0;  // loads stay unconditional
                 load_xrec(xprep + tt * xstride, d.blocks_padded, blk, x[t]);
-                if (blk >= d.blocks) x[t][27] = 0;  // padding: exactly 0 whatever it holds
+                if (blk >= d.blocks) x[t][24] = 0;  // padding: exactly 0 whatever it holds
             }
             __builtin_amdgcn_sched_barrier(0);  // every load in flight before any math
 #pragma unroll
@@ -158,25 +158,9 @@ hipError_t launch_gemv(hipStream_t s, const uint8_t *const *d_tables, uint32_t c
 // atomic stores (coherent at device scope, i.e. not left dirty in one XCD's
 // L2), each thread waits for its stores to complete, and only then is the
 // device-scope counter incremented; the workgroup that sees the final count
-// reads the values back with agent-scope atomic loads.
+// reads the values back with agent-scope atomic loads (store_coherent,
+// load_coherent, wait_own_stores, counter_arrive in tqf_device.h).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void store_coherent(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_coherent(const float *p) {
-    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void wait_own_stores() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-__device__ __forceinline__ uint32_t counter_arrive(uint32_t *c) {
-    return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void counter_reset(uint32_t *c) {
-    __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // ---------------------------------------------------------------------------
 // Block-wide reduction of N floats per thread (256 threads); result valid in
@@ -512,13 +496,13 @@ __global__ __launch_bounds__(kGateUpWaves * kWave) void gate_up_kernel(
         uint4 ng[kGateUpRows], nu[kGateUpRows];
 #pragma unroll
         for (int n = 0; n < kGateUpRows; ++n) {
-            ng[n] = load_nibbles(Wg, rl + n, b);
-            nu[n] = load_nibbles(Wu, rl + n, b);
+            ng[n] = q4_signed(load_nibbles(Wg, rl + n, b));
+            nu[n] = q4_signed(load_nibbles(Wu, rl + n, b));
         }
         const uint4 sg = load_scales(Wg, rl / 8, b), su = load_scales(Wu, rl / 8, b);
         uint32_t x[28];
         load_xrec(xprep + (size_t)tok * LPR * kXprepDwords, LPR, b, x);
-        if (b >= L.hidden / 32) x[27] = 0;  // padding block: contributes exactly 0
+        if (b >= L.hidden / 32) x[24] = 0;  // padding block: contributes exactly 0
         __builtin_amdgcn_sched_barrier(0);  // every load in flight before any math
         float v[2 * kGateUpRows];
 #pragma unroll
@@ -602,11 +586,11 @@ __global__ __launch_bounds__(kDownSlots * kWave) void down_kernel(
         const uint32_t rl = r0 + j * kDownRows;
         uint4 nib[kDownRows];
 #pragma unroll
-        for (int n = 0; n < kDownRows; ++n) nib[n] = load_nibbles(W, rl + n, b);
+        for (int n = 0; n < kDownRows; ++n) nib[n] = q4_signed(load_nibbles(W, rl + n, b));
         const uint4 s0 = load_scales(W, rl / 8, b), s1 = load_scales(W, rl / 8 + 1, b);
         uint32_t x[28];
         load_xrec(hprep + (size_t)slot * LPR * kXprepDwords, LPR, b, x);
-        if (b >= L.width / 32) x[27] = 0;  // padding block: contributes exactly 0
+        if (b >= L.width / 32) x[24] = 0;  // padding block: contributes exactly 0
         __builtin_amdgcn_sched_barrier(0);  // every load in flight before any math
         float a[kDownRows];
 #pragma unroll
