@@ -26,7 +26,8 @@
  *   - Weights use GGML Q4_0 (18-byte blocks of 32: f16 scale, 16 nibble bytes;
  *     element j = (qs[j] & 15) - 8, element j+16 = (qs[j] >> 4) - 8,
  *     format/quant/dequant.rs:110-123).  Upload repacks them losslessly into a
- *     device tile layout; tqf_hip_weights_download() inverts it.
+ *     device row-lane layout (8-row chunks: nibble rows, then their scales);
+ *     tqf_hip_weights_download() inverts it.
  */
 #ifndef TQF_HIP_H
 #define TQF_HIP_H
