@@ -121,6 +121,61 @@ def cpu_baseline(be, layers, host_f32, inputs, budget_s: float):
     return res, threads, n_sample
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix-core peak
+GROUPED_TOKENS = 512
+
+
+def grouped_gemm_bench(be, layer, seed: int, iters: int = 20, cases=("zipf", "dense8")):
+    """Config 5 on one resident layer: 512 bf16 tokens with Zipf(1.1)
+    Gumbel-top-k routes (seed 0), timed per kernel with HIP events; plus the
+    same pair count routed to 8 experts only (every expert M = 512), which
+    isolates the matrix-core rate of the two GEMM kernels."""
+    from turboqwenfare_amd import _lib, mtp, synth
+
+    T = GROUPED_TOKENS
+    x = synth.bf16_round(synth.normal((T, H), seed=seed + 50))
+    zipf_ids, zipf_w = synth.zipf_routes(T, E, 8, 1.1, 0)
+    dense_ids = np.tile(np.arange(8, dtype=np.uint16), (T, 1))
+    dx, dy = be.to_device(x), be.alloc(T * H * 4)
+    flops = 6.0 * H * F * T * 8  # gate + up (2 H F each) + down (2 H F) per pair
+    out = {"tokens": T, "pairs": T * 8, "algorithmic_gflop": flops / 1e9}
+    for name, ids, w in (("zipf", zipf_ids, zipf_w), ("dense8", dense_ids, zipf_w)):
+        if name not in cases:
+            continue
+        dids, dw = be.to_device(ids), be.to_device(w)
+        for _ in range(3):
+            be.grouped_gemm_device(layer, dx, T, dids, dw, dy)
+        be.profile_enable(True)
+        for _ in range(iters):
+            be.grouped_gemm_device(layer, dx, T, dids, dw, dy)
+        per = {}
+        for kind, nm in ((_lib.KERNEL_GROUPED_GATE_UP, "gate_up"),
+                         (_lib.KERNEL_GROUPED_DOWN, "down"), (_lib.KERNEL_GROUPED_AUX, "aux")):
+            n, ms, _ = be.profile_read(kind)
+            per[nm] = ms / iters * 1e3  # us per call (aux: plan + combine)
+        be.profile_enable(False)
+        distinct = len(np.unique(ids))
+        weight_bytes = distinct * mtp.expert_bytes_q4_0()
+        algo_bytes = weight_bytes + T * H * 2 + T * 8 * 6 + T * H * 4
+        total_us = per["gate_up"] + per["down"] + per["aux"]
+        gemm_us = per["gate_up"] + per["down"]
+        out[name] = {
+            "distinct_experts": distinct,
+            "head_expert_pairs": int(np.bincount(ids.reshape(-1).astype(np.int64)).max()),
+            "us": total_us, "kernel_us": per,
+            "algorithmic_bytes": algo_bytes,
+            "hbm_gbs": algo_bytes / (total_us * 1e-6) / 1e9,
+            "hbm_frac": algo_bytes / (total_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "gemm_tflops": flops / (gemm_us * 1e-6) / 1e12,
+            "mfma_util": flops / (gemm_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+        }
+        be.free(dids)
+        be.free(dw)
+    be.free(dx)
+    be.free(dy)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -243,6 +298,8 @@ def main():
     for w in pool:
         be.free_weights(w)
     log("bench: config-1 GEMV pool " + json.dumps(gemv))
+    grouped = grouped_gemm_bench(be, layers[0], args.seed)
+    log("bench: config-5 grouped GEMM " + json.dumps(grouped))
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -290,6 +347,7 @@ def main():
                          "max": int(max(unions))},
         "kernels": prof,
         "gemv_config1": gemv,
+        "grouped_gemm_config5": grouped,
         "eager_profiled_ms_per_step": eager_ms,
         "cpu_baseline": cpu,
     }

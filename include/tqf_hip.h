@@ -204,6 +204,26 @@ int32_t tqf_hip_accept_device(tqf_hip_ctx *ctx, const float *d_target, const flo
 int32_t tqf_hip_top_logit_candidates(tqf_hip_ctx *ctx, const float *logits, uint32_t rows,
                                      uint32_t vocab, uint32_t *tokens4, float *logits4);
 
+/* ---- prefill-shaped grouped expert GEMM: the routed loop of
+ *      Qwen36StreamingMoe::forward_batch (experts/mod.rs:1562-1566, one
+ *      forward_batch_expert :1079-1131 GEMV chain per row and route) over a
+ *      prefill chunk (prefill_chunk, model/qwen36/runtime.rs:265-366), and
+ *      the unused Metal tqf_q4k_gemm (backend/metal/kernels.rs:311-336) -----
+ * x_bf16 [t x hidden], ids [t x 8] (< n_experts), w [t x 8] f32 ->
+ * y [t x hidden] f32 = sum_k w[t,k] * expert_{ids[t,k]}(x_t), summed in route
+ * order (the routed part only: the caller adds the shared expert).  The
+ * (token, k) pairs are sorted by expert on the device and each expert's
+ * gate/up/down run as bf16 matrix-core GEMMs with exact Q4_0 weights and
+ * fp32 accumulation.  1 <= t <= TQF_HIP_GROUPED_MAX_TOKENS. */
+#define TQF_HIP_GROUPED_MAX_TOKENS 4096
+int32_t tqf_hip_grouped_gemm(tqf_hip_ctx *ctx, const tqf_hip_layer *layer, const uint16_t *x_bf16,
+                             uint32_t t, const uint16_t *ids, const float *w, float *y);
+/* Device-pointer form; *d_status (may be NULL, zeroed by the caller) is set
+ * to TQF_HIP_ERR_INVALID if an id is out of range (y is then not written). */
+int32_t tqf_hip_grouped_gemm_device(tqf_hip_ctx *ctx, const tqf_hip_layer *layer,
+                                    const uint16_t *d_x_bf16, uint32_t t, const uint16_t *d_ids,
+                                    const float *d_w, float *d_y, int32_t *d_status);
+
 /* ---- one MTP verify step: the stack over the k+1 verify rows, then the
  *      acceptance, as one stream-ordered (graph-replayed) unit.  The verify
  *      loop the reference leaves unwired (runtime/mtp.rs:1-20). ------------- */
@@ -222,12 +242,17 @@ int32_t tqf_hip_verify_step_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack,
 #define TQF_HIP_KERNEL_GEMV 3     /* standalone Q4_0 GEMV                     */
 #define TQF_HIP_KERNEL_ACCEPT 4   /* the acceptance kernels, summed           */
 #define TQF_HIP_KERNEL_STACK 5    /* the persistent whole-stack MoE kernel     */
-#define TQF_HIP_KERNEL_KINDS 6
+#define TQF_HIP_KERNEL_GROUPED_GATE_UP 6 /* grouped GEMM: gate/up + SwiGLU    */
+#define TQF_HIP_KERNEL_GROUPED_DOWN 7    /* grouped GEMM: down                */
+#define TQF_HIP_KERNEL_GROUPED_AUX 8     /* grouped GEMM: sort plan + combine */
+#define TQF_HIP_KERNEL_KINDS 9
 /* While enabled, eager (non-graph) launches of each kind are bracketed by HIP
  * events on the context stream.  Enabling clears the totals. */
 int32_t tqf_hip_profile_enable(tqf_hip_ctx *ctx, int32_t enable);
 /* Synchronises, then reports launches, summed kernel milliseconds and the
- * summed algorithmic HBM bytes of those launches for one kind. */
+ * summed algorithmic HBM bytes of those launches for one kind (0 for the
+ * grouped GEMM kinds, whose bytes depend on the routes: the caller, who holds
+ * the ids, counts the distinct experts). */
 int32_t tqf_hip_profile_read(tqf_hip_ctx *ctx, int32_t kind, uint64_t *launches,
                              double *total_ms, double *algorithmic_bytes);
 

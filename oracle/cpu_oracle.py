@@ -57,6 +57,7 @@ _SIGS = {
     "orc_xoshiro_next_u64": (_u64, [C.POINTER(_Xoshiro)]),
     "orc_xoshiro_next_f32": (_f32, [C.POINTER(_Xoshiro)]),
     "orc_philox4x32_10": (None, [_vp, _vp, _vp]),
+    "orc_routed_combine": (_i32, [_vp, _vp, _u32, _vp, _vp, _vp, C.c_int]),
     "orc_accept": (_i32, [_vp, _vp, _vp, _u32, _u32, _f32, C.c_int, _vp, _vp, _vp, _vp]),
     "orc_accept_exp": (_f32, [_f32]),
     "orc_fix40": (_u64, [_f32]),
@@ -220,6 +221,20 @@ class MoeLayerHost:
                                        nthreads) != 0:
             raise ValueError("router error")
         return y, ids, w
+
+
+    def routed_combine(self, x: np.ndarray, ids: np.ndarray, w: np.ndarray,
+                       nthreads: int = 1) -> np.ndarray:
+        """y[t] = sum_k w[t,k] * expert_{ids[t,k]}(x[t]) in route order."""
+        x = _f32a(x)
+        ids = np.ascontiguousarray(ids, dtype=np.uint16)
+        w = _f32a(w)
+        t = x.shape[0]
+        y = np.empty((t, self.hidden), dtype=np.float32)
+        if lib().orc_routed_combine(C.byref(self._s), _p(x), t, _p(ids), _p(w), _p(y),
+                                    nthreads) != 0:
+            raise ValueError("expert id out of range")
+        return y
 
 
 def batch_union(ids: np.ndarray) -> list[int]:

@@ -381,6 +381,47 @@ done:
     return rc;
 }
 
+int orc_routed_combine(const orc_moe_layer *L, const float *x, uint32_t t, const uint16_t *ids,
+                       const float *w, float *y, int nthreads)
+{
+    const uint32_t H = L->hidden, F = L->width;
+    if (nthreads < 1) nthreads = 1;
+    for (size_t i = 0; i < (size_t)t * ORC_TOP_K; ++i)
+        if (ids[i] >= L->n_experts) return -1;
+    int bad = 0;
+#ifdef _OPENMP
+#pragma omp parallel num_threads(nthreads) if (nthreads > 1)
+#endif
+    {
+        float *scratch = (float *)malloc(sizeof(float) * (3 * (size_t)F + H));
+        if (!scratch) {
+#ifdef _OPENMP
+#pragma omp atomic write
+#endif
+            bad = 1;
+        } else {
+            float *routed = scratch + 3 * (size_t)F;
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+            for (int64_t r = 0; r < (int64_t)t; ++r) {
+                const float *xt = x + (size_t)r * H;
+                float *out = y + (size_t)r * H;
+                for (uint32_t i = 0; i < H; ++i) out[i] = 0.0f;
+                for (int k = 0; k < ORC_TOP_K; ++k) {
+                    uint32_t e = ids[(size_t)r * ORC_TOP_K + k];
+                    float weight = w[(size_t)r * ORC_TOP_K + k];
+                    expert_forward_nocheck(L->routed_gate[e], L->routed_up[e], L->routed_down[e], H,
+                                           F, xt, routed, scratch);
+                    for (uint32_t i = 0; i < H; ++i) out[i] += routed[i] * weight;
+                }
+            }
+            free(scratch);
+        }
+    }
+    return bad ? -1 : 0;
+}
+
 /* ======================================================================= */
 /* a16: runtime/decode.rs:48-64 -- top_logit_candidates.                    */
 /* ======================================================================= */

@@ -114,6 +114,15 @@ typedef struct orc_moe_layer {
 int orc_moe_forward_batch(const orc_moe_layer *layer, const float *x, uint32_t m,
                           float *y, uint16_t *ids, float *w, int nthreads);
 
+/* The routed accumulate of forward_batch (experts/mod.rs:1562-1566) for
+ * given routes: y[t] = 0, then for k = 0..7 in route order
+ * y[t] += expert_{ids[t,k]}(x_t) * w[t,k] (add_scaled_in_place, weights.rs:
+ * 267-281; expert as weights.rs:566-610).  x, y are [t x hidden]; ids, w
+ * [t x 8].  nthreads > 1 parallelises over tokens (bit-identical).  Returns
+ * 0, or -1 on an id >= n_experts or an allocation failure. */
+int orc_routed_combine(const orc_moe_layer *layer, const float *x, uint32_t t,
+                       const uint16_t *ids, const float *w, float *y, int nthreads);
+
 /* Distinct-expert union of M routes in first-demand order (experts/mod.rs:
  * 268-275 BatchExpertPlan, :937 prepare_batch_route).  Returns the count. */
 uint32_t orc_batch_union(const uint16_t *ids, uint32_t m, uint16_t *out_union);

@@ -127,3 +127,29 @@ def test_synthetic_rejects_bad_cols(bad):
             synth.q4_0_synthetic(2, bad, 0, 0)
     else:
         assert synth.q4_0_synthetic(2, bad, 0, 0).size == 2 * (bad // 32) * 18
+
+
+def test_zipf_routes_definition_and_config5_statistics():
+    # config 5: 512 tokens, Zipf(s=1.1) popularity, Gumbel-top-k without
+    # replacement, seed 0 (head expert M = 448, ~251 distinct, median ~5)
+    ids, w = synth.zipf_routes(512, 256, 8, 1.1, 0)
+    assert ids.shape == (512, 8) and ids.dtype == np.uint16 and w.dtype == np.float32
+    assert all(len(set(r.tolist())) == 8 for r in ids)
+    assert np.all(np.abs(w.sum(axis=1) - 1.0) < 1e-6) and np.all(np.diff(w, axis=1) <= 0)
+    counts = np.bincount(ids.reshape(-1).astype(np.int64), minlength=256)
+    assert counts.max() == 448 and 240 <= int((counts > 0).sum()) <= 256
+    assert 4 <= float(np.median(counts[counts > 0])) <= 8
+    # popularity follows the rank: the head expert is the rank-0 one
+    rank = np.random.default_rng(0).permutation(256)
+    assert int(np.argmax(counts)) == int(np.argmin(rank))
+    a, b = synth.zipf_routes(64, seed=3), synth.zipf_routes(64, seed=3)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+def test_bf16_round_nearest_even_kats():
+    v = np.array([1.0, 1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, -2.5, 3.0e38, 1.0e-40], np.float32)
+    assert synth.bf16_round(v).tolist() == [0x3F80, 0x3F80, 0x3F82, 0xC020, 0x7F62, 0x0001]
+    x = np.random.default_rng(0).standard_normal(1000).astype(np.float32)
+    r = synth.bf16_to_f32(synth.bf16_round(x))
+    assert np.all(np.abs(r - x) <= np.abs(x) * 2.0 ** -8)  # half an ulp of 8 significant bits
+    assert np.array_equal(synth.bf16_to_f32(synth.bf16_round(r)), r)

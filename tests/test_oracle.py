@@ -290,6 +290,51 @@ def test_moe_layer_threaded_equals_serial(small_layer):
         assert np.array_equal(u, v)
 
 
+def test_routed_combine_against_float64_and_its_invariants(small_layer):
+    # experts/mod.rs:1562-1566 for given routes: y = sum_k w_k expert_k(x) in
+    # route order, checked in float64 against independently decoded weights
+    host, _, _, x, mats = small_layer
+    H, F = 256, 256
+    rng = np.random.default_rng(3)
+    t = 5
+    xs = rng.standard_normal((t, H)).astype(np.float32)
+    ids = rng.integers(0, 256, size=(t, 8)).astype(np.uint16)
+    ids[0, 3] = ids[0, 1]  # a repeated expert is computed twice
+    w = rng.random((t, 8)).astype(np.float32)
+    y = host.routed_combine(xs, ids, w)
+    for r in range(t):
+        want = np.zeros(H)
+        for k in range(8):
+            want = want + float(w[r, k]) * np_expert(*mats[int(ids[r, k])], H, F, xs[r])
+        assert np.max(np.abs(y[r] - want) / np.maximum(np.abs(want), 1.0)) < 1e-5
+    # one-hot routes reproduce a single expert exactly
+    oh = np.zeros_like(w)
+    oh[:, 0] = 1.0
+    y1 = host.routed_combine(xs, ids, oh)
+    for r in range(t):
+        e = int(ids[r, 0])
+        assert np.array_equal(y1[r], orc.expert_forward(*mats[e], H, F, xs[r]))
+    # threads do not change a bit; an out-of-range id is an error
+    assert np.array_equal(host.routed_combine(xs, ids, w, nthreads=4), y)
+    bad = ids.copy()
+    bad[2, 2] = 256
+    with pytest.raises(ValueError):
+        host.routed_combine(xs, bad, w)
+
+
+def test_routed_combine_is_the_routed_part_of_the_layer(small_layer):
+    # forward_batch = shared * sigmoid(gate . x) + routed part, with the layer's
+    # own routes (the two differ only in where the fp32 sums start)
+    host, _, gate, x, mats = small_layer
+    y, ids, w = host.forward_batch(x)
+    routed = host.routed_combine(x, ids, w)
+    for t in range(4):
+        sg = orc.sigmoid(float(np.dot(gate.astype(np.float64), x[t].astype(np.float64))))
+        shared = orc.expert_forward(*mats[256], 256, 256, x[t]) * np.float32(sg)
+        want = y[t].astype(np.float64) - shared
+        assert np.max(np.abs(routed[t] - want) / np.maximum(np.abs(want), 1.0)) < 1e-5
+
+
 def test_config1_gemv_matches_golden():
     import sys
     sys.path.insert(0, str(GOLDEN))

@@ -25,7 +25,11 @@ KERNEL_DOWN = 2
 KERNEL_GEMV = 3
 KERNEL_ACCEPT = 4
 KERNEL_STACK = 5
-KERNEL_KINDS = 6
+KERNEL_GROUPED_GATE_UP = 6
+KERNEL_GROUPED_DOWN = 7
+KERNEL_GROUPED_AUX = 8
+KERNEL_KINDS = 9
+GROUPED_MAX_TOKENS = 4096
 
 _vp = C.c_void_p
 _i32 = C.c_int32
@@ -89,6 +93,8 @@ SIGNATURES = {
     "tqf_hip_accept": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _f32, _i32, _vp, _vp, _vp, _vp]),
     "tqf_hip_accept_device": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _f32, _i32, _vp, _vp, _vp, _vp]),
     "tqf_hip_top_logit_candidates": (_i32, [_vp, _vp, _u32, _u32, _vp, _vp]),
+    "tqf_hip_grouped_gemm": (_i32, [_vp, _vp, _vp, _u32, _vp, _vp, _vp]),
+    "tqf_hip_grouped_gemm_device": (_i32, [_vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp]),
     "tqf_hip_verify_step_device": (
         _i32, [_vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _u32, _f32, _i32, _vp, _vp, _vp, _vp]),
     "tqf_hip_profile_enable": (_i32, [_vp, _i32]),

@@ -254,6 +254,29 @@ class HipBackend:
                                                     _ptr(ids), _ptr(w)))
         return y, ids, w
 
+    # ---- grouped expert GEMM (prefill) ---------------------------------------------
+    def grouped_gemm(self, layer: MoeLayer, x_bf16: np.ndarray, ids: np.ndarray,
+                     w: np.ndarray) -> np.ndarray:
+        """x_bf16 [t, hidden] u16, ids [t, 8] u16, w [t, 8] f32 -> y [t, hidden] f32,
+        the route-weighted sum of the routed experts (tqf_hip_grouped_gemm)."""
+        x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+        ids = np.ascontiguousarray(ids, dtype=np.uint16)
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        t = x.shape[0]
+        if x.shape != (t, layer.hidden) or ids.shape != (t, _lib.TOP_K) or w.shape != ids.shape:
+            raise ValueError("grouped_gemm: x [t, hidden], ids and w [t, 8]")
+        y = np.empty((t, layer.hidden), dtype=np.float32)
+        self._check(self.lib.tqf_hip_grouped_gemm(self.ctx, layer.handle, _ptr(x), t, _ptr(ids),
+                                                  _ptr(w), _ptr(y)))
+        return y
+
+    def grouped_gemm_device(self, layer: MoeLayer, d_x: DeviceBuffer, t: int, d_ids: DeviceBuffer,
+                            d_w: DeviceBuffer, d_y: DeviceBuffer,
+                            d_status: DeviceBuffer | None = None) -> None:
+        self._check(self.lib.tqf_hip_grouped_gemm_device(
+            self.ctx, layer.handle, d_x.ptr, t, d_ids.ptr, d_w.ptr, d_y.ptr,
+            d_status.ptr if d_status else None))
+
     # ---- stack / verify step -------------------------------------------------------
     def prepare_stack(self, layers: Sequence[MoeLayer], norms: Sequence[F32Tensor]) -> Stack:
         n = len(layers)

@@ -19,7 +19,8 @@ from pathlib import Path
 PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_PATH = PKG_DIR / "libtqf_hip.so"
-SOURCES = ["tqf_q4.hip", "tqf_stack.hip", "tqf_accept.hip", "tqf_synth.hip", "tqf_api.hip"]
+SOURCES = ["tqf_q4.hip", "tqf_stack.hip", "tqf_grouped.hip", "tqf_accept.hip", "tqf_synth.hip",
+           "tqf_api.hip"]
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
@@ -29,6 +30,10 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
 ]
+# Per-source additions.  The grouped GEMM keeps MFMA results in VGPRs (the
+# per-block fp32 scaling reads every result; accumulators in AGPRs would cost
+# a v_accvgpr_read per value).
+EXTRA_FLAGS = {"tqf_grouped.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def hipcc_path() -> str:
@@ -47,7 +52,7 @@ def build(verbose: bool = False) -> Path:
     procs = []
     for src in SOURCES:
         obj = build_dir / (Path(src).stem + ".o")
-        cmd = [hipcc, *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [hipcc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)]
         procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
         objs.append(obj)
     failed = []

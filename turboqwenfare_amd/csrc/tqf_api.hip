@@ -497,6 +497,7 @@ extern "C" int32_t tqf_hip_destroy(tqf_hip_ctx *ctx) {
     (void)hipFree(ctx->d_stage);
     (void)hipFree(ctx->d_table);
     (void)hipFree(ctx->d_gemv_xprep);
+    (void)hipFree(ctx->d_grouped);
     (void)hipFree(const_cast<const uint8_t **>(ctx->d_adhoc_mats));
     for (Slab &s : ctx->slabs) (void)hipFree(s.base);
     (void)hipHostFree(ctx->prof_ring);
@@ -1146,6 +1147,101 @@ extern "C" int32_t tqf_hip_top_logit_candidates(tqf_hip_ctx *ctx, const float *l
     TQF_HIP(ctx, hipMemcpyAsync(tokens4, dtok, (size_t)rows * 16, hipMemcpyDeviceToHost, ctx->stream));
     TQF_HIP(ctx, hipMemcpyAsync(logits4, dval, (size_t)rows * 16, hipMemcpyDeviceToHost, ctx->stream));
     TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return TQF_HIP_OK;
+}
+
+// ===========================================================================
+// grouped expert GEMM (prefill)
+// ===========================================================================
+namespace {
+int32_t check_grouped(tqf_hip_ctx *ctx, const tqf_hip_layer *layer, uint32_t t) {
+    if (!layer) return fail(ctx, TQF_HIP_ERR_INVALID, "null layer");
+    if (t == 0 || t > TQF_HIP_GROUPED_MAX_TOKENS)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "t must be in 1..TQF_HIP_GROUPED_MAX_TOKENS");
+    const LayerDev &L = layer->dev;
+    if (L.hidden % 256 || L.width % 256 || L.n_experts == 0 || L.n_experts > 256)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "layer geometry unsupported by the grouped GEMM");
+    return TQF_HIP_OK;
+}
+
+int32_t enqueue_grouped(tqf_hip_ctx *ctx, const LayerDev &L, const uint16_t *x, uint32_t t,
+                        const uint16_t *ids, const float *w, float *y, int32_t *status) {
+    const size_t need = grouped_scratch_bytes(t, L.n_experts, L.hidden, L.width);
+    if (!ctx->d_grouped || ctx->grouped_bytes < need) {
+        TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        TQF_HIP(ctx, grow(ctx->d_grouped, ctx->grouped_bytes, need));
+    }
+    const GroupedBuffers g = grouped_buffers(ctx->d_grouped, t, L.n_experts, L.hidden, L.width);
+    const double pairs = (double)t * kTopK;
+    {
+        Prof p(ctx);
+        hipError_t e = launch_grouped_plan(ctx->stream, ids, t, L.n_experts, g, status);
+        if (e != hipSuccess) return hip_fail(ctx, "grouped plan kernel launch", e);
+        p.end(TQF_HIP_KERNEL_GROUPED_AUX, pairs * 2, 0, nullptr);
+    }
+    {
+        Prof p(ctx);
+        hipError_t e = launch_grouped_gate_up(ctx->stream, L, x, g);
+        if (e != hipSuccess) return hip_fail(ctx, "grouped gate/up kernel launch", e);
+        p.end(TQF_HIP_KERNEL_GROUPED_GATE_UP, 0, 0, nullptr);
+    }
+    {
+        Prof p(ctx);
+        hipError_t e = launch_grouped_down(ctx->stream, L, g);
+        if (e != hipSuccess) return hip_fail(ctx, "grouped down kernel launch", e);
+        p.end(TQF_HIP_KERNEL_GROUPED_DOWN, 0, 0, nullptr);
+    }
+    {
+        Prof p(ctx);
+        hipError_t e = launch_grouped_combine(ctx->stream, g, w, t, L.hidden, y);
+        if (e != hipSuccess) return hip_fail(ctx, "grouped combine kernel launch", e);
+        p.end(TQF_HIP_KERNEL_GROUPED_AUX, pairs * (L.hidden * 4.0 + 8) + t * L.hidden * 4.0, 0, nullptr);
+    }
+    return TQF_HIP_OK;
+}
+}  // namespace
+
+extern "C" int32_t tqf_hip_grouped_gemm_device(tqf_hip_ctx *ctx, const tqf_hip_layer *layer,
+                                               const uint16_t *d_x_bf16, uint32_t t,
+                                               const uint16_t *d_ids, const float *d_w,
+                                               float *d_y, int32_t *d_status) {
+    TQF_ENTER(ctx);
+    if (!d_x_bf16 || !d_ids || !d_w || !d_y) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (int32_t rc = check_grouped(ctx, layer, t)) return rc;
+    return enqueue_grouped(ctx, layer->dev, d_x_bf16, t, d_ids, d_w, d_y, d_status);
+}
+
+extern "C" int32_t tqf_hip_grouped_gemm(tqf_hip_ctx *ctx, const tqf_hip_layer *layer,
+                                        const uint16_t *x_bf16, uint32_t t, const uint16_t *ids,
+                                        const float *w, float *y) {
+    TQF_ENTER(ctx);
+    if (!x_bf16 || !ids || !w || !y) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (int32_t rc = check_grouped(ctx, layer, t)) return rc;
+    const LayerDev &L = layer->dev;
+    for (size_t i = 0; i < (size_t)t * kTopK; ++i)
+        if (ids[i] >= L.n_experts) return fail(ctx, TQF_HIP_ERR_INVALID, "expert id out of range");
+    const size_t xb = align_up((size_t)t * L.hidden * 2, kAlign);
+    const size_t ib = align_up((size_t)t * kTopK * 2, kAlign);
+    const size_t wb = align_up((size_t)t * kTopK * 4, kAlign);
+    const size_t yb = align_up((size_t)t * L.hidden * 4, kAlign);
+    if (int32_t rc = ensure_stage(ctx, xb + ib + wb + yb + kAlign)) return rc;
+    uint8_t *base = static_cast<uint8_t *>(ctx->d_stage);
+    uint16_t *dx = reinterpret_cast<uint16_t *>(base);
+    uint16_t *dids = reinterpret_cast<uint16_t *>(base + xb);
+    float *dw = reinterpret_cast<float *>(base + xb + ib);
+    float *dy = reinterpret_cast<float *>(base + xb + ib + wb);
+    int32_t *dstatus = reinterpret_cast<int32_t *>(base + xb + ib + wb + yb);
+    const int32_t zero = 0;
+    TQF_HIP(ctx, hipMemcpyAsync(dstatus, &zero, 4, hipMemcpyHostToDevice, ctx->stream));
+    TQF_HIP(ctx, hipMemcpyAsync(dx, x_bf16, (size_t)t * L.hidden * 2, hipMemcpyHostToDevice, ctx->stream));
+    TQF_HIP(ctx, hipMemcpyAsync(dids, ids, (size_t)t * kTopK * 2, hipMemcpyHostToDevice, ctx->stream));
+    TQF_HIP(ctx, hipMemcpyAsync(dw, w, (size_t)t * kTopK * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (int32_t rc = enqueue_grouped(ctx, L, dx, t, dids, dw, dy, dstatus)) return rc;
+    int32_t status = 0;
+    TQF_HIP(ctx, hipMemcpyAsync(&status, dstatus, 4, hipMemcpyDeviceToHost, ctx->stream));
+    TQF_HIP(ctx, hipMemcpyAsync(y, dy, (size_t)t * L.hidden * 4, hipMemcpyDeviceToHost, ctx->stream));
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (status != 0) return fail(ctx, status, "expert id out of range");
     return TQF_HIP_OK;
 }
 

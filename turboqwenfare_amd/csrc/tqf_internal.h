@@ -290,6 +290,9 @@ struct tqf_hip_ctx {
     // persistent stack kernel
     tqf::StackScratch stack;
     uint32_t stack_grid = 0;  // 0: not determined yet
+    // grouped expert GEMM scratch
+    void *d_grouped = nullptr;
+    size_t grouped_bytes = 0;
 };
 
 namespace tqf {
@@ -331,5 +334,29 @@ hipError_t launch_accept(hipStream_t s, const float *target, const float *draft,
                          int32_t *tokens, void *scratch, hipEvent_t ev_start, hipEvent_t ev_stop);
 hipError_t launch_top4(hipStream_t s, const float *logits, uint32_t rows, uint32_t vocab,
                        uint32_t *tokens4, float *logits4);
+
+// ---- grouped expert GEMM (tqf_grouped.hip) --------------------------------
+// Scratch views of one call over T tokens (P = 8 T pairs): the expert-sorted
+// positions, the tile list, h (bf16 hi and lo, [P x width]) and the
+// per-pair expert outputs ([P x hidden] f32).  Shapes: hidden and width
+// multiples of 256, at most 256 experts.
+struct GroupedBuffers {
+    int32_t *pos_of_pair, *pair_of_pos, *n_tiles;
+    uint2 *tiles;
+    uint16_t *h_hi, *h_lo;
+    float *out;
+    uint32_t tokens, max_tiles;
+};
+size_t grouped_scratch_bytes(uint32_t T, uint32_t E, uint32_t H, uint32_t F);
+GroupedBuffers grouped_buffers(void *scratch, uint32_t T, uint32_t E, uint32_t H, uint32_t F);
+// status (may be null) is set to TQF_HIP_ERR_INVALID when an id is >= E; the
+// later kernels then do nothing.
+hipError_t launch_grouped_plan(hipStream_t s, const uint16_t *ids, uint32_t T, uint32_t E,
+                               const GroupedBuffers &g, int32_t *status);
+hipError_t launch_grouped_gate_up(hipStream_t s, const LayerDev &L, const uint16_t *x_bf16,
+                                  const GroupedBuffers &g);
+hipError_t launch_grouped_down(hipStream_t s, const LayerDev &L, const GroupedBuffers &g);
+hipError_t launch_grouped_combine(hipStream_t s, const GroupedBuffers &g, const float *w,
+                                  uint32_t T, uint32_t H, float *y);
 
 }  // namespace tqf

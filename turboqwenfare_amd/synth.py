@@ -76,3 +76,33 @@ def normal(shape, seed: int, std: float = 1.0) -> np.ndarray:
     """Seeded N(0, std^2) float32 activations / router weights (host only)."""
     rng = np.random.default_rng(seed)
     return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
+
+
+def zipf_routes(tokens: int, n_experts: int = 256, top_k: int = 8, s: float = 1.1,
+                seed: int = 0) -> tuple[np.ndarray, np.ndarray]:
+    """Skewed prefill routes: per token, top_k distinct experts drawn without
+    replacement from a Zipf(s) popularity by Gumbel-top-k (argmax of
+    log p_e + Gumbel noise), with weights softmax-renormalised over the chosen
+    scores (summing to 1 like RouterResult::from_logits).  Expert ranks are a
+    seeded permutation, so the head expert is not expert 0.
+    Returns ids [tokens, top_k] u16 (descending score) and w [tokens, top_k] f32."""
+    rng = np.random.default_rng(seed)
+    rank = rng.permutation(n_experts)
+    logp = -s * np.log(rank.astype(np.float64) + 1.0)
+    scores = logp[None, :] + rng.gumbel(size=(tokens, n_experts))
+    ids = np.argsort(-scores, axis=1, kind="stable")[:, :top_k]
+    sel = np.take_along_axis(scores, ids, axis=1)
+    p = np.exp(sel - sel[:, :1])
+    w = (p / p.sum(axis=1, keepdims=True)).astype(np.float32)
+    return ids.astype(np.uint16), w
+
+
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bit patterns (u16), round to nearest even."""
+    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = (b + np.uint64(0x7FFF) + ((b >> np.uint64(16)) & np.uint64(1))) >> np.uint64(16)
+    return r.astype(np.uint16)
+
+
+def bf16_to_f32(x: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(x, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
