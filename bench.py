@@ -191,7 +191,21 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (torch) and exit: the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--grouped-only", choices=("zipf", "dense8", "both"), default=None,
+                    help="only run the config-5 grouped expert GEMM on one resident layer "
+                         "(the command its rocprofv3 profiles are taken with) and exit")
+    ap.add_argument("--grouped-iters", type=int, default=20)
     args = ap.parse_args()
+    if args.grouped_only:
+        from turboqwenfare_amd.backend import HipBackend
+
+        be = HipBackend(0)
+        layers, _, _ = build_model(be, 1, args.seed)
+        cases = ("zipf", "dense8") if args.grouped_only == "both" else (args.grouped_only,)
+        grouped = grouped_gemm_bench(be, layers[0], args.seed, args.grouped_iters, cases)
+        log("bench: config-5 grouped GEMM " + json.dumps(grouped))
+        be.close()
+        return
     if args.copy_calibration:
         import torch
 

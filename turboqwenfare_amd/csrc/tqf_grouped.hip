@@ -12,13 +12,13 @@
 // Kernels (stream-ordered, no host round trip):
 //   plan     one workgroup: counting sort of the T*8 (token, k) pairs by
 //            expert (stable in pair order), the tile list of 32-pair tiles;
-//   gate_up  grid (F / 64 column groups, tiles): gate and up on bf16 MFMA,
+//   gate_up  grid (F / 128 column blocks, tiles): gate and up on bf16 MFMA,
 //            SwiGLU, h stored as bf16 hi + lo;
-//   down     grid (H / 64 column groups, tiles): down on bf16 MFMA;
+//   down     grid (H / 256 column blocks, tiles): down on bf16 MFMA;
 //   combine  y[t] = sum_k w[t,k] * out[pos(t,k)] in route order.
-// Column group g of a grid row lands on XCD g % 8 (workgroups are dealt to
-// the 8 XCDs round-robin and the group count is a multiple of 8), so every
-// tile of one expert reads the same weight rows through the same L2.
+// (Dealing a tile's column blocks to one XCD, so that they share its
+// activation rows in one L2, measured no faster: the GEMM kernels are bound
+// by per-workgroup latency, not by fetch bandwidth.)
 //
 // Exactness of the weights.  A Q4_0 block is (q - 8) * d with a per-row,
 // per-32-column f16 scale d.  Rounding (q - 8) * d to bf16 would cost 8 bits,
