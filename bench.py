@@ -9,8 +9,9 @@ SwiGLU experts, followed by acceptance sampling over fp32 logits [4, 151936]
 at T = 0.7 with Philox uniforms.  Inputs are resident in HBM before timing.
 
 Prints ONE JSON line (progress goes to stderr).  `value` is verify steps/s.
-The roofline object is for the dominant kernel (union-expert gate/up GEMV)
-timed with HIP events on the library's stream; `cpu_baseline` is the
+The roofline object is for the dominant kernel (the persistent stack kernel,
+one cooperative launch per step) timed with HIP events on the library's
+stream; `cpu_baseline` is the
 reference's scalar path (the C restatement in oracle/) timed on this host's
 cores on a bounded sample of the same workload.
 """
@@ -71,6 +72,16 @@ def verify_inputs(seed: int):
     ur = synth.philox_uniforms(seed, 1, K + 1)
     h0 = synth.normal((M, H), seed=seed + 1)
     return target, draft, dtok, u, ur, h0
+
+
+def host_cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_baseline(be, layers, host_f32, inputs, budget_s: float):
@@ -256,6 +267,17 @@ def main():
     steps_per_s = args.steps / elapsed
     log(f"bench: verify step {elapsed / args.steps * 1e3:.3f} ms")
 
+    # Step-time distribution: each step synchronised on its own (so each
+    # sample also holds one launch + synchronise round trip).
+    per_step = []
+    for _ in range(args.steps):
+        t0 = time.perf_counter()
+        step()
+        be.synchronize()
+        per_step.append((time.perf_counter() - t0) * 1e3)
+    q10, q50, q90 = (float(v) for v in np.percentile(per_step, [10, 50, 90]))
+    log(f"bench: synchronised step p10 {q10:.3f} / median {q50:.3f} / p90 {q90:.3f} ms")
+
     # Kernel timing with HIP events on the library stream (eager launches).
     be.profile_enable(True)
     t0 = time.perf_counter()
@@ -319,6 +341,7 @@ def main():
     if not args.no_cpu_baseline:
         res, threads, n_sample = cpu_baseline(be, layers, host_f32, inputs, args.cpu_budget)
         cpu = dict(value=res[threads], unit="verify steps/s", cores=threads, kind="port",
+                   host_cpu=host_cpu_model(), host_nproc=os.cpu_count(),
                    sample=f"{n_sample} of {args.layers} MoE layers at M=4 plus one acceptance at "
                           f"V={V}, scaled to {args.layers} layers; oracle/tqf_oracle.c -O3 "
                           f"-ffp-contract=off, OpenMP over output rows",
@@ -363,6 +386,7 @@ def main():
         "gemv_config1": gemv,
         "grouped_gemm_config5": grouped,
         "eager_profiled_ms_per_step": eager_ms,
+        "synchronised_step_ms": {"p10": q10, "median": q50, "p90": q90},
         "cpu_baseline": cpu,
     }
     if cpu:
