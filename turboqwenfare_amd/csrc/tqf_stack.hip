@@ -74,6 +74,50 @@ __shared__ float s_h[MT][32];
 __shared__ const uint8_t *s_mats[(256 + 1) * 3];  // the layer's expert matrix table
 extern __shared__ uint4 s_dyn[];
 
+// Phase C's down weights are prefetched into LDS during phase B with direct
+// global -> LDS loads, where they fit: a wavefront's share of one pair is the
+// contiguous octet chunk of its 8 rows (nibbles of 8 rows x LPRD blocks, then
+// their scales: 9 LPRD 16 B), copied byte for byte.  The images sit above
+// every phase's own LDS region.
+template <int LPRD, int MAXP>
+struct DownPrefetch {
+    static constexpr uint32_t kWaveBytes = 9 * LPRD * 16;
+    static constexpr bool kOn = LPRD == 16 && MAXP <= 5;
+    static constexpr uint32_t kBytes = kOn ? MAXP * kWaves * kWaveBytes : 0;
+};
+constexpr uint32_t kPrefOffset = MT * H * 4;  // phase A's h rows, the largest region
+static_assert(MT * 7 * kBpGate * 16 <= kPrefOffset, "phase B region");
+static_assert(5 * 7 * 16 * 16 <= kPrefOffset, "phase C region of the prefetching variant");
+
+// Workgroup barrier for LDS data only: this wavefront's LDS accesses
+// complete (lgkmcnt(0)), then s_barrier.  __syncthreads() would also wait for
+// every outstanding vector-memory operation, including direct global -> LDS
+// loads still in flight, which the gate/up units must not wait for.
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt / expcnt at their maxima, lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Direct global -> LDS copies: lane l's `size` bytes at gaddr land at LDS
+// byte address lds + l * size (m0 holds the wavefront's LDS base).  Issued as
+// inline assembly so that the compiler adds no LDS-alias waits for them:
+// every reader of the destination runs after a full s_waitcnt and a barrier
+// (the grid barrier before phase C).  An operation the compiler does not
+// count can only make its own vmcnt waits stricter, since loads retire in
+// order.
+__device__ __forceinline__ uint32_t lds_addr(uint32_t byte_off) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)(
+               reinterpret_cast<uint8_t *>(s_dyn)) + byte_off;
+}
+__device__ __forceinline__ void copy_to_lds_16(const void *gaddr, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(gaddr) : "memory", "m0");
+}
+__device__ __forceinline__ void copy_to_lds_4(const void *gaddr, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(gaddr) : "memory", "m0");
+}
+
 // Copies n 64-bit words written by other workgroups into LDS: every load of
 // a thread is issued before the first LDS store (one round trip).
 template <int PER_THREAD>
@@ -363,11 +407,46 @@ __device__ void compute_routes(const StackArgs &a) {
     __syncthreads();
 }
 
+// ---- phase B: prefetch of phase C's down weights ------------------------------------
+// This workgroup's phase C share (the same member / pair split as phase_c):
+// per pair, wavefront w's octet chunk of the pair's down matrix into its LDS
+// image.  Issued inside the workgroup's first gate/up unit once its own loads
+// are consumed, so the copies overlap the unit's compute (whose barriers are
+// LDS-only); the grid barrier before phase C drains them.
+template <int LPRD, int MAXP>
+__device__ void prefetch_down(const StackArgs &a) {
+    using PF = DownPrefetch<LPRD, MAXP>;
+    if constexpr (PF::kOn) {
+        const uint32_t K = a.members;
+        const uint32_t tau = blockIdx.x % kStackTeams, k = blockIdx.x / kStackTeams;
+        if (k >= K) return;
+        const int n_pairs = P.n_pairs;
+        const int p0 = (int)(k * n_pairs / K), p1 = (int)((k + 1) * n_pairs / K);
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+        const int lane = threadIdx.x % kWave;
+        const uint32_t octet = tau * 8 + (uint32_t)wave;  // rows tau * 64 + 8 wave ..
+        const uint32_t img = kPrefOffset + (uint32_t)wave * MAXP * PF::kWaveBytes;
+#pragma unroll
+        for (int q = 0; q < MAXP; ++q) {
+            if (p0 + q < p1) {
+                const uint8_t *chunk = s_mats[P.pair_expert[p0 + q] * 3 + 2] + (size_t)octet * PF::kWaveBytes;
+                const uint32_t dst = img + (uint32_t)q * PF::kWaveBytes;
+#pragma unroll
+                for (int i = 0; i < LPRD / 8; ++i)  // nibbles: 1 KiB per instruction
+                    copy_to_lds_16(chunk + i * 1024 + lane * 16, lds_addr(dst + i * 1024));
+#pragma unroll
+                for (int i = 0; i < LPRD / 16; ++i)  // scales: 256 B per instruction
+                    copy_to_lds_4(chunk + 8 * LPRD * 16 + i * 256 + lane * 4, lds_addr(dst + 8 * LPRD * 16 + i * 256));
+            }
+        }
+    }
+}
+
 // ---- phase B: gate/up units ---------------------------------------------------
 // Unit = (group g, rows [32 blk32, +32)) for all of g's tokens.  Wavefront w
 // owns rows 4w..4w+3 of the unit in both matrices.
-template <int LPRD>
-__device__ void gate_up_unit(const StackArgs &a, const StackLayer &L, int unit) {
+template <int LPRD, int MAXP>
+__device__ void gate_up_unit(const StackArgs &a, const StackLayer &L, int unit, bool prefetch) {
     uint4 *s_x = s_dyn;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x % kWave;
@@ -408,7 +487,11 @@ __device__ void gate_up_unit(const StackArgs &a, const StackLayer &L, int unit) 
             if (k < cnt * kRow) dst[k] = v[i];
         }
     }
-    __syncthreads();
+    lds_barrier();
+    // every load of this unit is consumed here (waited for explicitly, on
+    // every path), so no later wait of the unit covers the prefetch's copies
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt / lgkmcnt at their maxima
+    if (prefetch) prefetch_down<LPRD, MAXP>(a);
     for (int i = 0; i < cnt; ++i) {
         uint32_t x[28];
 #pragma unroll
@@ -429,7 +512,7 @@ __device__ void gate_up_unit(const StackArgs &a, const StackLayer &L, int unit) 
         const float up = dpp_f<0x108>(gate);            // row_shl:8
         if ((lane & 15) == 0) s_h[i][4 * wave + (lane >> 4)] = (gate / (1.0f + expf(-gate))) * up;
     }
-    __syncthreads();
+    lds_barrier();
     // h records: two tokens per wavefront
     if (2 * wave < cnt) {
         const int i = 2 * wave + (lane >> 5);
@@ -440,7 +523,7 @@ __device__ void gate_up_unit(const StackArgs &a, const StackLayer &L, int unit) 
                      a.hprep + (size_t)pair * LPRD * kXprepDwords, LPRD, (uint32_t)blk32,
                      CoherentStore());
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // ---- phase C -------------------------------------------------------------------
@@ -464,8 +547,9 @@ __device__ void phase_c(const StackArgs &a, const StackLayer &L, const float *hi
     // every weight load of the member up front (pair index clamped into the
     // member's range), then the h records of its pairs into LDS (7 planes x
     // LPRD blocks each)
+    using PF = DownPrefetch<LPRD, MAXP>;
     uint4 nib[MAXP][RG], sc[MAXP];
-    if (cnt > 0) {
+    if (!PF::kOn && cnt > 0) {
 #pragma unroll
         for (int q = 0; q < MAXP; ++q) {
             const int pq = p0 + (q < cnt ? q : cnt - 1);
@@ -500,6 +584,14 @@ __device__ void phase_c(const StackArgs &a, const StackLayer &L, const float *hi
                 x[4 * qd + 3] = v.w;
             }
             if (pad) x[24] = 0;
+            if constexpr (PF::kOn) {  // this wavefront's image of the pair (prefetch_down)
+                const uint8_t *img = reinterpret_cast<const uint8_t *>(s_dyn) + kPrefOffset +
+                                     ((size_t)wave * MAXP + q) * PF::kWaveBytes;
+#pragma unroll
+                for (int rr = 0; rr < RG; ++rr)
+                    nib[q][rr] = q4_signed(*reinterpret_cast<const uint4 *>(img + ((j * RG + rr) * LPRD + b) * 16));
+                sc[q] = *reinterpret_cast<const uint4 *>(img + 8 * LPRD * 16 + b * 16);
+            }
 #pragma unroll
             for (int rr = 0; rr < RG; ++rr) {
                 const float v = coef * (octet_scale(sc[q], (int)(j * RG) + rr) * q4_block_dot(nib[q][rr], x));
@@ -607,7 +699,12 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
             __hip_atomic_store(a.status, (int32_t)TQF_HIP_ERR_ROUTER, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
         const int n_units = P.n_groups * (int)(a.F / 32);
-        for (int u = blockIdx.x; u < n_units; u += gridDim.x) gate_up_unit<LPRD>(a, L, u);
+        bool prefetch = true;  // with the first unit's loads, or alone
+        for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
+            gate_up_unit<LPRD, MAXP>(a, L, u, prefetch);
+            prefetch = false;
+        }
+        if (prefetch) prefetch_down<LPRD, MAXP>(a);
         if (!(ok = grid_sync(a.sync, epoch, a.status))) break;
         phase_c<LPRD, MAXP>(a, L, hin);
         if (l + 1 < a.n_layers && !(ok = grid_sync(a.sync, epoch, a.status))) break;
@@ -621,7 +718,10 @@ size_t stack_lds_bytes(uint32_t bp_down, uint32_t members) {
     const uint32_t maxp = (MT * (kTopK + 1) + members - 1) / members;
     const size_t c = (size_t)maxp * 7 * bp_down * 16;           // phase C: h records
     size_t m = a > b ? a : b;
-    return m > c ? m : c;
+    m = m > c ? m : c;
+    // the prefetching variant (pick: bp_down 16, maxp <= 5) adds its images
+    if (bp_down == 16 && maxp <= 5) m = (m > kPrefOffset ? m : kPrefOffset) + DownPrefetch<16, 5>::kBytes;
+    return m;
 }
 
 namespace {
@@ -654,6 +754,14 @@ uint32_t stack_grid(int device, uint32_t bp_down) {
     if (members > 16) {  // the team combine reads at most 16 member partials
         members = 16;
         grid = members * kStackTeams;
+    }
+    // dynamic LDS beyond the default limit, set once per context for every
+    // variant this grid can launch (bp_down 16 / 32 / 64)
+    for (uint32_t bp : {16u, 32u, 64u}) {
+        const void *kv = kernel_for(bp, members);
+        if (kv && hipFuncSetAttribute(kv, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)stack_lds_bytes(bp, members)) != hipSuccess)
+            return 0;
     }
     const void *k = kernel_for(bp_down, members);
     if (!k) return 0;
