@@ -334,7 +334,8 @@ bool stack_persistent_ok(tqf_hip_ctx *ctx, const tqf_hip_stack *st, uint32_t m) 
         return false;
     const uint32_t bp_down = padded_blocks(st->width / 32);
     if (ctx->stack_grid == 0) ctx->stack_grid = stack_grid(ctx->device, bp_down);
-    return ctx->stack_grid >= (uint32_t)kStackTeams;
+    // phase A writes the activation records of block q from workgroup q / 2
+    return ctx->stack_grid >= (uint32_t)kStackTeams && ctx->stack_grid >= (uint32_t)kStackMT * 32;
 }
 
 int32_t enqueue_stack_persistent(tqf_hip_ctx *ctx, const tqf_hip_stack *st, const float *d_h_in,
