@@ -12,6 +12,18 @@ __device__ __forceinline__ float f16_to_f32(uint32_t h16) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(h16 & 0xFFFFu));
 }
 
+// Lanes of this wavefront holding the same 9-bit key (a match-any from nine
+// ballots; every lane of the wavefront must take part).
+__device__ __forceinline__ uint64_t match_peers(uint32_t key) {
+    uint64_t peers = ~0ull;
+#pragma unroll
+    for (int bit = 0; bit < 9; ++bit) {
+        const uint64_t m = __ballot((key >> bit) & 1u);
+        peers &= ((key >> bit) & 1u) ? m : ~m;
+    }
+    return peers;
+}
+
 // ---- wavefront reductions with DPP (no LDS round trip) ---------------------
 // gfx9 DPP controls: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1]
 // (lane ^ 2), row_half_mirror (lane i <- 7 - i within 8), row_mirror

@@ -80,18 +80,6 @@ __device__ __forceinline__ void biased_operands(uint32_t c0, uint32_t c1, bf16x8
 // Row of D[v] for this lane.
 __device__ __forceinline__ int d_row(int v, int half) { return 8 * (v / 4) + 4 * half + (v % 4); }
 
-// Lanes of this wavefront holding the same 9-bit key (a match-any from nine
-// ballots).
-__device__ __forceinline__ uint64_t match_peers(uint32_t key) {
-    uint64_t peers = ~0ull;
-#pragma unroll
-    for (int bit = 0; bit < 9; ++bit) {
-        const uint64_t m = __ballot((key >> bit) & 1u);
-        peers &= ((key >> bit) & 1u) ? m : ~m;
-    }
-    return peers;
-}
-
 }  // namespace
 
 // ---- plan: counting sort of the (token, k) pairs by expert ------------------

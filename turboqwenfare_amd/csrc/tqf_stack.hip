@@ -262,8 +262,60 @@ __device__ void phase_a(const StackArgs &a, const StackLayer &L, const float *hi
     }
 }
 
+// ---- phase B: the loads of one gate/up unit ----------------------------------------
+// Wavefront w's rows 4w..4w+3 of the unit in gate and up (one block per lane,
+// raw nibbles) and their scales, held in registers between issue and use.
+constexpr int kRecRow = 7 * kBpGate * 2;  // 64-bit words of one token's records
+constexpr int kRecPer = (MT * kRecRow + kThreads - 1) / kThreads;
+struct UnitLoads {
+    uint4 ng[4], nu[4], sg, su;
+};
+
+__device__ __forceinline__ void unit_loads(const StackArgs &a, int expert, int blk32, UnitLoads &U) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int lane = threadIdx.x % kWave;
+    const RowLane Wg = row_lane(s_mats[expert * 3 + 0], kBpGate), Wu = row_lane(s_mats[expert * 3 + 1], kBpGate);
+    const uint32_t r = (uint32_t)blk32 * 32 + 4 * wave;
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+        U.ng[n] = load_nibbles(Wg, r + n, lane);
+        U.nu[n] = load_nibbles(Wu, r + n, lane);
+    }
+    U.sg = load_scales(Wg, r / 8, lane);
+    U.su = load_scales(Wu, r / 8, lane);
+}
+
+// This workgroup's first unit (blockIdx.x) from the routes alone, before the
+// pair plan exists: its group is the shared expert or the g-th distinct routed
+// expert in first-demand order (the plan's group order).  Every wavefront
+// issues its weight loads, which then fly while wavefront 0 builds the plan.
+// False: the workgroup has no unit.
+__device__ __forceinline__ bool early_unit_loads(const StackArgs &a, UnitLoads &U) {
+    const int lane = threadIdx.x % kWave;
+    const int nb32 = (int)a.F / 32;
+    const int g = (int)blockIdx.x / nb32, blk32 = (int)blockIdx.x % nb32;
+    const int m = (int)a.m, n = m * kTopK;
+    int expert;
+    if (g == 0) {
+        expert = (int)a.E;
+    } else {
+        // route entry i = (t, k) on lane i; other lanes carry distinct dummy keys
+        const int e_i = lane < n ? P.ids[lane / kTopK][lane % kTopK] : 256 + lane;
+        const uint64_t peers = match_peers((uint32_t)e_i);
+        const uint64_t below = (1ull << lane) - 1ull;
+        const uint64_t firsts = __ballot(lane < n && (peers & below) == 0);
+        if (g > __builtin_popcountll(firsts)) return false;
+        uint64_t mk = firsts;
+        for (int r = 1; r < g; ++r) mk &= mk - 1ull;
+        expert = __builtin_amdgcn_readlane(e_i, (int)__builtin_ctzll(mk));
+    }
+    unit_loads(a, expert, blk32, U);
+    return true;
+}
+
 // ---- phase B: routes ------------------------------------------------------------
-__device__ void compute_routes(const StackArgs &a) {
+// `pre`: whether this workgroup's first unit's loads were issued (in `U`).
+__device__ void compute_routes(const StackArgs &a, UnitLoads &U, bool &pre) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x % kWave;
     const uint32_t m = a.m, E = a.E;
@@ -345,6 +397,7 @@ __device__ void compute_routes(const StackArgs &a) {
         }
     }
     __syncthreads();
+    pre = false;
     if (P.bad) {
         if (threadIdx.x == 0) {
             P.n_groups = 0;
@@ -353,6 +406,7 @@ __device__ void compute_routes(const StackArgs &a) {
         __syncthreads();
         return;
     }
+    pre = early_unit_loads(a, U);
     // the pair plan, one route entry i = (t, k) per lane of wavefront 0: the
     // entries of the same expert as bits of one mask (broadcast LDS reads)
     if (wave == 0) {
@@ -445,46 +499,36 @@ __device__ void prefetch_down(const StackArgs &a) {
 // ---- phase B: gate/up units ---------------------------------------------------
 // Unit = (group g, rows [32 blk32, +32)) for all of g's tokens.  Wavefront w
 // owns rows 4w..4w+3 of the unit in both matrices.
+// `preloaded`: U already holds this unit's loads (early_unit_loads).
 template <int LPRD, int MAXP>
-__device__ void gate_up_unit(const StackArgs &a, const StackLayer &L, int unit, bool prefetch) {
+__device__ void gate_up_unit(const StackArgs &a, const StackLayer &L, int unit, bool prefetch,
+                             UnitLoads &U, bool preloaded) {
     uint4 *s_x = s_dyn;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x % kWave;
     const int nb32 = (int)a.F / 32;
     const int g = unit / nb32, blk32 = unit % nb32;
     const int cnt = P.grp_cnt[g];
-    const int expert = P.grp_expert[g];
-    // weights first (HBM), then the activation records of the group's tokens
-    // into LDS (7 planes x 64 blocks each): one round trip for both
-    const uint8_t *gm = s_mats[expert * 3 + 0];
-    const uint8_t *um = s_mats[expert * 3 + 1];
-    const RowLane Wg = row_lane(gm, kBpGate), Wu = row_lane(um, kBpGate);
+    // weights (HBM) and the activation records of the group's tokens: one
+    // round trip for both, issued here unless they are already in flight
+    if (!preloaded) unit_loads(a, P.grp_expert[g], blk32, U);
     const uint32_t r = (uint32_t)blk32 * 32 + 4 * wave;
-    uint4 ng[4], nu[4];
-#pragma unroll
-    for (int n = 0; n < 4; ++n) {
-        ng[n] = q4_signed(load_nibbles(Wg, r + n, lane));
-        nu[n] = q4_signed(load_nibbles(Wu, r + n, lane));
-    }
-    const uint4 sg = load_scales(Wg, r / 8, lane), su = load_scales(Wu, r / 8, lane);
     const int pos = (int)(r & 7);  // 0 or 4
     {
-        constexpr int kRow = 7 * kBpGate * 2;  // 64-bit words of one token's records
-        constexpr int kPer = (MT * kRow + kThreads - 1) / kThreads;
-        uint64_t v[kPer];
+        uint64_t v[kRecPer];
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
+        for (int i = 0; i < kRecPer; ++i) {
             const int k = (int)threadIdx.x + i * kThreads;
-            const int ti = k / kRow, off = k % kRow;
+            const int ti = k / kRecRow, off = k % kRecRow;
             const uint64_t *src = reinterpret_cast<const uint64_t *>(
                 a.xprep + (size_t)P.grp_tok[g][ti < cnt ? ti : 0] * kBpGate * kXprepDwords);
             v[i] = ti < cnt ? load_coherent_u64(src + off) : 0;
         }
-        uint64_t *dst = reinterpret_cast<uint64_t *>(s_x);
+        uint64_t *dst = reinterpret_cast<uint64_t *>(s_x);  // 7 planes x 64 blocks per token
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
+        for (int i = 0; i < kRecPer; ++i) {
             const int k = (int)threadIdx.x + i * kThreads;
-            if (k < cnt * kRow) dst[k] = v[i];
+            if (k < cnt * kRecRow) dst[k] = v[i];
         }
     }
     lds_barrier();
@@ -492,6 +536,13 @@ __device__ void gate_up_unit(const StackArgs &a, const StackLayer &L, int unit, 
     // every path), so no later wait of the unit covers the prefetch's copies
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt / lgkmcnt at their maxima
     if (prefetch) prefetch_down<LPRD, MAXP>(a);
+    uint4 ng[4], nu[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+        ng[n] = q4_signed(U.ng[n]);
+        nu[n] = q4_signed(U.nu[n]);
+    }
+    const uint4 sg = U.sg, su = U.su;
     for (int i = 0; i < cnt; ++i) {
         uint32_t x[28];
 #pragma unroll
@@ -689,7 +740,9 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
             if (k < (a.E + 1) * 3) s_mats[k] = mp[i];
         }
         if (!(ok = grid_sync(a.sync, epoch, a.status))) break;
-        compute_routes(a);
+        UnitLoads U;
+        bool pre;
+        compute_routes(a, U, pre);
         if (blockIdx.x == 0 && threadIdx.x < a.m * kTopK) {
             const uint32_t t = threadIdx.x / kTopK, kk = threadIdx.x % kTopK;
             if (a.ids_out) a.ids_out[((size_t)l * a.m + t) * kTopK + kk] = P.bad ? 0 : (uint16_t)P.ids[t][kk];
@@ -701,7 +754,7 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
         const int n_units = P.n_groups * (int)(a.F / 32);
         bool prefetch = true;  // with the first unit's loads, or alone
         for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
-            gate_up_unit<LPRD, MAXP>(a, L, u, prefetch);
+            gate_up_unit<LPRD, MAXP>(a, L, u, prefetch, U, pre && u == (int)blockIdx.x);
             prefetch = false;
         }
         if (prefetch) prefetch_down<LPRD, MAXP>(a);
