@@ -64,6 +64,12 @@ _SIGS = {
     "orc_fix62": (_u64, [_f32]),
     "orc_u64_to_f32": (_f32, [_u64]),
     "orc_scale_floor": (_u64, [_u64, _f32]),
+    "orc_dequantize_q4_k": (None, [_vp, _vp]),
+    "orc_dequantize_q4_k_indep": (None, [_vp, _vp]),
+    "orc_q4k_gemv": (_i32, [_vp, _u32, _u32, _vp, _vp]),
+    "orc_quantize_q8_k": (None, [_vp, _vp, _vp, _vp]),
+    "orc_q4_k_dot_pre": (_f32, [_vp, _u32, _vp, _vp, _vp]),
+    "orc_q4_k_matvec": (_i32, [_vp, _u32, _u32, _vp, _vp]),
 }
 
 _LIB = None
@@ -320,3 +326,55 @@ def u64_to_f32(v: int) -> float:
 
 def scale_floor(total: int, u: float) -> int:
     return int(lib().orc_scale_floor(total, u))
+
+
+# ---- f1 / a4 / a20: Q4_K -------------------------------------------------------
+Q4_K_BLOCK_BYTES = 144
+Q4_K_BLOCK_ELEMS = 256
+
+
+def dequantize_q4_k(block, independent: bool = False) -> np.ndarray:
+    b = np.ascontiguousarray(np.frombuffer(bytes(block), dtype=np.uint8) if not isinstance(block, np.ndarray)
+                             else block, dtype=np.uint8)
+    out = np.empty(256, dtype=np.float32)
+    fn = lib().orc_dequantize_q4_k_indep if independent else lib().orc_dequantize_q4_k
+    fn(_p(b), _p(out))
+    return out
+
+
+def q4k_gemv(w: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np.ndarray:
+    """backend/reference.rs:61-79: fp32 dequantize-and-accumulate per row."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = _f32a(x)
+    y = np.empty(rows, dtype=np.float32)
+    if lib().orc_q4k_gemv(_p(w), rows, cols, _p(x), _p(y)) != 0:
+        raise ValueError("cols must be a multiple of 256")
+    return y
+
+
+def quantize_q8_k(values) -> tuple[np.ndarray, np.ndarray, float]:
+    v = _f32a(values)
+    assert v.size == 256
+    q = np.empty(256, dtype=np.int8)
+    sums = np.empty(16, dtype=np.int16)
+    scale = np.zeros(1, dtype=np.float32)
+    lib().orc_quantize_q8_k(_p(v), _p(q), _p(sums), _p(scale))
+    return q, sums, float(scale[0])
+
+
+def q4_k_dot_pre(row: np.ndarray, q8: np.ndarray, sums: np.ndarray, scales: np.ndarray) -> float:
+    row = np.ascontiguousarray(row, dtype=np.uint8)
+    q8 = np.ascontiguousarray(q8, dtype=np.int8)
+    sums = np.ascontiguousarray(sums, dtype=np.int16)
+    scales = _f32a(scales)
+    return float(lib().orc_q4_k_dot_pre(_p(row), scales.size, _p(q8), _p(sums), _p(scales)))
+
+
+def q4_k_matvec(w: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np.ndarray:
+    """weights.rs:680-735 with the Q4_K branch: Q8_K activations, integer dot."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = _f32a(x)
+    y = np.empty(rows, dtype=np.float32)
+    if lib().orc_q4_k_matvec(_p(w), rows, cols, _p(x), _p(y)) != 0:
+        raise ValueError("cols must be a multiple of 256")
+    return y

@@ -762,3 +762,188 @@ int orc_accept(const float *target, const float *draft, const int32_t *dtok, uin
     *accepted = (int32_t)istar;
     return 0;
 }
+
+
+/* ======================================================================== */
+/* f1 / a4 / a20: Q4_K                                                      */
+/* ======================================================================== */
+#define ORC_Q4_K_BLOCK_BYTES 144
+#define ORC_Q4_K_BLOCK_ELEMS 256
+
+/* dequant.rs:139-148 -- get_scale_min_k4: the 6-bit (scale, min) of
+ * sub-block j from the 12 packed bytes. */
+static void q4k_scale_min(int j, const uint8_t *q, int *sc, int *mn)
+{
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *mn = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 0x0F) | ((q[j - 4] >> 6) << 4);
+        *mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+/* dequant.rs:154-184 -- pairs of sub-blocks per 64 elements: low nibbles of
+ * 32 bytes, then their high nibbles; value = (d sc) q - (dmin m). */
+void orc_dequantize_q4_k(const uint8_t *block, float *out)
+{
+    const float d = orc_f16_to_f32((uint16_t)(block[0] | (block[1] << 8)));
+    const float dmin = orc_f16_to_f32((uint16_t)(block[2] | (block[3] << 8)));
+    const uint8_t *scales = block + 4, *qs = block + 16;
+    int is = 0, out_idx = 0, q_idx = 0;
+    for (int g = 0; g < 4; ++g) {
+        int sc1, m1, sc2, m2;
+        q4k_scale_min(is, scales, &sc1, &m1);
+        const float d1 = d * (float)sc1, mm1 = dmin * (float)m1;
+        q4k_scale_min(is + 1, scales, &sc2, &m2);
+        const float d2 = d * (float)sc2, mm2 = dmin * (float)m2;
+        for (int l = 0; l < 32; ++l) out[out_idx + l] = d1 * (float)(qs[q_idx + l] & 0x0F) - mm1;
+        for (int l = 0; l < 32; ++l) out[out_idx + 32 + l] = d2 * (float)(qs[q_idx + l] >> 4) - mm2;
+        out_idx += 64;
+        q_idx += 32;
+        is += 2;
+    }
+}
+
+/* validate.rs:97-126 -- each sub-block j located from j alone (group j / 2,
+ * nibble half j % 2), with the independent f16 decoder. */
+void orc_dequantize_q4_k_indep(const uint8_t *block, float *out)
+{
+    const float d = orc_f16_to_f32_indep((uint16_t)(block[0] | (block[1] << 8)));
+    const float dmin = orc_f16_to_f32_indep((uint16_t)(block[2] | (block[3] << 8)));
+    const uint8_t *s = block + 4, *qs = block + 16;
+    for (int j = 0; j < 8; ++j) {
+        const int sc = j < 4 ? (s[j] & 63) : ((s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4));
+        const int m = j < 4 ? (s[j + 4] & 63) : ((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+        const float dj = d * (float)sc, mj = dmin * (float)m;
+        const int group = j / 2, half = j % 2;
+        for (int l = 0; l < 32; ++l) {
+            const uint8_t byte = qs[group * 32 + l];
+            const int nib = half == 0 ? (byte & 0x0F) : (byte >> 4);
+            out[group * 64 + half * 32 + l] = dj * (float)nib - mj;
+        }
+    }
+}
+
+/* backend/reference.rs:61-79 -- acc starts at 0.0 and takes every element
+ * of the row in order (a plain loop, not an iterator sum). */
+int orc_q4k_gemv(const uint8_t *w, uint32_t rows, uint32_t cols, const float *x, float *y)
+{
+    if (cols % ORC_Q4_K_BLOCK_ELEMS != 0) return -1;
+    const uint32_t bpr = cols / ORC_Q4_K_BLOCK_ELEMS;
+    float dq[ORC_Q4_K_BLOCK_ELEMS];
+    for (uint32_t r = 0; r < rows; ++r) {
+        float acc = 0.0f;
+        for (uint32_t b = 0; b < bpr; ++b) {
+            orc_dequantize_q4_k(w + ((size_t)r * bpr + b) * ORC_Q4_K_BLOCK_BYTES, dq);
+            const float *v = x + (size_t)b * ORC_Q4_K_BLOCK_ELEMS;
+            for (int i = 0; i < ORC_Q4_K_BLOCK_ELEMS; ++i) acc += dq[i] * v[i];
+        }
+        y[r] = acc;
+    }
+    return 0;
+}
+
+/* weights.rs:898-931 -- the signed value of largest magnitude (first on
+ * ties) maps to -127; values round half to even; .min(127) then `as i8`. */
+void orc_quantize_q8_k(const float *values, int8_t *q, int16_t *sums, float *scale)
+{
+    float smax = 0.0f, amax = 0.0f;
+    for (int i = 0; i < 256; ++i) {
+        const float a = fabsf(values[i]);
+        if (a > amax) {
+            amax = a;
+            smax = values[i];
+        }
+    }
+    if (amax == 0.0f) {
+        memset(q, 0, 256);
+        memset(sums, 0, 16 * sizeof(int16_t));
+        *scale = 0.0f;
+        return;
+    }
+    const float inv = -127.0f / smax;
+    *scale = 1.0f / inv;
+    for (int i = 0; i < 256; ++i) {
+        float t = nearbyintf(values[i] * inv); /* round_ties_even (default mode) */
+        if (t > 127.0f) t = 127.0f;
+        if (t < -128.0f) t = -128.0f;          /* `as i8` saturates */
+        q[i] = (int8_t)t;
+    }
+    for (int j = 0; j < 16; ++j) {
+        int s = 0;
+        for (int i = 0; i < 16; ++i) s += q[16 * j + i];
+        sums[j] = (int16_t)s;
+    }
+}
+
+/* weights.rs:944-1021 -- integer lane sums (lane = element index mod 8 within
+ * each quarter of a sub-block), then the f32 combination in the reference's
+ * order: sums[lane] += (d * q8scale) * lane_sum; minimum_sum -= (dmin *
+ * q8scale) * block_minimum_sum; result = minimum_sum + sum(sums). */
+float orc_q4_k_dot_pre(const uint8_t *row, uint32_t nblocks, const int8_t *q8, const int16_t *sums,
+                       const float *scales)
+{
+    float lane_acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float minimum_sum = 0.0f;
+    for (uint32_t b = 0; b < nblocks; ++b) {
+        const uint8_t *w = row + (size_t)b * ORC_Q4_K_BLOCK_BYTES;
+        const float ws = orc_f16_to_f32((uint16_t)(w[0] | (w[1] << 8)));
+        const float ms = orc_f16_to_f32((uint16_t)(w[2] | (w[3] << 8)));
+        const uint8_t *packed = w + 4, *vals = w + 16;
+        const int8_t *qb = q8 + (size_t)b * 256;
+        const int16_t *sb = sums + (size_t)b * 16;
+        int32_t bms = 0;
+        for (int k = 0; k < 8; ++k) {
+            int sc, mn;
+            q4k_scale_min(k, packed, &sc, &mn);
+            bms += mn * ((int32_t)sb[2 * k] + (int32_t)sb[2 * k + 1]);
+        }
+        int8_t unp[256];
+        for (int c = 0; c < 4; ++c)
+            for (int i = 0; i < 32; ++i) {
+                unp[c * 64 + i] = (int8_t)(vals[c * 32 + i] & 0x0F);
+                unp[c * 64 + 32 + i] = (int8_t)(vals[c * 32 + i] >> 4);
+            }
+        int32_t lane_sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int k = 0; k < 8; ++k) {
+            int sc, mn;
+            q4k_scale_min(k, packed, &sc, &mn);
+            for (int quarter = 0; quarter < 4; ++quarter)
+                for (int lane = 0; lane < 8; ++lane) {
+                    const int idx = k * 32 + quarter * 8 + lane;
+                    lane_sums[lane] += sc * (int32_t)qb[idx] * (int32_t)unp[idx];
+                }
+        }
+        const float combined = ws * scales[b];
+        for (int lane = 0; lane < 8; ++lane) lane_acc[lane] += combined * (float)lane_sums[lane];
+        minimum_sum -= ms * scales[b] * (float)bms;
+    }
+    float total = -0.0f; /* Iterator::sum::<f32>() seed */
+    for (int lane = 0; lane < 8; ++lane) total += lane_acc[lane];
+    return minimum_sum + total;
+}
+
+/* weights.rs:680-735 -- quantize x once per 256-element chunk, then one
+ * q4_k_dot_pre per row. */
+int orc_q4_k_matvec(const uint8_t *w, uint32_t rows, uint32_t cols, const float *x, float *y)
+{
+    if (cols % ORC_Q4_K_BLOCK_ELEMS != 0) return -1;
+    const uint32_t nb = cols / ORC_Q4_K_BLOCK_ELEMS;
+    int8_t *q8 = (int8_t *)malloc((size_t)nb * 256);
+    int16_t *sums = (int16_t *)malloc((size_t)nb * 16 * sizeof(int16_t));
+    float *scales = (float *)malloc((size_t)nb * sizeof(float));
+    if (!q8 || !sums || !scales) {
+        free(q8);
+        free(sums);
+        free(scales);
+        return -1;
+    }
+    for (uint32_t b = 0; b < nb; ++b) orc_quantize_q8_k(x + (size_t)b * 256, q8 + (size_t)b * 256, sums + (size_t)b * 16, &scales[b]);
+    for (uint32_t r = 0; r < rows; ++r)
+        y[r] = orc_q4_k_dot_pre(w + (size_t)r * nb * ORC_Q4_K_BLOCK_BYTES, nb, q8, sums, scales);
+    free(q8);
+    free(sums);
+    free(scales);
+    return 0;
+}

@@ -176,6 +176,36 @@ uint64_t orc_fix62(float v);                 /* floor(v * 2^62), v in [0,1]  */
 float orc_u64_to_f32(uint64_t v);            /* round to nearest even        */
 uint64_t orc_scale_floor(uint64_t total, float u); /* floor(total * u) exact */
 
+/* ---- f1 / a4 / a20: Q4_K (144-byte super-blocks of 256) --------------- */
+/* dequant.rs:139-184 (get_scale_min_k4, dequantize_q4_k).  Pinned:
+ * dequant.rs:287-306 KAT; validate.rs:289-298 byte pattern i*19+3 against the
+ * independent decoder below; one-hot probes through orc_q4k_gemv. */
+void orc_dequantize_q4_k(const uint8_t *block144, float *out256);
+/* validate.rs:97-126 (sub-blocks walked directly, independent f16). */
+void orc_dequantize_q4_k_indep(const uint8_t *block144, float *out256);
+/* backend/reference.rs:61-79 q4k_gemv: rows x (cols/256) blocks row-major;
+ * one fp32 accumulator per row over every dequantized element in order.
+ * Returns 0, or -1 if cols is not a multiple of 256.  Pinned: float64 brute
+ * force on the reference's LCG fixture (backend/metal/kernels.rs:1118-1138)
+ * and random blocks; one-hot columns recover orc_dequantize_q4_k exactly
+ * (kernels.rs:1168-1196). */
+int orc_q4k_gemv(const uint8_t *w, uint32_t rows, uint32_t cols, const float *x, float *y);
+/* weights.rs:898-931 quantize_q8_k over one 256-element chunk: values q[256],
+ * per-16 sums[16], scale.  Pinned: closed forms (the largest |v| maps to
+ * -127, ties round to even, a zero chunk gives scale 0), numpy sums. */
+void orc_quantize_q8_k(const float *values256, int8_t *q256, int16_t *sums16, float *scale);
+/* weights.rs:933-1021 q4_k_dot_pre (the scalar lane loop; the NEON path is
+ * bit-identical to it) of one row of nblocks blocks against pre-quantized
+ * chunks (q8 [nblocks x 256], sums [nblocks x 16], scales [nblocks]).
+ * Pinned: float64 evaluation of the same integer terms. */
+float orc_q4_k_dot_pre(const uint8_t *row, uint32_t nblocks, const int8_t *q8, const int16_t *sums,
+                       const float *scales);
+/* weights.rs:680-735: Q8_K quantization of x per 256-element chunk (hoisted
+ * out of the row loop), then q4_k_dot_pre per row.  Returns 0, or -1 if cols
+ * is not a multiple of 256.  Pinned: composition of the two above; agrees
+ * with orc_q4k_gemv to the Q8_K quantization error. */
+int orc_q4_k_matvec(const uint8_t *w, uint32_t rows, uint32_t cols, const float *x, float *y);
+
 #ifdef __cplusplus
 }
 #endif

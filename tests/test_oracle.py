@@ -519,3 +519,166 @@ def test_accept_matches_golden():
             assert a == g["accept_len"][gi, seed]
             assert toks == list(g["accept_tokens"][gi, seed, : a + 1])
     assert set(g["accept_len"][0]) == {0, 1, 2, 3} and set(g["accept_len"][1]) == {0, 1, 2, 3}
+
+
+# ---- f1 / a4 / a20: Q4_K ------------------------------------------------------
+def lcg_q4_k_weights(rows: int, cols: int) -> np.ndarray:
+    """The reference's Q4_K fixture (backend/metal/kernels.rs:1118-1132):
+    d = 1.0, dmin = 0.25, every other byte from the LCG
+    counter = counter * 1103515245 + 12345 (u32), byte = counter >> 16."""
+    n_blocks = rows * (cols // 256)
+    out = np.zeros((n_blocks, 144), np.uint8)
+    counter = 1
+    for b in range(n_blocks):
+        out[b, 0:2] = (0x00, 0x3C)
+        out[b, 2:4] = (0x00, 0x34)
+        for i in range(4, 144):
+            counter = (counter * 1_103_515_245 + 12_345) & 0xFFFFFFFF
+            out[b, i] = (counter >> 16) & 0xFF
+    return out.reshape(-1)
+
+
+def lcg_vector(cols: int) -> np.ndarray:
+    """kernels.rs:1134-1138: ((i % 11) * 0.3 - 1.5) in f32."""
+    return np.array([np.float32(i % 11) * np.float32(0.3) - np.float32(1.5) for i in range(cols)], np.float32)
+
+
+def q4_k_exact(block: np.ndarray) -> np.ndarray:
+    """The decoded values as exact rationals in float64: d sc q - dmin m with
+    d, dmin the f16 fields (numpy binary16) and the 6-bit (sc, m) of each
+    sub-block from the 12 packed bytes."""
+    b = np.asarray(block, np.uint8)
+    d = float(b[0:2].view(np.float16)[0])
+    dmin = float(b[2:4].view(np.float16)[0])
+    s = [int(v) for v in b[4:16]]
+    out = np.zeros(256)
+    for j in range(8):
+        if j < 4:
+            sc, m = s[j] & 63, s[j + 4] & 63
+        else:
+            sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4)
+            m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4)
+        qs = b[16 + 32 * (j // 2): 16 + 32 * (j // 2) + 32].astype(np.int64)
+        q = (qs & 0xF) if j % 2 == 0 else (qs >> 4)
+        out[64 * (j // 2) + 32 * (j % 2): 64 * (j // 2) + 32 * (j % 2) + 32] = d * sc * q - dmin * m
+    return out
+
+
+def test_q4_k_dequant_kat():
+    # dequant.rs:287-306: d = 1, dmin = 0, every sub-block scale 1, qs[0] = 0x12
+    b = np.zeros(144, np.uint8)
+    b[0:2] = (0x00, 0x3C)
+    b[4:8] = 1
+    b[8:12] = 1
+    b[16] = 0x12
+    for indep in (False, True):
+        out = orc.dequantize_q4_k(b, independent=indep)
+        assert out[0] == 2.0 and out[32] == 1.0 and out[1] == 0.0
+
+
+def test_q4_k_primary_equals_independent():
+    # validate.rs:289-298: the byte pattern i * 19 + 3, then random blocks
+    blk = np.array([(i * 19 + 3) & 0xFF for i in range(144)], np.uint8)
+    assert np.array_equal(orc.dequantize_q4_k(blk), orc.dequantize_q4_k(blk, independent=True))
+    rng = np.random.default_rng(41)
+    for _ in range(300):
+        blk = rng.integers(0, 256, 144).astype(np.uint8)
+        blk[1] &= 0x7B  # finite f16 d and dmin (exponent below all-ones)
+        blk[3] &= 0x7B
+        a, b = orc.dequantize_q4_k(blk), orc.dequantize_q4_k(blk, independent=True)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_q4_k_dequant_is_the_once_rounded_exact_value():
+    # every fp32 step before the final subtraction is exact (d sc needs 17
+    # bits, (d sc) q 21, dmin m 17), so each value is the exact decode
+    # rounded once to f32
+    rng = np.random.default_rng(42)
+    blocks = [lcg_q4_k_weights(1, 256)] + [rng.integers(0, 256, 144).astype(np.uint8) for _ in range(200)]
+    for blk in blocks:
+        blk = blk.copy()
+        blk[1] &= 0x7B
+        blk[3] &= 0x7B
+        assert np.array_equal(orc.dequantize_q4_k(blk), q4_k_exact(blk).astype(np.float32))
+
+
+def test_q4k_gemv_reference_fixture_against_float64():
+    # kernels.rs:1140-1165 shape (17 x 512) and fixture; float64 brute force
+    rows, cols = 17, 512
+    w = lcg_q4_k_weights(rows, cols)
+    x = lcg_vector(cols)
+    y = orc.q4k_gemv(w, rows, cols, x)
+    dq = np.concatenate([q4_k_exact(w[i * 144:(i + 1) * 144]) for i in range(rows * 2)]).reshape(rows, cols)
+    want = dq @ x.astype(np.float64)
+    assert np.max(np.abs(y - want) / np.maximum(np.abs(want), 1.0)) < 1e-5
+    # the reference's own test bound against its Metal kernel is 1e-2 absolute
+    assert np.max(np.abs(y - want)) < 1e-2
+
+
+def test_q4k_gemv_one_hot_columns_recover_the_decode():
+    # kernels.rs:1168-1196: a one-hot input selects one decoded element
+    w = lcg_q4_k_weights(1, 256)
+    dq = orc.dequantize_q4_k(w)
+    for k in range(256):
+        x = np.zeros(256, np.float32)
+        x[k] = 1.0
+        assert orc.q4k_gemv(w, 1, 256, x)[0] == dq[k]
+    with pytest.raises(ValueError):
+        orc.q4k_gemv(w, 1, 200, np.zeros(200, np.float32))
+
+
+def test_quantize_q8_k_closed_forms():
+    q, sums, scale = orc.quantize_q8_k(np.zeros(256, np.float32))
+    assert scale == 0.0 and not q.any() and not sums.any()
+    rng = np.random.default_rng(43)
+    v = rng.standard_normal(256).astype(np.float32)
+    i_max = int(np.argmax(np.abs(v)))
+    q, sums, scale = orc.quantize_q8_k(v)
+    assert q[i_max] == -127  # the largest magnitude maps to -127 (sign folded into the scale)
+    assert np.array_equal(sums, q.astype(np.int64).reshape(16, 16).sum(axis=1).astype(np.int16))
+    assert np.max(np.abs(q.astype(np.float64) * scale - v)) <= abs(scale) / 2 * (1 + 1e-6)
+    # signed maximum -127 -> inverse scale exactly 1: ties round to even
+    t = np.zeros(256, np.float32)
+    t[0] = -127.0
+    t[1:7] = (2.5, 3.5, -2.5, -3.5, 0.5, 126.5)
+    q, _, scale = orc.quantize_q8_k(t)
+    assert scale == 1.0
+    assert list(q[:7]) == [-127, 2, 4, -2, -4, 0, 126]
+
+
+def test_q4_k_dot_pre_against_float64_of_its_integer_terms():
+    rng = np.random.default_rng(44)
+    nb = 3
+    row = rng.integers(0, 256, nb * 144).astype(np.uint8)
+    for b in range(nb):
+        row[b * 144 + 1] &= 0x3B  # modest finite d, dmin
+        row[b * 144 + 3] &= 0x3B
+    x = rng.standard_normal(nb * 256).astype(np.float32)
+    qs, ss, scs = zip(*(orc.quantize_q8_k(x[b * 256:(b + 1) * 256]) for b in range(nb)))
+    q8, sums, scales = np.concatenate(qs), np.concatenate(ss), np.array(scs, np.float32)
+    got = orc.q4_k_dot_pre(row, q8, sums, scales)
+    want = 0.0
+    for b in range(nb):
+        blk = row[b * 144:(b + 1) * 144]
+        d = float(blk[0:2].view(np.float16)[0])
+        dmin = float(blk[2:4].view(np.float16)[0])
+        # d sc q - dmin m summed against q8, times the Q8_K scale, exactly
+        dq_over = q4_k_exact(blk)  # d sc q - dmin m
+        want += float(scales[b]) * float(np.dot(dq_over, q8[b * 256:(b + 1) * 256].astype(np.float64)))
+    assert abs(got - want) <= 1e-5 * max(abs(want), 1.0)
+
+
+def test_q4_k_matvec_within_the_q8_k_rounding_bound():
+    # each activation moves by at most half its chunk's Q8_K step, so the
+    # integer path sits within sum_b |scale_b|/2 * sum_i |w_i| of the fp32 GEMV
+    rng = np.random.default_rng(45)
+    rows, cols = 8, 512
+    w = lcg_q4_k_weights(rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    a = orc.q4_k_matvec(w, rows, cols, x)
+    b = orc.q4k_gemv(w, rows, cols, x)
+    steps = np.array([orc.quantize_q8_k(x[c * 256:(c + 1) * 256])[2] for c in range(cols // 256)])
+    for r in range(rows):
+        dq = np.concatenate([q4_k_exact(w[(r * 2 + c) * 144:(r * 2 + c + 1) * 144]) for c in range(2)])
+        bound = sum(abs(steps[c]) / 2 * np.abs(dq[c * 256:(c + 1) * 256]).sum() for c in range(2))
+        assert abs(float(a[r]) - float(b[r])) <= bound * 1.001 + 1e-3
