@@ -187,6 +187,43 @@ def grouped_gemm_bench(be, layer, seed: int, iters: int = 20, cases=("zipf", "de
     return out
 
 
+def q4k_pool_bench(be, pool_size: int, seed: int, iters: int = 10):
+    """Canonical Q4_K GEMVs at the config-1 shape (512 x 2048, m = 1) over a
+    rotating pool of distinct device matrices (one launch reads every one):
+    the fp32-semantics GEMV (backend::reference::q4k_gemv) and the Q8_K
+    integer matvec (matvec_payload / q4_k_dot_pre).  Every pool matrix is a
+    device copy of one seeded Q4_K matrix with f16 d, dmin in [0.002, 0.05)."""
+    from turboqwenfare_amd import _lib, synth
+
+    rng = np.random.default_rng(seed)
+    n = 512 * (2048 // 256)
+    blk = rng.integers(0, 256, size=(n, 144), dtype=np.uint8)
+    blk[:, 0:2] = rng.uniform(0.002, 0.05, n).astype(np.float16).view(np.uint8).reshape(n, 2)
+    blk[:, 2:4] = rng.uniform(0.002, 0.05, n).astype(np.float16).view(np.uint8).reshape(n, 2)
+    host = blk.reshape(-1)
+    pool = [be.upload_q4_k(host, 512, 2048) for _ in range(pool_size)]
+    dx = be.to_device(synth.normal((2048,), seed=seed))
+    dy = be.alloc(pool_size * 512 * 4)
+    out = {}
+    for name, fn, kind in (("gemv_fp32", be.q4k_gemv_batched_device, _lib.KERNEL_Q4K_GEMV),
+                           ("matvec_q8k", be.q4k_matvec_batched_device, _lib.KERNEL_Q4K_MATVEC)):
+        fn(pool, dx, dy)
+        be.profile_enable(True)
+        for _ in range(iters):
+            fn(pool, dx, dy)
+        n_l, ms, by = be.profile_read(kind)
+        be.profile_enable(False)
+        r = dict(matrices=pool_size, bytes_per_launch=by / n_l, avg_us=ms / n_l * 1e3,
+                 gbs=by / (ms * 1e-3) / 1e9)
+        r["frac"] = r["gbs"] / HBM_PEAK_GBS
+        out[name] = r
+    for w in pool:
+        be.free_weights(w)
+    be.free(dx)
+    be.free(dy)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -206,7 +243,18 @@ def main():
                     help="only run the config-5 grouped expert GEMM on one resident layer "
                          "(the command its rocprofv3 profiles are taken with) and exit")
     ap.add_argument("--grouped-iters", type=int, default=20)
+    ap.add_argument("--q4k-only", action="store_true",
+                    help="only run the Q4_K config-1 GEMV pools (the command their rocprofv3 "
+                         "profiles are taken with) and exit")
     args = ap.parse_args()
+    if args.q4k_only:
+        from turboqwenfare_amd.backend import HipBackend
+
+        be = HipBackend(0)
+        log("bench: Q4_K config-1 pools " + json.dumps(q4k_pool_bench(be, args.gemv_pool,
+                                                                      args.seed)))
+        be.close()
+        return
     if args.grouped_only:
         from turboqwenfare_amd.backend import HipBackend
 
@@ -334,6 +382,8 @@ def main():
     for w in pool:
         be.free_weights(w)
     log("bench: config-1 GEMV pool " + json.dumps(gemv))
+    q4k = q4k_pool_bench(be, args.gemv_pool, args.seed)
+    log("bench: Q4_K config-1 pools " + json.dumps(q4k))
     grouped = grouped_gemm_bench(be, layers[0], args.seed)
     log("bench: config-5 grouped GEMM " + json.dumps(grouped))
 
@@ -384,6 +434,7 @@ def main():
                          "max": int(max(unions))},
         "kernels": prof,
         "gemv_config1": gemv,
+        "q4k_config1": q4k,
         "grouped_gemm_config5": grouped,
         "eager_profiled_ms_per_step": eager_ms,
         "synchronised_step_ms": {"p10": q10, "median": q50, "p90": q90},

@@ -100,7 +100,7 @@ int32_t tqf_hip_tensor_upload(tqf_hip_ctx *ctx, const float *data, size_t count,
 int32_t tqf_hip_tensor_free(tqf_hip_ctx *ctx, tqf_hip_tensor *t);
 
 /* ---- Q4_0 GEMV / small-M GEMM ------------------------------------------- */
-/* Replaces backend::reference::q4k_gemv/q4k_gemm (backend/reference.rs:61-92)
+/* Replaces backend::reference::q4k_gemv/q4k_gemm (backend/reference.rs:49-81)
  * and metal::kernels::q4k_gemv_persistent_weights (kernels.rs:565-593) for
  * Q4_0 (matvec_row, model/qwen36/weights.rs:827-843).  x is [m x cols] f32,
  * y is [m x rows] f32, 1 <= m <= TQF_HIP_MAX_TOKENS. */
@@ -224,6 +224,62 @@ int32_t tqf_hip_grouped_gemm_device(tqf_hip_ctx *ctx, const tqf_hip_layer *layer
                                     const uint16_t *d_x_bf16, uint32_t t, const uint16_t *d_ids,
                                     const float *d_w, float *d_y, int32_t *d_status);
 
+/* ---- canonical Q4_K matrices (GGML 144-byte super-blocks of 256 elements,
+ *      format/quant/dequant.rs:139-184): the format of the checkpoint's
+ *      routed experts (LoadedQwen36Expert::payload_parts, model/qwen36/
+ *      weights.rs:552-561) ------------------------------------------------- */
+/* A handle from these uploads is a tqf_hip_weights of format Q4_K: only the
+ * q4k entry points accept it (the Q4_0 ones reject it, and vice versa). */
+#define TQF_HIP_FORMAT_Q4_0 0
+#define TQF_HIP_FORMAT_Q4_K 1
+/* Device bytes of a Q4_K upload of this shape; 0 unless cols is a positive
+ * multiple of 256. */
+uint64_t tqf_hip_q4k_weights_bytes_for(uint32_t rows, uint32_t cols);
+/* `q4_k` is rows x (cols/256) row-major 144-byte super-blocks; len must equal
+ * rows*(cols/256)*144.  Lossless repack (GpuResidentExpert::upload,
+ * backend/metal/expert.rs:110-147, for one matrix). */
+int32_t tqf_hip_q4k_weights_upload(tqf_hip_ctx *ctx, const uint8_t *q4_k, size_t len,
+                                   uint32_t rows, uint32_t cols, tqf_hip_weights **out);
+int32_t tqf_hip_q4k_weights_upload_device(tqf_hip_ctx *ctx, const void *d_q4_k, size_t len,
+                                          uint32_t rows, uint32_t cols, tqf_hip_weights **out);
+/* Inverse repack back to the GGML Q4_K bytes (format/quant/validate.rs:
+ * 148-250's "reorder only if the values are proven unchanged"). */
+int32_t tqf_hip_q4k_weights_download(tqf_hip_ctx *ctx, const tqf_hip_weights *w, uint8_t *q4_k,
+                                     size_t len);
+/* fp32 semantics of backend::reference::q4k_gemv / q4k_gemm (backend/
+ * reference.rs:49-81) and of the Metal tqf_q4k_gemv (backend/metal/
+ * kernels.rs:535-593): y[t][r] = sum_i dequant(w[r])_i x[t][i].  x [m x cols],
+ * y [m x rows] f32, 1 <= m <= TQF_HIP_MAX_TOKENS.  Within 2^-22 of each
+ * 32-element block's largest |x| per product; fp32 accumulation. */
+int32_t tqf_hip_q4k_gemv(tqf_hip_ctx *ctx, const tqf_hip_weights *w, const float *x, uint32_t m,
+                         float *y);
+int32_t tqf_hip_q4k_gemv_device(tqf_hip_ctx *ctx, const tqf_hip_weights *w, const float *d_x,
+                                uint32_t m, float *d_y);
+/* `count` same-shape Q4_K matrices against one x [cols]: d_y [count x rows]. */
+int32_t tqf_hip_q4k_gemv_batched_device(tqf_hip_ctx *ctx, const tqf_hip_weights *const *ws,
+                                        uint32_t count, const float *d_x, float *d_y);
+/* The checkpoint's CPU matvec, matvec_payload for GgmlType::Q4K (model/
+ * qwen36/weights.rs:680-735): quantize_q8_k per 256-element chunk of each x
+ * row (:898-931), then q4_k_dot_pre per output row (:944-1021).  Bit-identical
+ * to that scalar code (NaN as NaN).  Shapes as tqf_hip_q4k_gemv. */
+int32_t tqf_hip_q4k_matvec(tqf_hip_ctx *ctx, const tqf_hip_weights *w, const float *x, uint32_t m,
+                           float *y);
+int32_t tqf_hip_q4k_matvec_device(tqf_hip_ctx *ctx, const tqf_hip_weights *w, const float *d_x,
+                                  uint32_t m, float *d_y);
+int32_t tqf_hip_q4k_matvec_batched_device(tqf_hip_ctx *ctx, const tqf_hip_weights *const *ws,
+                                          uint32_t count, const float *d_x, float *d_y);
+/* LoadedQwen36Expert::forward (weights.rs:566-610) over m rows: gate and up
+ * Q4_K matvecs ([width x hidden]), silu_mul (weights.rs:241-260), down
+ * matvec ([hidden x width]), each matvec with the Q8_K semantics above.
+ * x [m x hidden], y [m x hidden] f32. */
+int32_t tqf_hip_q4k_expert_forward(tqf_hip_ctx *ctx, const tqf_hip_weights *gate,
+                                   const tqf_hip_weights *up, const tqf_hip_weights *down,
+                                   const float *x, uint32_t m, float *y);
+int32_t tqf_hip_q4k_expert_forward_device(tqf_hip_ctx *ctx, const tqf_hip_weights *gate,
+                                          const tqf_hip_weights *up,
+                                          const tqf_hip_weights *down, const float *d_x,
+                                          uint32_t m, float *d_y);
+
 /* ---- one MTP verify step: the stack over the k+1 verify rows, then the
  *      acceptance, as one stream-ordered (graph-replayed) unit.  The verify
  *      loop the reference leaves unwired (runtime/mtp.rs:1-20). ------------- */
@@ -245,7 +301,9 @@ int32_t tqf_hip_verify_step_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack,
 #define TQF_HIP_KERNEL_GROUPED_GATE_UP 6 /* grouped GEMM: gate/up + SwiGLU    */
 #define TQF_HIP_KERNEL_GROUPED_DOWN 7    /* grouped GEMM: down                */
 #define TQF_HIP_KERNEL_GROUPED_AUX 8     /* grouped GEMM: sort plan + combine */
-#define TQF_HIP_KERNEL_KINDS 9
+#define TQF_HIP_KERNEL_Q4K_GEMV 9        /* Q4_K GEMV, fp32 semantics         */
+#define TQF_HIP_KERNEL_Q4K_MATVEC 10     /* Q4_K matvec, Q8_K semantics       */
+#define TQF_HIP_KERNEL_KINDS 11
 /* While enabled, eager (non-graph) launches of each kind are bracketed by HIP
  * events on the context stream.  Enabling clears the totals. */
 int32_t tqf_hip_profile_enable(tqf_hip_ctx *ctx, int32_t enable);

@@ -343,7 +343,7 @@ def dequantize_q4_k(block, independent: bool = False) -> np.ndarray:
 
 
 def q4k_gemv(w: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np.ndarray:
-    """backend/reference.rs:61-79: fp32 dequantize-and-accumulate per row."""
+    """backend/reference.rs:49-67: fp32 dequantize-and-accumulate per row."""
     w = np.ascontiguousarray(w, dtype=np.uint8)
     x = _f32a(x)
     y = np.empty(rows, dtype=np.float32)
@@ -378,3 +378,13 @@ def q4_k_matvec(w: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np.ndarra
     if lib().orc_q4_k_matvec(_p(w), rows, cols, _p(x), _p(y)) != 0:
         raise ValueError("cols must be a multiple of 256")
     return y
+
+
+def q4_k_expert_forward(gate: np.ndarray, up: np.ndarray, down: np.ndarray, hidden: int,
+                        width: int, x: np.ndarray) -> np.ndarray:
+    """LoadedQwen36Expert::forward (weights.rs:566-610) for one row: Q4_K
+    gate and up matvecs, silu_mul (weights.rs:241-260), Q4_K down matvec,
+    each matvec with the Q8_K path of matvec_payload."""
+    g = q4_k_matvec(gate, width, hidden, x)
+    u = q4_k_matvec(up, width, hidden, x)
+    return q4_k_matvec(down, hidden, width, silu_mul(g, u))

@@ -825,7 +825,7 @@ void orc_dequantize_q4_k_indep(const uint8_t *block, float *out)
     }
 }
 
-/* backend/reference.rs:61-79 -- acc starts at 0.0 and takes every element
+/* backend/reference.rs:49-67 -- acc starts at 0.0 and takes every element
  * of the row in order (a plain loop, not an iterator sum). */
 int orc_q4k_gemv(const uint8_t *w, uint32_t rows, uint32_t cols, const float *x, float *y)
 {
@@ -866,7 +866,7 @@ void orc_quantize_q8_k(const float *values, int8_t *q, int16_t *sums, float *sca
     *scale = 1.0f / inv;
     for (int i = 0; i < 256; ++i) {
         float t = nearbyintf(values[i] * inv); /* round_ties_even (default mode) */
-        if (t > 127.0f) t = 127.0f;
+        if (!(t <= 127.0f)) t = 127.0f;        /* f32::min(127): NaN gives 127 */
         if (t < -128.0f) t = -128.0f;          /* `as i8` saturates */
         q[i] = (int8_t)t;
     }

@@ -40,6 +40,14 @@ class Q4Weights:
 
 
 @dataclass
+class Q4KWeights:
+    """A Q4_K matrix on the device (GGML 144-byte super-blocks of 256)."""
+    handle: int
+    rows: int
+    cols: int
+
+
+@dataclass
 class F32Tensor:
     handle: int
     count: int
@@ -204,6 +212,86 @@ class HipBackend:
         self._check(self.lib.tqf_hip_expert_forward(self.ctx, gate.handle, up.handle, down.handle,
                                                     _ptr(x2), m, _ptr(y)))
         return y[0] if squeeze else y
+
+    # ---- Q4_K ------------------------------------------------------------------
+    @staticmethod
+    def q4k_weights_bytes_for(rows: int, cols: int) -> int:
+        return int(_lib.load().tqf_hip_q4k_weights_bytes_for(rows, cols))
+
+    def upload_q4_k(self, q4_k: np.ndarray | bytes, rows: int, cols: int) -> Q4KWeights:
+        a = np.frombuffer(bytes(q4_k), dtype=np.uint8) if isinstance(q4_k, (bytes, bytearray)) \
+            else np.ascontiguousarray(q4_k, dtype=np.uint8)
+        h = C.c_void_p()
+        self._check(self.lib.tqf_hip_q4k_weights_upload(self.ctx, _ptr(a), a.nbytes, rows, cols,
+                                                        C.byref(h)))
+        return Q4KWeights(h.value, rows, cols)
+
+    def upload_q4_k_device(self, d_q4_k: DeviceBuffer, rows: int, cols: int) -> Q4KWeights:
+        h = C.c_void_p()
+        self._check(self.lib.tqf_hip_q4k_weights_upload_device(
+            self.ctx, d_q4_k.ptr, rows * (cols // 256) * 144, rows, cols, C.byref(h)))
+        return Q4KWeights(h.value, rows, cols)
+
+    def download_q4_k(self, w: Q4KWeights) -> np.ndarray:
+        out = np.empty(w.rows * (w.cols // 256) * 144, dtype=np.uint8)
+        self._check(self.lib.tqf_hip_q4k_weights_download(self.ctx, w.handle, _ptr(out),
+                                                          out.nbytes))
+        return out
+
+    def _q4k_call(self, fn, w: Q4KWeights, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        squeeze = x.ndim == 1
+        x2 = x.reshape(1, -1) if squeeze else x
+        if x2.shape[1] != w.cols:
+            raise ValueError(f"x has {x2.shape[1]} columns, matrix has {w.cols}")
+        m = x2.shape[0]
+        y = np.empty((m, w.rows), dtype=np.float32)
+        self._check(fn(self.ctx, w.handle, _ptr(x2), m, _ptr(y)))
+        return y[0] if squeeze else y
+
+    def q4k_gemv(self, w: Q4KWeights, x: np.ndarray) -> np.ndarray:
+        """backend::reference::q4k_gemv semantics (fp32 dequant-and-accumulate)."""
+        return self._q4k_call(self.lib.tqf_hip_q4k_gemv, w, x)
+
+    def q4k_matvec(self, w: Q4KWeights, x: np.ndarray) -> np.ndarray:
+        """matvec_payload Q4_K semantics (Q8_K activations, q4_k_dot_pre)."""
+        return self._q4k_call(self.lib.tqf_hip_q4k_matvec, w, x)
+
+    def q4k_gemv_device(self, w: Q4KWeights, d_x: DeviceBuffer, m: int, d_y: DeviceBuffer) -> None:
+        self._check(self.lib.tqf_hip_q4k_gemv_device(self.ctx, w.handle, d_x.ptr, m, d_y.ptr))
+
+    def q4k_matvec_device(self, w: Q4KWeights, d_x: DeviceBuffer, m: int,
+                          d_y: DeviceBuffer) -> None:
+        self._check(self.lib.tqf_hip_q4k_matvec_device(self.ctx, w.handle, d_x.ptr, m, d_y.ptr))
+
+    def q4k_gemv_batched_device(self, ws: Sequence[Q4KWeights], d_x: DeviceBuffer,
+                                d_y: DeviceBuffer) -> None:
+        arr = (C.c_void_p * len(ws))(*[w.handle for w in ws])
+        self._check(self.lib.tqf_hip_q4k_gemv_batched_device(self.ctx, arr, len(ws), d_x.ptr,
+                                                             d_y.ptr))
+
+    def q4k_matvec_batched_device(self, ws: Sequence[Q4KWeights], d_x: DeviceBuffer,
+                                  d_y: DeviceBuffer) -> None:
+        arr = (C.c_void_p * len(ws))(*[w.handle for w in ws])
+        self._check(self.lib.tqf_hip_q4k_matvec_batched_device(self.ctx, arr, len(ws), d_x.ptr,
+                                                               d_y.ptr))
+
+    def q4k_expert_forward(self, gate: Q4KWeights, up: Q4KWeights, down: Q4KWeights,
+                           x: np.ndarray) -> np.ndarray:
+        """LoadedQwen36Expert::forward with Q4_K payloads."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        squeeze = x.ndim == 1
+        x2 = x.reshape(1, -1) if squeeze else x
+        m = x2.shape[0]
+        y = np.empty((m, down.rows), dtype=np.float32)
+        self._check(self.lib.tqf_hip_q4k_expert_forward(self.ctx, gate.handle, up.handle,
+                                                        down.handle, _ptr(x2), m, _ptr(y)))
+        return y[0] if squeeze else y
+
+    def q4k_expert_forward_device(self, gate: Q4KWeights, up: Q4KWeights, down: Q4KWeights,
+                                  d_x: DeviceBuffer, m: int, d_y: DeviceBuffer) -> None:
+        self._check(self.lib.tqf_hip_q4k_expert_forward_device(
+            self.ctx, gate.handle, up.handle, down.handle, d_x.ptr, m, d_y.ptr))
 
     # ---- MoE layer -------------------------------------------------------------
     def prepare_moe_layer(self, router: F32Tensor, shared_input_gate: F32Tensor,

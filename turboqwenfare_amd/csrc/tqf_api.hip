@@ -277,7 +277,12 @@ struct Prof {
 double q4_bytes(uint32_t rows, uint32_t cols) { return (double)rows * (cols / 32) * kQ4Block; }
 
 // ---- validation -----------------------------------------------------------
-bool valid_weights(const tqf_hip_weights *w) { return w && w->tiles; }
+bool valid_weights(const tqf_hip_weights *w) {
+    return w && w->tiles && w->format == TQF_HIP_FORMAT_Q4_0;
+}
+bool valid_q4k(const tqf_hip_weights *w) {
+    return w && w->tiles && w->format == TQF_HIP_FORMAT_Q4_K;
+}
 
 // ---- the layer sequence ---------------------------------------------------
 // One MoE layer: route (optionally RMSNorm) -> gate/up -> down (+ residual).
@@ -498,6 +503,7 @@ extern "C" int32_t tqf_hip_destroy(tqf_hip_ctx *ctx) {
     (void)hipFree(ctx->d_stage);
     (void)hipFree(ctx->d_table);
     (void)hipFree(ctx->d_gemv_xprep);
+    (void)hipFree(ctx->d_q4k);
     (void)hipFree(ctx->d_grouped);
     (void)hipFree(const_cast<const uint8_t **>(ctx->d_adhoc_mats));
     for (Slab &s : ctx->slabs) (void)hipFree(s.base);
@@ -574,9 +580,10 @@ extern "C" uint64_t tqf_hip_weights_bytes_for(uint32_t rows, uint32_t cols) {
 }
 
 namespace {
-int32_t weights_alloc(tqf_hip_ctx *ctx, uint32_t rows, uint32_t cols, tqf_hip_weights **out) {
+int32_t weights_alloc(tqf_hip_ctx *ctx, uint32_t rows, uint32_t cols, tqf_hip_weights **out,
+                      int32_t format = TQF_HIP_FORMAT_Q4_0) {
     const MatrixDims d = matrix_dims(rows, cols);
-    const size_t bytes = layout_bytes(d);
+    const size_t bytes = format == TQF_HIP_FORMAT_Q4_K ? q4k_layout_bytes(d) : layout_bytes(d);
     void *tiles = nullptr, *self = nullptr;
     hipError_t e = arena_alloc(ctx, bytes, &tiles);
     if (e != hipSuccess) return fail(ctx, TQF_HIP_ERR_NOMEM, "weights allocation failed");
@@ -595,6 +602,7 @@ int32_t weights_alloc(tqf_hip_ctx *ctx, uint32_t rows, uint32_t cols, tqf_hip_we
     }
     tqf_hip_weights *w = new tqf_hip_weights();
     w->dims = d;
+    w->format = format;
     w->tiles = static_cast<uint8_t *>(tiles);
     w->bytes = bytes;
     w->d_self = static_cast<const uint8_t **>(self);
@@ -740,6 +748,28 @@ extern "C" int32_t tqf_hip_tensor_free(tqf_hip_ctx *ctx, tqf_hip_tensor *t) {
 // GEMV
 // ===========================================================================
 namespace {
+// Device table of `count` matrices (same shape, one format) for batched
+// launches; rewritten only when the list changes.
+int32_t set_table(tqf_hip_ctx *ctx, const tqf_hip_weights *const *ws, uint32_t count,
+                  bool (*valid)(const tqf_hip_weights *)) {
+    if (count > 65535) return fail(ctx, TQF_HIP_ERR_INVALID, "count must be <= 65535");
+    std::vector<const uint8_t *> table(count);
+    for (uint32_t i = 0; i < count; ++i) {
+        if (!valid(ws[i])) return fail(ctx, TQF_HIP_ERR_INVALID, "null or wrong-format weights in batch");
+        if (ws[i]->dims.rows != ws[0]->dims.rows || ws[i]->dims.cols != ws[0]->dims.cols)
+            return fail(ctx, TQF_HIP_ERR_INVALID, "batched matrices must share one shape");
+        table[i] = ws[i]->tiles;
+    }
+    if (table != ctx->table_shadow) {
+        TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        drop_graphs(ctx);
+        TQF_HIP(ctx, grow(ctx->d_table, ctx->table_cap, count * sizeof(void *)));
+        TQF_HIP(ctx, hipMemcpy(ctx->d_table, table.data(), count * sizeof(void *), hipMemcpyHostToDevice));
+        ctx->table_shadow = table;
+    }
+    return TQF_HIP_OK;
+}
+
 int32_t gemv_enqueue(tqf_hip_ctx *ctx, const uint8_t *const *table, uint32_t count,
                      const MatrixDims &d, const float *d_x, uint32_t m, float *d_y) {
     const uint32_t bp = d.blocks_padded;
@@ -791,22 +821,290 @@ extern "C" int32_t tqf_hip_q4_gemv_batched_device(tqf_hip_ctx *ctx,
                                                   const float *d_x, float *d_y) {
     TQF_ENTER(ctx);
     if (!ws || !d_x || !d_y || count == 0) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer or count 0");
-    if (count > 65535) return fail(ctx, TQF_HIP_ERR_INVALID, "count must be <= 65535");
-    std::vector<const uint8_t *> table(count);
-    for (uint32_t i = 0; i < count; ++i) {
-        if (!valid_weights(ws[i])) return fail(ctx, TQF_HIP_ERR_INVALID, "null weights in batch");
-        if (ws[i]->dims.rows != ws[0]->dims.rows || ws[i]->dims.cols != ws[0]->dims.cols)
-            return fail(ctx, TQF_HIP_ERR_INVALID, "batched matrices must share one shape");
-        table[i] = ws[i]->tiles;
+    if (int32_t rc = set_table(ctx, ws, count, valid_weights)) return rc;
+    return gemv_enqueue(ctx, ctx->d_table, count, ws[0]->dims, d_x, 1, d_y);
+}
+
+// ===========================================================================
+// Q4_K
+// ===========================================================================
+namespace {
+double q4k_bytes_of(uint32_t rows, uint32_t cols) { return (double)rows * (cols / 256) * kQ4KBlock; }
+
+int32_t check_q4k_shape(tqf_hip_ctx *ctx, size_t len, uint32_t rows, uint32_t cols) {
+    if (rows == 0 || cols == 0 || cols % 256)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "Q4_K matrix needs rows > 0 and cols a positive multiple of 256");
+    if (len != (size_t)rows * (cols / 256) * kQ4KBlock)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "Q4_K byte length does not match rows x cols");
+    return TQF_HIP_OK;
+}
+
+int32_t q4k_upload_from(tqf_hip_ctx *ctx, const uint8_t *d_src, uint32_t rows, uint32_t cols,
+                        tqf_hip_weights **out) {
+    tqf_hip_weights *w = nullptr;
+    if (int32_t rc = weights_alloc(ctx, rows, cols, &w, TQF_HIP_FORMAT_Q4_K)) return rc;
+    hipError_t e = launch_q4k_repack(ctx->stream, d_src, w->dims, w->tiles);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        weights_release(ctx, w);
+        return hip_fail(ctx, "Q4_K weights upload", e);
     }
-    if (table != ctx->table_shadow) {
+    *out = w;
+    return TQF_HIP_OK;
+}
+
+// Grows the shared record buffer to `bytes` (synchronising first, as a
+// resize may free memory an earlier launch still reads).
+int32_t ensure_gemv_records(tqf_hip_ctx *ctx, size_t bytes) {
+    if (ctx->d_gemv_xprep && ctx->gemv_xprep_bytes >= bytes) return TQF_HIP_OK;
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    drop_graphs(ctx);
+    TQF_HIP(ctx, grow(ctx->d_gemv_xprep, ctx->gemv_xprep_bytes, bytes));
+    return TQF_HIP_OK;
+}
+
+int32_t q4k_gemv_enqueue(tqf_hip_ctx *ctx, const uint8_t *const *table, uint32_t count,
+                         const MatrixDims &d, const float *d_x, uint32_t m, float *d_y) {
+    const uint32_t bp = d.blocks_padded;
+    if (int32_t rc = ensure_gemv_records(ctx, (size_t)m * bp * kXprepDwords * 4)) return rc;
+    hipError_t e = launch_q4k_prep(ctx->stream, d_x, m, d.cols, bp, ctx->d_gemv_xprep);
+    if (e != hipSuccess) return hip_fail(ctx, "Q4_K prep kernel launch", e);
+    Prof p(ctx);
+    e = launch_q4k_gemv(ctx->stream, table, count, d, ctx->d_gemv_xprep, m, d_y);
+    if (e != hipSuccess) return hip_fail(ctx, "Q4_K gemv kernel launch", e);
+    p.end(TQF_HIP_KERNEL_Q4K_GEMV,
+          (double)count * (q4k_bytes_of(d.rows, d.cols) + (double)m * d.rows * 4) + (double)m * d.cols * 4,
+          0, nullptr);
+    return TQF_HIP_OK;
+}
+
+int32_t q4k_matvec_enqueue(tqf_hip_ctx *ctx, const uint8_t *const *table, uint32_t count,
+                           const MatrixDims &d, const float *d_x, uint32_t m, float *d_y) {
+    const uint32_t bp = d.blocks_padded;
+    if (int32_t rc = ensure_gemv_records(ctx, (size_t)m * bp * kQ8KRecDwords * 4)) return rc;
+    hipError_t e = launch_q8k_quantize(ctx->stream, d_x, m, d.cols, bp, ctx->d_gemv_xprep);
+    if (e != hipSuccess) return hip_fail(ctx, "Q8_K quantize kernel launch", e);
+    Prof p(ctx);
+    e = launch_q4k_q8k_gemv(ctx->stream, table, count, d, ctx->d_gemv_xprep, m, d_y);
+    if (e != hipSuccess) return hip_fail(ctx, "Q4_K matvec kernel launch", e);
+    p.end(TQF_HIP_KERNEL_Q4K_MATVEC,
+          (double)count * (q4k_bytes_of(d.rows, d.cols) + (double)m * d.rows * 4) + (double)m * d.cols * 4,
+          0, nullptr);
+    return TQF_HIP_OK;
+}
+
+using Q4kEnqueue = int32_t (*)(tqf_hip_ctx *, const uint8_t *const *, uint32_t, const MatrixDims &,
+                               const float *, uint32_t, float *);
+
+// Host-pointer form: stage x, run, copy y back, wait.
+int32_t q4k_host_call(tqf_hip_ctx *ctx, const tqf_hip_weights *w, const float *x, uint32_t m,
+                      float *y, Q4kEnqueue enqueue) {
+    if (!valid_q4k(w) || !x || !y) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer or not Q4_K weights");
+    if (m == 0 || m > kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "m must be in 1..8");
+    const MatrixDims &d = w->dims;
+    const size_t xb = (size_t)m * d.cols * 4, yb = (size_t)m * d.rows * 4;
+    if (int32_t rc = ensure_stage(ctx, align_up(xb, kAlign) + yb)) return rc;
+    float *dx = static_cast<float *>(ctx->d_stage);
+    float *dy = reinterpret_cast<float *>(static_cast<uint8_t *>(ctx->d_stage) + align_up(xb, kAlign));
+    TQF_HIP(ctx, hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream));
+    if (int32_t rc = enqueue(ctx, w->d_self, 1, d, dx, m, dy)) return rc;
+    TQF_HIP(ctx, hipMemcpyAsync(y, dy, yb, hipMemcpyDeviceToHost, ctx->stream));
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return TQF_HIP_OK;
+}
+}  // namespace
+
+extern "C" uint64_t tqf_hip_q4k_weights_bytes_for(uint32_t rows, uint32_t cols) {
+    if (rows == 0 || cols == 0 || cols % 256) return 0;
+    return align_up(q4k_layout_bytes(matrix_dims(rows, cols)), kAlign) + kAlign;
+}
+
+extern "C" int32_t tqf_hip_q4k_weights_upload(tqf_hip_ctx *ctx, const uint8_t *q4_k, size_t len,
+                                              uint32_t rows, uint32_t cols,
+                                              tqf_hip_weights **out) {
+    TQF_ENTER(ctx);
+    if (!q4_k || !out) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    *out = nullptr;
+    if (int32_t rc = check_q4k_shape(ctx, len, rows, cols)) return rc;
+    if (int32_t rc = ensure_stage(ctx, len)) return rc;
+    TQF_HIP(ctx, hipMemcpyAsync(ctx->d_stage, q4_k, len, hipMemcpyHostToDevice, ctx->stream));
+    return q4k_upload_from(ctx, static_cast<const uint8_t *>(ctx->d_stage), rows, cols, out);
+}
+
+extern "C" int32_t tqf_hip_q4k_weights_upload_device(tqf_hip_ctx *ctx, const void *d_q4_k,
+                                                     size_t len, uint32_t rows, uint32_t cols,
+                                                     tqf_hip_weights **out) {
+    TQF_ENTER(ctx);
+    if (!d_q4_k || !out) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    *out = nullptr;
+    if (int32_t rc = check_q4k_shape(ctx, len, rows, cols)) return rc;
+    return q4k_upload_from(ctx, static_cast<const uint8_t *>(d_q4_k), rows, cols, out);
+}
+
+extern "C" int32_t tqf_hip_q4k_weights_download(tqf_hip_ctx *ctx, const tqf_hip_weights *w,
+                                                uint8_t *q4_k, size_t len) {
+    TQF_ENTER(ctx);
+    if (!valid_q4k(w) || !q4_k) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer or not Q4_K weights");
+    const MatrixDims &d = w->dims;
+    const uint32_t nb = d.cols / 256;
+    if (len != (size_t)d.rows * nb * kQ4KBlock)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "Q4_K byte length does not match the matrix");
+    std::vector<uint8_t> tiles(w->bytes);
+    TQF_HIP(ctx, hipMemcpyAsync(tiles.data(), w->tiles, w->bytes, hipMemcpyDeviceToHost, ctx->stream));
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    for (uint32_t r = 0; r < d.rows; ++r) {
+        for (uint32_t s = 0; s < nb; ++s) {
+            uint8_t *dst = q4_k + ((size_t)r * nb + s) * kQ4KBlock;
+            std::memcpy(dst, tiles.data() + q4k_dm_offset(d, r, s), 4);
+            uint32_t sc[8], mn[8];
+            for (int j = 0; j < 8; ++j) {
+                const uint8_t *p = tiles.data() + scale_offset(d, r, s * 8 + j);
+                sc[j] = p[0];
+                mn[j] = p[1];
+            }
+            // the 12-byte packing that q4_k_scale_min (weights.rs:933-942) unpacks
+            for (int i = 0; i < 4; ++i) {
+                dst[4 + i] = (uint8_t)(sc[i] | ((sc[i + 4] >> 4) << 6));
+                dst[8 + i] = (uint8_t)(mn[i] | ((mn[i + 4] >> 4) << 6));
+                dst[12 + i] = (uint8_t)((sc[i + 4] & 15) | ((mn[i + 4] & 15) << 4));
+            }
+            for (int j = 0; j < 8; ++j) {
+                const uint8_t *nib = tiles.data() + nibble_offset(d, r, s * 8 + j);
+                uint8_t q[32];
+                for (int i = 0; i < 4; ++i)
+                    for (int t = 0; t < 4; ++t) {
+                        q[2 * i + 8 * t] = nib[4 * i + t] & 15;
+                        q[2 * i + 1 + 8 * t] = nib[4 * i + t] >> 4;
+                    }
+                uint8_t *qs = dst + 16 + 32 * (j >> 1);
+                for (int e = 0; e < 32; ++e)
+                    qs[e] = (j & 1) ? (uint8_t)((qs[e] & 15) | (q[e] << 4)) : q[e];
+            }
+        }
+    }
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_q4k_gemv(tqf_hip_ctx *ctx, const tqf_hip_weights *w, const float *x,
+                                    uint32_t m, float *y) {
+    TQF_ENTER(ctx);
+    return q4k_host_call(ctx, w, x, m, y, q4k_gemv_enqueue);
+}
+
+extern "C" int32_t tqf_hip_q4k_gemv_device(tqf_hip_ctx *ctx, const tqf_hip_weights *w,
+                                           const float *d_x, uint32_t m, float *d_y) {
+    TQF_ENTER(ctx);
+    if (!valid_q4k(w) || !d_x || !d_y) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer or not Q4_K weights");
+    if (m == 0 || m > kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "m must be in 1..8");
+    return q4k_gemv_enqueue(ctx, w->d_self, 1, w->dims, d_x, m, d_y);
+}
+
+extern "C" int32_t tqf_hip_q4k_gemv_batched_device(tqf_hip_ctx *ctx,
+                                                   const tqf_hip_weights *const *ws,
+                                                   uint32_t count, const float *d_x, float *d_y) {
+    TQF_ENTER(ctx);
+    if (!ws || !d_x || !d_y || count == 0) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer or count 0");
+    if (int32_t rc = set_table(ctx, ws, count, valid_q4k)) return rc;
+    return q4k_gemv_enqueue(ctx, ctx->d_table, count, ws[0]->dims, d_x, 1, d_y);
+}
+
+extern "C" int32_t tqf_hip_q4k_matvec(tqf_hip_ctx *ctx, const tqf_hip_weights *w, const float *x,
+                                      uint32_t m, float *y) {
+    TQF_ENTER(ctx);
+    return q4k_host_call(ctx, w, x, m, y, q4k_matvec_enqueue);
+}
+
+extern "C" int32_t tqf_hip_q4k_matvec_device(tqf_hip_ctx *ctx, const tqf_hip_weights *w,
+                                             const float *d_x, uint32_t m, float *d_y) {
+    TQF_ENTER(ctx);
+    if (!valid_q4k(w) || !d_x || !d_y) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer or not Q4_K weights");
+    if (m == 0 || m > kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "m must be in 1..8");
+    return q4k_matvec_enqueue(ctx, w->d_self, 1, w->dims, d_x, m, d_y);
+}
+
+extern "C" int32_t tqf_hip_q4k_matvec_batched_device(tqf_hip_ctx *ctx,
+                                                     const tqf_hip_weights *const *ws,
+                                                     uint32_t count, const float *d_x,
+                                                     float *d_y) {
+    TQF_ENTER(ctx);
+    if (!ws || !d_x || !d_y || count == 0) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer or count 0");
+    if (int32_t rc = set_table(ctx, ws, count, valid_q4k)) return rc;
+    return q4k_matvec_enqueue(ctx, ctx->d_table, count, ws[0]->dims, d_x, 1, d_y);
+}
+
+namespace {
+// One Q4_K expert over m rows: Q8_K(x) -> gate, up -> silu_mul -> Q8_K(h)
+// -> down, every matvec with q4_k_dot_pre's arithmetic.
+int32_t q4k_expert_enqueue(tqf_hip_ctx *ctx, const tqf_hip_weights *gate,
+                           const tqf_hip_weights *up, const tqf_hip_weights *down,
+                           const float *d_x, uint32_t m, float *d_y) {
+    const MatrixDims &dg = gate->dims, &dd = down->dims;
+    const uint32_t F = dg.rows, H = dg.cols;
+    const size_t qx = align_up((size_t)m * dg.blocks_padded * kQ8KRecDwords * 4, kAlign);
+    const size_t qh = align_up((size_t)m * dd.blocks_padded * kQ8KRecDwords * 4, kAlign);
+    const size_t gu = align_up((size_t)2 * m * F * 4, kAlign);
+    const size_t hb = align_up((size_t)m * F * 4, kAlign);
+    const size_t need = qx + qh + gu + hb;
+    if (!ctx->d_q4k || ctx->q4k_bytes < need) {
         TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
         drop_graphs(ctx);
-        TQF_HIP(ctx, grow(ctx->d_table, ctx->table_cap, count * sizeof(void *)));
-        TQF_HIP(ctx, hipMemcpy(ctx->d_table, table.data(), count * sizeof(void *), hipMemcpyHostToDevice));
-        ctx->table_shadow = table;
+        TQF_HIP(ctx, grow(ctx->d_q4k, ctx->q4k_bytes, need));
     }
-    return gemv_enqueue(ctx, ctx->d_table, count, ws[0]->dims, d_x, 1, d_y);
+    uint32_t *q8x = reinterpret_cast<uint32_t *>(ctx->d_q4k);
+    uint32_t *q8h = reinterpret_cast<uint32_t *>(ctx->d_q4k + qx);
+    float *dgu = reinterpret_cast<float *>(ctx->d_q4k + qx + qh);
+    float *dh = reinterpret_cast<float *>(ctx->d_q4k + qx + qh + gu);
+    hipError_t e = launch_q8k_quantize(ctx->stream, d_x, m, H, dg.blocks_padded, q8x);
+    if (e == hipSuccess) e = launch_q4k_q8k_gemv(ctx->stream, gate->d_self, 1, dg, q8x, m, dgu);
+    if (e == hipSuccess)
+        e = launch_q4k_q8k_gemv(ctx->stream, up->d_self, 1, up->dims, q8x, m, dgu + (size_t)m * F);
+    if (e == hipSuccess) e = launch_q4k_silu_mul(ctx->stream, dgu, m, F, dh);
+    if (e == hipSuccess) e = launch_q8k_quantize(ctx->stream, dh, m, F, dd.blocks_padded, q8h);
+    if (e == hipSuccess) e = launch_q4k_q8k_gemv(ctx->stream, down->d_self, 1, dd, q8h, m, d_y);
+    if (e != hipSuccess) return hip_fail(ctx, "Q4_K expert kernels", e);
+    (void)H;
+    return TQF_HIP_OK;
+}
+
+int32_t check_q4k_expert(tqf_hip_ctx *ctx, const tqf_hip_weights *gate, const tqf_hip_weights *up,
+                         const tqf_hip_weights *down, uint32_t m) {
+    if (!valid_q4k(gate) || !valid_q4k(up) || !valid_q4k(down))
+        return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer or not Q4_K weights");
+    if (m == 0 || m > kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "m must be in 1..8");
+    const uint32_t F = gate->dims.rows, H = gate->dims.cols;
+    if (up->dims.rows != F || up->dims.cols != H || down->dims.rows != H || down->dims.cols != F)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "expert shapes: gate/up [width x hidden], down [hidden x width]");
+    return TQF_HIP_OK;
+}
+}  // namespace
+
+extern "C" int32_t tqf_hip_q4k_expert_forward(tqf_hip_ctx *ctx, const tqf_hip_weights *gate,
+                                              const tqf_hip_weights *up,
+                                              const tqf_hip_weights *down, const float *x,
+                                              uint32_t m, float *y) {
+    TQF_ENTER(ctx);
+    if (!x || !y) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (int32_t rc = check_q4k_expert(ctx, gate, up, down, m)) return rc;
+    const size_t xb = (size_t)m * gate->dims.cols * 4;
+    if (int32_t rc = ensure_stage(ctx, 2 * align_up(xb, kAlign))) return rc;
+    float *dx = static_cast<float *>(ctx->d_stage);
+    float *dy = reinterpret_cast<float *>(static_cast<uint8_t *>(ctx->d_stage) + align_up(xb, kAlign));
+    TQF_HIP(ctx, hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream));
+    if (int32_t rc = q4k_expert_enqueue(ctx, gate, up, down, dx, m, dy)) return rc;
+    TQF_HIP(ctx, hipMemcpyAsync(y, dy, xb, hipMemcpyDeviceToHost, ctx->stream));
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_q4k_expert_forward_device(tqf_hip_ctx *ctx,
+                                                     const tqf_hip_weights *gate,
+                                                     const tqf_hip_weights *up,
+                                                     const tqf_hip_weights *down,
+                                                     const float *d_x, uint32_t m, float *d_y) {
+    TQF_ENTER(ctx);
+    if (!d_x || !d_y) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (int32_t rc = check_q4k_expert(ctx, gate, up, down, m)) return rc;
+    return q4k_expert_enqueue(ctx, gate, up, down, d_x, m, d_y);
 }
 
 // ===========================================================================

@@ -96,6 +96,34 @@ inline size_t layout_bytes(const MatrixDims &d) {
     return (size_t)d.rows_padded * d.blocks_padded * kQ4Block;
 }
 
+// Q4_K row-lane layout.  A GGML Q4_K matrix is rows x (cols / 256)
+// super-blocks of 144 bytes: f16 d, f16 dmin, 12 bytes packing eight 6-bit
+// (scale, min) pairs, 128 nibble bytes (format/quant/dequant.rs:139-184).
+// Element i of sub-block j (32 elements) decodes to d sc_j q_i - dmin m_j.
+// The device copy keeps the Q4_0 geometry with 32-element sub-blocks in
+// place of Q4_0 blocks (MatrixDims.blocks = cols / 32):
+//   nibble slot (row, sub-block)   16 bytes at nibble_offset(); byte 4i + t
+//                                  holds element 2i + 8t (low nibble) and
+//                                  2i + 1 + 8t (high nibble) ("class order":
+//                                  class c = elements c, c+8, c+16, c+24)
+//   scale slot (octet, sub-block)  16 bytes at scale_offset(): per row the
+//                                  bytes (sc, m) of that sub-block
+//   (d, dmin) table                after the octet chunks: per (octet,
+//                                  super-block) 32 bytes, per row f16 d then
+//                                  f16 dmin
+// 148 bytes per 256 elements and row (GGML: 144); every bit is kept and
+// tqf_hip_q4k_weights_download() re-packs the GGML bytes.
+constexpr int kQ4KBlock = 144;
+__host__ __device__ inline size_t q4k_dm_base(const MatrixDims &d) {
+    return (size_t)(d.rows_padded >> 3) * 9 * d.blocks_padded * 16;
+}
+__host__ __device__ inline size_t q4k_dm_offset(const MatrixDims &d, size_t row, size_t sb) {
+    return q4k_dm_base(d) + (((row >> 3) * (d.blocks_padded >> 3) + sb) * 8 + (row & 7)) * 4;
+}
+inline size_t q4k_layout_bytes(const MatrixDims &d) {
+    return q4k_dm_base(d) + (size_t)d.rows_padded * (d.blocks_padded >> 3) * 4;
+}
+
 // Route plan written by the route kernel and read by the expert kernels.
 // Work is planned per (expert, token) pair so that every workgroup carries
 // the same arithmetic: slots [0, M) are the shared expert for tokens 0..M-1
@@ -173,6 +201,7 @@ struct Slab {
 
 struct tqf_hip_weights {
     tqf::MatrixDims dims;
+    int32_t format;              // TQF_HIP_FORMAT_Q4_0 or TQF_HIP_FORMAT_Q4_K
     uint8_t *tiles;              // device: nibble plane, then scale plane
     size_t bytes;
     const uint8_t **d_self;      // device: one-entry table {tiles}
@@ -281,6 +310,9 @@ struct tqf_hip_ctx {
     size_t table_cap = 0;
     uint32_t *d_gemv_xprep = nullptr;
     size_t gemv_xprep_bytes = 0;
+    // Q4_K expert forward: Q8_K records of x and h, gate/up outputs, h
+    uint8_t *d_q4k = nullptr;
+    size_t q4k_bytes = 0;
     // host staging for the synchronous host-pointer entry points
     void *d_stage = nullptr;
     size_t stage_bytes = 0;
@@ -334,6 +366,24 @@ hipError_t launch_accept(hipStream_t s, const float *target, const float *draft,
                          int32_t *tokens, void *scratch, hipEvent_t ev_start, hipEvent_t ev_stop);
 hipError_t launch_top4(hipStream_t s, const float *logits, uint32_t rows, uint32_t vocab,
                        uint32_t *tokens4, float *logits4);
+
+// ---- Q4_K (tqf_q4k.hip) ----------------------------------------------------
+// Activation records: q4k_prep writes the fp32-semantics GEMV's records
+// (28 dwords per (token, sub-block), row stride 28 Bp); q8k_quantize writes
+// Q8_K records (12 dwords per (token, sub-block), row stride 12 Bp) for
+// cols a multiple of 256.
+constexpr int kQ8KRecDwords = 12;
+hipError_t launch_q4k_repack(hipStream_t s, const uint8_t *d_aos, const MatrixDims &d,
+                             uint8_t *tiles);
+hipError_t launch_q4k_prep(hipStream_t s, const float *x, uint32_t m, uint32_t cols, uint32_t bp,
+                           uint32_t *xprep);
+hipError_t launch_q4k_gemv(hipStream_t s, const uint8_t *const *tables, uint32_t count,
+                           const MatrixDims &d, const uint32_t *xprep, uint32_t m, float *y);
+hipError_t launch_q8k_quantize(hipStream_t s, const float *x, uint32_t m, uint32_t cols,
+                               uint32_t bp, uint32_t *q8);
+hipError_t launch_q4k_q8k_gemv(hipStream_t s, const uint8_t *const *tables, uint32_t count,
+                               const MatrixDims &d, const uint32_t *q8, uint32_t m, float *y);
+hipError_t launch_q4k_silu_mul(hipStream_t s, const float *gu, uint32_t m, uint32_t F, float *h);
 
 // ---- grouped expert GEMM (tqf_grouped.hip) --------------------------------
 // Scratch views of one call over T tokens (P = 8 T pairs): the expert-sorted
