@@ -958,7 +958,7 @@ extern "C" int32_t tqf_hip_q4k_weights_download(tqf_hip_ctx *ctx, const tqf_hip_
             std::memcpy(dst, tiles.data() + q4k_dm_offset(d, r, s), 4);
             uint32_t sc[8], mn[8];
             for (int j = 0; j < 8; ++j) {
-                const uint8_t *p = tiles.data() + scale_offset(d, r, s * 8 + j);
+                const uint8_t *p = tiles.data() + scale_offset(d, q4k_slot_row(r, s * 8 + j), s * 8 + j);
                 sc[j] = p[0];
                 mn[j] = p[1];
             }
@@ -969,7 +969,7 @@ extern "C" int32_t tqf_hip_q4k_weights_download(tqf_hip_ctx *ctx, const tqf_hip_
                 dst[12 + i] = (uint8_t)((sc[i + 4] & 15) | ((mn[i + 4] & 15) << 4));
             }
             for (int j = 0; j < 8; ++j) {
-                const uint8_t *nib = tiles.data() + nibble_offset(d, r, s * 8 + j);
+                const uint8_t *nib = tiles.data() + nibble_offset(d, q4k_slot_row(r, s * 8 + j), s * 8 + j);
                 uint8_t q[32];
                 for (int i = 0; i < 4; ++i)
                     for (int t = 0; t < 4; ++t) {

@@ -108,12 +108,23 @@ inline size_t layout_bytes(const MatrixDims &d) {
 //                                  class c = elements c, c+8, c+16, c+24)
 //   scale slot (octet, sub-block)  16 bytes at scale_offset(): per row the
 //                                  bytes (sc, m) of that sub-block
+// Within an octet, the eight rows of sub-block b sit in permuted positions:
+// position p of the nibble and scale slots holds row p ^ (b mod 8)
+// (q4k_slot_row), so that the lane that owns sub-block b reads row p ^ k
+// (k = b mod 8) into register slot p with the same contiguous wavefront
+// loads as the Q4_0 layout, and the eight lanes of a super-block can be
+// summed with a select-free butterfly (lane k keeps row k).
 //   (d, dmin) table                after the octet chunks: per (octet,
 //                                  super-block) 32 bytes, per row f16 d then
 //                                  f16 dmin
 // 148 bytes per 256 elements and row (GGML: 144); every bit is kept and
 // tqf_hip_q4k_weights_download() re-packs the GGML bytes.
 constexpr int kQ4KBlock = 144;
+// The nibble_offset()/scale_offset() row argument under which row r of
+// sub-block b is stored.
+__host__ __device__ inline size_t q4k_slot_row(size_t row, size_t block) {
+    return (row & ~(size_t)7) | ((row ^ block) & 7);
+}
 __host__ __device__ inline size_t q4k_dm_base(const MatrixDims &d) {
     return (size_t)(d.rows_padded >> 3) * 9 * d.blocks_padded * 16;
 }

@@ -59,7 +59,7 @@ __global__ __launch_bounds__(256) void q4k_repack_kernel(const uint8_t *__restri
     q4k_scale_min(src + 4, j, sc, mn);
     const uint8_t *qs = src + 16 + 32 * (j >> 1);
     const int shift = 4 * (j & 1);
-    uint8_t *nib = dst + nibble_offset(d, r, b);
+    uint8_t *nib = dst + nibble_offset(d, q4k_slot_row(r, b), b);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -68,7 +68,7 @@ __global__ __launch_bounds__(256) void q4k_repack_kernel(const uint8_t *__restri
             const uint32_t hi = (qs[2 * i + 1 + 8 * t] >> shift) & 15u;
             nib[4 * i + t] = (uint8_t)(lo | (hi << 4));
         }
-    uint8_t *scp = dst + scale_offset(d, r, b);
+    uint8_t *scp = dst + scale_offset(d, q4k_slot_row(r, b), b);
     scp[0] = (uint8_t)sc;
     scp[1] = (uint8_t)mn;
     if (j == 0) {
@@ -144,6 +144,45 @@ __device__ __forceinline__ void octet_sc_m(const uint4 v, int n, uint32_t &sc, u
     mn = (h >> 8) & 0xFFu;
 }
 
+constexpr int kDppRowRor8 = 0x128;  // row_ror:8: lane i <- lane i ^ 8 within 16
+
+// Slots 4 (k & 4), 2 (k & 2) and 1 (k & 1) apart swapped: the bits of k
+// that dm0/dm1's load addresses have not already applied (k & 4 there).
+__device__ __forceinline__ void xor_permute8(uint32_t (&v)[8], int k) {
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        if ((p & 2) == 0) {
+            const uint32_t a = v[p], b = v[p + 2];
+            v[p] = (k & 2) ? b : a;
+            v[p + 2] = (k & 2) ? a : b;
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < 8; p += 2) {
+        const uint32_t a = v[p], b = v[p + 1];
+        v[p] = (k & 1) ? b : a;
+        v[p + 1] = (k & 1) ? a : b;
+    }
+}
+
+// Row sums of a lane group: register slot p of lane k (k = lane mod 8)
+// holds a partial of row p ^ k.  Three select-free butterfly stages over the
+// eight lanes leave row k's sum over them in slot 0 (each stage adds the
+// partner's slot p ^ mask to slot p), then the LPR / 8 groups of a lane
+// group are added (lanes k, k + 8, ...).  Valid in the first eight lanes.
+template <int LPR>
+__device__ __forceinline__ float xor_reduce_rows(float (&v)[8]) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) v[p] += dpp_f<kDppHalfMirror>(v[p ^ 7]);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) v[p] += dpp_f<kDppQuadRev>(v[p ^ 3]);
+    v[0] += dpp_f<kDppXor1>(v[1]);
+    if constexpr (LPR >= 16) v[0] += dpp_f<kDppRowRor8>(v[0]);
+    if constexpr (LPR >= 32) permlane16_stage<1>(v);
+    if constexpr (LPR >= 64) permlane32_stage<1>(v);
+    return v[0];
+}
+
 // ---------------------------------------------------------------------------
 // fp32-semantics GEMV / small-M GEMM: the Q4_0 GEMV's geometry (lane group
 // of LPR lanes per row octet, lane b owns sub-block b of each chunk, every
@@ -169,8 +208,9 @@ __global__ __launch_bounds__(kQ4KWaves * kWave) void q4k_gemv_kernel(
     const uint8_t *base = tables[mat];
     const RowLane W = row_lane(base, d.blocks_padded);
     const uint32_t rl = r0 + jg * NL;
-    const uint32_t row = rl + reduced_index<LPR, NL>(lane);
-    const bool writer = reduced_first_copy<LPR, NL>(lane) && row < d.rows;
+    const int k = (int)(b & 7);  // register slot p holds row rl + (p ^ k)
+    const uint32_t row = rl + k;
+    const bool writer = b < 8 && row < d.rows;
     const uint32_t chunks = d.blocks_padded / LPR;
     const size_t xstride = (size_t)d.blocks_padded * kXprepDwords;
     const uint8_t *dm_octet = base + q4k_dm_offset(d, rl, 0);
@@ -187,7 +227,8 @@ __global__ __launch_bounds__(kQ4KWaves * kWave) void q4k_gemv_kernel(
             for (int n = 0; n < NL; ++n) nib[n] = q4_signed(load_nibbles(W, rl + n, blk));
             const uint4 scm = load_scales(W, rl / 8, blk);
             const uint8_t *dmp = dm_octet + (size_t)(blk >> 3) * 32;
-            const uint4 dm0 = load_global_u4(dmp), dm1 = load_global_u4(dmp + 16);
+            const uint4 dm0 = load_global_u4(dmp + ((k & 4) ? 16 : 0));  // rows 0..3 ^ (k & 4)
+            const uint4 dm1 = load_global_u4(dmp + ((k & 4) ? 0 : 16));
             uint32_t x[TG][28];
 #pragma unroll
             for (int t = 0; t < TG; ++t) {
@@ -196,7 +237,8 @@ __global__ __launch_bounds__(kQ4KWaves * kWave) void q4k_gemv_kernel(
                 if (blk >= d.blocks) x[t][24] = 0;  // padding: exactly 0 whatever it holds
             }
             __builtin_amdgcn_sched_barrier(0);  // every load in flight before any math
-            const uint32_t dmv[8] = {dm0.x, dm0.y, dm0.z, dm0.w, dm1.x, dm1.y, dm1.z, dm1.w};
+            uint32_t dmv[8] = {dm0.x, dm0.y, dm0.z, dm0.w, dm1.x, dm1.y, dm1.z, dm1.w};
+            xor_permute8(dmv, k);  // (d, dmin) of row p ^ k in slot p
             float dsc[NL], bias[NL];
 #pragma unroll
             for (int n = 0; n < NL; ++n) {
@@ -215,7 +257,7 @@ __global__ __launch_bounds__(kQ4KWaves * kWave) void q4k_gemv_kernel(
         }
 #pragma unroll
         for (int t = 0; t < TG; ++t) {
-            const float s = transpose_reduce<LPR, NL>(acc[t]);
+            const float s = xor_reduce_rows<LPR>(acc[t]);
             if (writer && t0 + t < m) y[((size_t)mat * m + t0 + t) * d.rows + row] = s;
         }
     }
@@ -326,8 +368,9 @@ hipError_t launch_q8k_quantize(hipStream_t s, const float *x, uint32_t m, uint32
 // class (the reference's lane = index mod 8 is the class), exact int32.
 // The eight lanes of one super-block are summed with a butterfly that needs
 // no selects: lane k of the eight keeps row k, and it holds the values of
-// row p ^ k in register slot p from the start (its loads are addressed that
-// way), so each halving stage adds the partner's slot p ^ mask to slot p.
+// row p ^ k in register slot p from the start (the layout stores them in
+// that order), so each halving stage adds the partner's slot p ^ mask to
+// slot p.
 // After it, lane 8g + k holds row k's eight class sums and its
 // block_minimum_sum for super-block g of the chunk.
 //
@@ -393,7 +436,7 @@ __global__ __launch_bounds__(kQ4KWaves * kWave) void q4k_q8k_gemv_kernel(
             const uint32_t blk = c * LPR + b;
             uint4 nib[8];
 #pragma unroll
-            for (int p = 0; p < 8; ++p) nib[p] = load_nibbles(W, rl + (p ^ k), blk);
+            for (int p = 0; p < 8; ++p) nib[p] = load_nibbles(W, rl + p, blk);  // row rl + (p ^ k)
             const uint4 scm = load_scales(W, rl / 8, blk);
             const uint32_t dmw = *(const __attribute__((address_space(1))) uint32_t *)(dm_row + (size_t)(blk >> 3) * 32);
             uint4 xa[TG], xb[TG], xc[TG];
@@ -406,16 +449,9 @@ __global__ __launch_bounds__(kQ4KWaves * kWave) void q4k_q8k_gemv_kernel(
                 xc[t] = load_global_u4(xr + 8 * bp);
             }
             __builtin_amdgcn_sched_barrier(0);
-            uint32_t scp[8], mnp[8];
+            uint32_t scp[8], mnp[8];  // (sc, m) of row p ^ k, stored in position p
 #pragma unroll
-            for (int p = 0; p < 8; ++p) {
-                const int e = p ^ k;
-                const uint32_t w01 = (e & 2) ? scm.y : scm.x, w23 = (e & 2) ? scm.w : scm.z;
-                const uint32_t w = (e & 4) ? w23 : w01;
-                const uint32_t h = (e & 1) ? (w >> 16) : w;
-                scp[p] = h & 0xFFu;
-                mnp[p] = (h >> 8) & 0xFFu;
-            }
+            for (int p = 0; p < 8; ++p) octet_sc_m(scm, p, scp[p], mnp[p]);
             const float ws = f16_to_f32(dmw), ms = f16_to_f32(dmw >> 16);
 #pragma unroll
             for (int t = 0; t < TG; ++t) {
@@ -423,20 +459,29 @@ __global__ __launch_bounds__(kQ4KWaves * kWave) void q4k_q8k_gemv_kernel(
                                    (int)xb[t].x, (int)xb[t].y, (int)xb[t].z, (int)xb[t].w};
                 const int s32 = (int)xc[t].x;
                 const float qscale = __uint_as_float(xc[t].y);
-                int L[64], bm[8];
+                // class dots of every slot; slots 4..7 are scaled and handed
+                // to the half-mirror partner, whose slots 0..3 take them in
+                // the same multiply-add as their own scaling (the first
+                // butterfly stage)
+                int D[64], L[32], bm[8];
 #pragma unroll
                 for (int p = 0; p < 8; ++p) {
                     const uint32_t wv[4] = {nib[p].x, nib[p].y, nib[p].z, nib[p].w};
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int lo = (int)(wv[i] & 0x0F0F0F0Fu), hi = (int)((wv[i] >> 4) & 0x0F0F0F0Fu);
-                        L[8 * p + 2 * i] = __mul24((int)scp[p], __builtin_amdgcn_sdot4(lo, qd[2 * i], 0, false));
-                        L[8 * p + 2 * i + 1] =
-                            __mul24((int)scp[p], __builtin_amdgcn_sdot4(hi, qd[2 * i + 1], 0, false));
+                        D[8 * p + 2 * i] = __builtin_amdgcn_sdot4(lo, qd[2 * i], 0, false);
+                        D[8 * p + 2 * i + 1] = __builtin_amdgcn_sdot4(hi, qd[2 * i + 1], 0, false);
                     }
                     bm[p] = __mul24((int)mnp[p], s32);
                 }
-                xor_stage<kDppHalfMirror, 7, 8>(L);
+#pragma unroll
+                for (int p = 0; p < 4; ++p)
+#pragma unroll
+                    for (int cc = 0; cc < 8; ++cc) {
+                        const int sent = __mul24((int)scp[p ^ 7], D[8 * (p ^ 7) + cc]);
+                        L[8 * p + cc] = __mul24((int)scp[p], D[8 * p + cc]) + dpp_i<kDppHalfMirror>(sent);
+                    }
                 xor_stage<kDppQuadRev, 3, 4>(L);
                 xor_stage<kDppXor1, 1, 2>(L);
                 xor_stage1<kDppHalfMirror, 7, 8>(bm);
