@@ -70,6 +70,9 @@ _SIGS = {
     "orc_quantize_q8_k": (None, [_vp, _vp, _vp, _vp]),
     "orc_q4_k_dot_pre": (_f32, [_vp, _u32, _vp, _vp, _vp]),
     "orc_q4_k_matvec": (_i32, [_vp, _u32, _u32, _vp, _vp]),
+    "orc_dequantize_q6_k": (None, [_vp, _vp]),
+    "orc_q6_k_dot_pre": (_f32, [_vp, _u32, _vp, _vp]),
+    "orc_q6_k_matvec": (_i32, [_vp, _u32, _u32, _vp, _vp]),
 }
 
 _LIB = None
@@ -388,3 +391,32 @@ def q4_k_expert_forward(gate: np.ndarray, up: np.ndarray, down: np.ndarray, hidd
     g = q4_k_matvec(gate, width, hidden, x)
     u = q4_k_matvec(up, width, hidden, x)
     return q4_k_matvec(down, hidden, width, silu_mul(g, u))
+
+
+Q6_K_BLOCK_BYTES = 210
+
+
+def dequantize_q6_k(block: np.ndarray) -> np.ndarray:
+    """dequant.rs:190-218 (the canonical LM head format)."""
+    b = np.ascontiguousarray(block, dtype=np.uint8)
+    out = np.empty(256, np.float32)
+    lib().orc_dequantize_q6_k(_p(b), _p(out))
+    return out
+
+
+def q6_k_dot_pre(row: np.ndarray, q8: np.ndarray, scales: np.ndarray) -> float:
+    """weights.rs:1023-1101 over len(row) / 210 blocks."""
+    row = np.ascontiguousarray(row, dtype=np.uint8)
+    q8 = np.ascontiguousarray(q8, dtype=np.int8)
+    scales = _f32a(scales)
+    return float(lib().orc_q6_k_dot_pre(_p(row), row.size // Q6_K_BLOCK_BYTES, _p(q8), _p(scales)))
+
+
+def q6_k_matvec(w: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np.ndarray:
+    """weights.rs:680-735 with the Q6_K branch: Q8_K activations, integer dot."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = _f32a(x)
+    y = np.empty(rows, dtype=np.float32)
+    if lib().orc_q6_k_matvec(_p(w), rows, cols, _p(x), _p(y)) != 0:
+        raise ValueError("cols must be a multiple of 256")
+    return y

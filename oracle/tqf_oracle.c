@@ -947,3 +947,82 @@ int orc_q4_k_matvec(const uint8_t *w, uint32_t rows, uint32_t cols, const float 
     free(scales);
     return 0;
 }
+
+/* ======================================================================= */
+/* f3: Q6_K, the canonical LM head format                                   */
+/* ======================================================================= */
+#define ORC_Q6_K_BLOCK_BYTES 210
+
+/* The signed 6-bit value q - 32 of element e (0..255) of one block: the two
+ * 128-element halves each interleave four 32-element groups, low nibbles
+ * from ql, two high bits from qh (dequant.rs:198-216). */
+static int q6k_value(const uint8_t *b, int e)
+{
+    const int half = e / 128, r = e % 128, grp = r / 32, i = r % 32;
+    const uint8_t *ql = b + 64 * half, *qh = b + 128 + 32 * half;
+    const uint8_t low = (grp & 1) ? ql[i + 32] : ql[i];
+    const int lo = (grp < 2) ? (low & 0x0F) : (low >> 4);
+    const int hi = (qh[i] >> (2 * grp)) & 3;
+    return (lo | (hi << 4)) - 32;
+}
+
+/* dequant.rs:190-218: (d * scale) * q in that order. */
+void orc_dequantize_q6_k(const uint8_t *b, float *out)
+{
+    const float d = orc_f16_to_f32((uint16_t)(b[208] | (b[209] << 8)));
+    for (int e = 0; e < 256; ++e) {
+        const int8_t sc = (int8_t)b[192 + e / 16];
+        out[e] = d * (float)sc * (float)q6k_value(b, e);
+    }
+}
+
+/* weights.rs:1023-1101: integer lane sums (lane = element index mod 8),
+ * sums[lane] += (d * q8scale) * lane_sum block after block, then the
+ * iterator sum from -0.0. */
+float orc_q6_k_dot_pre(const uint8_t *row, uint32_t nblocks, const int8_t *q8, const float *scales)
+{
+    float sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (uint32_t b = 0; b < nblocks; ++b) {
+        const uint8_t *w = row + (size_t)b * ORC_Q6_K_BLOCK_BYTES;
+        const int8_t *qb = q8 + (size_t)b * 256;
+        const float d = orc_f16_to_f32((uint16_t)(w[208] | (w[209] << 8)));
+        int32_t lane_sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int group = 0; group < 16; ++group) {
+            const int32_t sc = (int8_t)w[192 + group];
+            for (int half = 0; half < 2; ++half)
+                for (int lane = 0; lane < 8; ++lane) {
+                    const int idx = group * 16 + half * 8 + lane;
+                    lane_sums[lane] += sc * (int32_t)qb[idx] * q6k_value(w, idx);
+                }
+        }
+        const float combined = d * scales[b];
+        for (int lane = 0; lane < 8; ++lane) sums[lane] += combined * (float)lane_sums[lane];
+    }
+    float total = -0.0f;
+    for (int lane = 0; lane < 8; ++lane) total += sums[lane];
+    return total;
+}
+
+int orc_q6_k_matvec(const uint8_t *w, uint32_t rows, uint32_t cols, const float *x, float *y)
+{
+    if (cols % 256 != 0) return -1;
+    const uint32_t nb = cols / 256;
+    int8_t *q8 = (int8_t *)malloc((size_t)nb * 256);
+    int16_t *sums = (int16_t *)malloc((size_t)nb * 16 * sizeof(int16_t));
+    float *scales = (float *)malloc((size_t)nb * sizeof(float));
+    if (!q8 || !sums || !scales) {
+        free(q8);
+        free(sums);
+        free(scales);
+        return -1;
+    }
+    for (uint32_t b = 0; b < nb; ++b)
+        orc_quantize_q8_k(x + (size_t)b * 256, q8 + (size_t)b * 256, sums + (size_t)b * 16, &scales[b]);
+#pragma omp parallel for schedule(static) if (rows >= 4096)
+    for (uint32_t r = 0; r < rows; ++r)
+        y[r] = orc_q6_k_dot_pre(w + (size_t)r * nb * ORC_Q6_K_BLOCK_BYTES, nb, q8, scales);
+    free(q8);
+    free(sums);
+    free(scales);
+    return 0;
+}

@@ -183,7 +183,7 @@ uint64_t orc_scale_floor(uint64_t total, float u); /* floor(total * u) exact */
 void orc_dequantize_q4_k(const uint8_t *block144, float *out256);
 /* validate.rs:97-126 (sub-blocks walked directly, independent f16). */
 void orc_dequantize_q4_k_indep(const uint8_t *block144, float *out256);
-/* backend/reference.rs:61-79 q4k_gemv: rows x (cols/256) blocks row-major;
+/* backend/reference.rs:49-67 q4k_gemv: rows x (cols/256) blocks row-major;
  * one fp32 accumulator per row over every dequantized element in order.
  * Returns 0, or -1 if cols is not a multiple of 256.  Pinned: float64 brute
  * force on the reference's LCG fixture (backend/metal/kernels.rs:1118-1138)
@@ -205,6 +205,23 @@ float orc_q4_k_dot_pre(const uint8_t *row, uint32_t nblocks, const int8_t *q8, c
  * is not a multiple of 256.  Pinned: composition of the two above; agrees
  * with orc_q4k_gemv to the Q8_K quantization error. */
 int orc_q4_k_matvec(const uint8_t *w, uint32_t rows, uint32_t cols, const float *x, float *y);
+
+/* ---- f3: Q6_K (210-byte super-blocks of 256), the canonical LM head -------- */
+/* dequant.rs:190-218 dequantize_q6_k: ql[128], qh[64], 16 signed group
+ * scales, f16 d; value = (d * scale) * (q - 32).  Pinned: the all -32 KAT
+ * (dequant.rs:308-315); every value equals the exact float64 decode rounded
+ * once; a vectorised numpy decoder. */
+void orc_dequantize_q6_k(const uint8_t *block210, float *out256);
+/* weights.rs:1023-1101 q6_k_dot_pre (scalar lane loop) over nblocks blocks
+ * of one row against Q8_K values / scales of the same chunks.  Pinned:
+ * float64 evaluation of the same integer terms; lane sums against a numpy
+ * restatement. */
+float orc_q6_k_dot_pre(const uint8_t *row, uint32_t nblocks, const int8_t *q8, const float *scales);
+/* weights.rs:680-735 for GgmlType::Q6K: Q8_K per chunk, then q6_k_dot_pre per
+ * row.  Returns 0, or -1 if cols is not a multiple of 256.  Pinned: the
+ * -8192 KAT (weights.rs:2532-2543); the Q8_K rounding bound against the
+ * float64 GEMV of the decoded weights. */
+int orc_q6_k_matvec(const uint8_t *w, uint32_t rows, uint32_t cols, const float *x, float *y);
 
 #ifdef __cplusplus
 }

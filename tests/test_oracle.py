@@ -682,3 +682,99 @@ def test_q4_k_matvec_within_the_q8_k_rounding_bound():
         dq = np.concatenate([q4_k_exact(w[(r * 2 + c) * 144:(r * 2 + c + 1) * 144]) for c in range(2)])
         bound = sum(abs(steps[c]) / 2 * np.abs(dq[c * 256:(c + 1) * 256]).sum() for c in range(2))
         assert abs(float(a[r]) - float(b[r])) <= bound * 1.001 + 1e-3
+
+
+# ---- f3: Q6_K (the canonical LM head) -------------------------------------------
+def q6_k_values_np(block: np.ndarray) -> np.ndarray:
+    """q - 32 of the 256 elements by array slicing (ggml's block_q6_K: two
+    128-element halves of four interleaved 32-element groups)."""
+    b = np.asarray(block, np.uint8).astype(np.int64)
+    q = np.empty(256, np.int64)
+    for h in range(2):
+        lo, hb = b[64 * h:64 * h + 64], b[128 + 32 * h:128 + 32 * h + 32]
+        base = 128 * h
+        q[base:base + 32] = (lo[:32] & 15) | ((hb & 3) << 4)
+        q[base + 32:base + 64] = (lo[32:] & 15) | (((hb >> 2) & 3) << 4)
+        q[base + 64:base + 96] = (lo[:32] >> 4) | (((hb >> 4) & 3) << 4)
+        q[base + 96:base + 128] = (lo[32:] >> 4) | (((hb >> 6) & 3) << 4)
+    return q - 32
+
+
+def q6_k_exact(block: np.ndarray) -> np.ndarray:
+    b = np.asarray(block, np.uint8)
+    d = float(b[208:210].view(np.float16)[0])
+    sc = b[192:208].view(np.int8).astype(np.float64)
+    return d * np.repeat(sc, 16) * q6_k_values_np(b)
+
+
+def random_q6_k(n: int, seed: int) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    blk = rng.integers(0, 256, size=(n, 210), dtype=np.uint8)
+    blk[:, 208:210] = rng.uniform(0.001, 0.05, n).astype(np.float16).view(np.uint8).reshape(n, 2)
+    return blk
+
+
+def test_q6_k_kats():
+    # dequant.rs:308-315 and weights.rs:2532-2543: zero ql / qh (q = -32
+    # everywhere), group scales 1, d = 1; x = ones gives 256 x -32
+    b = np.zeros(210, np.uint8)
+    b[192:208] = 1
+    b[208:210] = (0x00, 0x3C)
+    assert np.all(orc.dequantize_q6_k(b) == -32.0)
+    assert orc.q6_k_matvec(b, 1, 256, np.ones(256, np.float32))[0] == -8192.0
+    with pytest.raises(ValueError):
+        orc.q6_k_matvec(b, 1, 200, np.ones(200, np.float32))
+
+
+def test_q6_k_dequant_is_the_once_rounded_exact_value():
+    # d * scale needs 19 bits (exact); times q - 32 it is rounded once
+    for blk in random_q6_k(300, 51):
+        assert np.array_equal(orc.dequantize_q6_k(blk), q6_k_exact(blk).astype(np.float32))
+
+
+def test_q6_k_single_field_probes():
+    # one low nibble, one high-bit pair, one scale: the element each field
+    # feeds moves alone
+    b = np.zeros(210, np.uint8)
+    b[192:208] = 1
+    b[208:210] = (0x00, 0x3C)
+    base = orc.dequantize_q6_k(b)
+    for byte, val, elem in ((0, 0x01, 0), (0, 0x10, 64), (32, 0x01, 32), (63, 0x10, 127),
+                            (64, 0x01, 128), (127, 0x10, 255), (128, 0x01, 0), (128, 0x04, 32),
+                            (128, 0x10, 64), (128, 0x40, 96), (191, 0x40, 255)):
+        p = b.copy()
+        p[byte] = val
+        diff = np.flatnonzero(orc.dequantize_q6_k(p) != base)
+        assert list(diff) == [elem], (byte, val, diff)
+    p = b.copy()
+    p[192 + 5] = 3  # group 5 = elements 80..95
+    assert list(np.flatnonzero(orc.dequantize_q6_k(p) != base)) == list(range(80, 96))
+
+
+def test_q6_k_dot_pre_against_float64_and_lane_sums():
+    rng = np.random.default_rng(52)
+    nb = 3
+    row = random_q6_k(nb, 53).reshape(-1)
+    x = rng.standard_normal(nb * 256).astype(np.float32)
+    qs, _, scs = zip(*(orc.quantize_q8_k(x[b * 256:(b + 1) * 256]) for b in range(nb)))
+    q8, scales = np.concatenate(qs), np.array(scs, np.float32)
+    got = orc.q6_k_dot_pre(row, q8, scales)
+    want = 0.0
+    for b in range(nb):
+        blk = row[b * 210:(b + 1) * 210]
+        want += float(scales[b]) * float(np.dot(q6_k_exact(blk), q8[b * 256:(b + 1) * 256].astype(np.float64)))
+    assert abs(got - want) <= 1e-5 * max(abs(want), 1.0)
+
+
+def test_q6_k_matvec_within_the_q8_k_rounding_bound():
+    rng = np.random.default_rng(54)
+    rows, cols = 8, 512
+    w = random_q6_k(rows * 2, 55).reshape(-1)
+    x = rng.standard_normal(cols).astype(np.float32)
+    y = orc.q6_k_matvec(w, rows, cols, x)
+    steps = [abs(orc.quantize_q8_k(x[c * 256:(c + 1) * 256])[2]) for c in range(2)]
+    for r in range(rows):
+        dq = np.concatenate([q6_k_exact(w[(r * 2 + c) * 210:(r * 2 + c + 1) * 210]) for c in range(2)])
+        exact = float(np.dot(dq, x.astype(np.float64)))
+        bound = sum(steps[c] / 2 * np.abs(dq[c * 256:(c + 1) * 256]).sum() for c in range(2))
+        assert abs(float(y[r]) - exact) <= bound * 1.001 + 1e-3
