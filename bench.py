@@ -224,6 +224,42 @@ def q4k_pool_bench(be, pool_size: int, seed: int, iters: int = 10):
     return out
 
 
+def lm_head_bench(be, seed: int, iters: int = 20):
+    """The LM head at the configs' vocabulary: Q6_K [151,936 x 2048] (255 MB,
+    the canonical checkpoint's lm_head format) against the M = 4 verify rows,
+    bit-exact Q8_K logits plus the fused top-4 candidates per row."""
+    from turboqwenfare_amd import _lib, synth
+
+    rng = np.random.default_rng(seed)
+    n = V * (H // 256)
+    blk = rng.integers(0, 256, size=(n, 210), dtype=np.uint8)
+    blk[:, 208:210] = rng.uniform(0.001, 0.05, n).astype(np.float16).view(np.uint8).reshape(n, 2)
+    w = be.upload_q6_k(blk.reshape(-1), V, H)
+    del blk
+    out = {"vocab": V, "hidden": H, "format": "q6_k", "bytes_weights": V * (H // 256) * 210}
+    for m in (1, M):
+        dx = be.to_device(synth.normal((m, H), seed=seed + m))
+        dy, dt, dl = be.alloc(m * V * 4), be.alloc(m * 16), be.alloc(m * 16)
+        be.lm_head_logits_device(w, dx, m, dy, dt, dl)
+        be.synchronize()
+        be.profile_enable(True)
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            be.lm_head_logits_device(w, dx, m, dy, dt, dl)
+        be.synchronize()
+        call_us = (time.perf_counter() - t0) / iters * 1e6
+        n_l, ms, by = be.profile_read(_lib.KERNEL_Q6K_MATVEC)
+        be.profile_enable(False)
+        r = dict(m=m, kernel_us=ms / n_l * 1e3, call_us=call_us, bytes_per_launch=by / n_l,
+                 gbs=by / (ms * 1e-3) / 1e9)
+        r["frac"] = r["gbs"] / HBM_PEAK_GBS
+        out[f"m{m}"] = r
+        for b in (dx, dy, dt, dl):
+            be.free(b)
+    be.free_weights(w)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -243,10 +279,20 @@ def main():
                     help="only run the config-5 grouped expert GEMM on one resident layer "
                          "(the command its rocprofv3 profiles are taken with) and exit")
     ap.add_argument("--grouped-iters", type=int, default=20)
+    ap.add_argument("--lm-head-only", action="store_true",
+                    help="only run the Q6_K LM head (the command its rocprofv3 profiles are "
+                         "taken with) and exit")
     ap.add_argument("--q4k-only", action="store_true",
                     help="only run the Q4_K config-1 GEMV pools (the command their rocprofv3 "
                          "profiles are taken with) and exit")
     args = ap.parse_args()
+    if args.lm_head_only:
+        from turboqwenfare_amd.backend import HipBackend
+
+        be = HipBackend(0)
+        log("bench: LM head " + json.dumps(lm_head_bench(be, args.seed)))
+        be.close()
+        return
     if args.q4k_only:
         from turboqwenfare_amd.backend import HipBackend
 
@@ -384,6 +430,8 @@ def main():
     log("bench: config-1 GEMV pool " + json.dumps(gemv))
     q4k = q4k_pool_bench(be, args.gemv_pool, args.seed)
     log("bench: Q4_K config-1 pools " + json.dumps(q4k))
+    lm = lm_head_bench(be, args.seed)
+    log("bench: LM head " + json.dumps(lm))
     grouped = grouped_gemm_bench(be, layers[0], args.seed)
     log("bench: config-5 grouped GEMM " + json.dumps(grouped))
 
@@ -435,6 +483,7 @@ def main():
         "kernels": prof,
         "gemv_config1": gemv,
         "q4k_config1": q4k,
+        "lm_head_q6k": lm,
         "grouped_gemm_config5": grouped,
         "eager_profiled_ms_per_step": eager_ms,
         "synchronised_step_ms": {"p10": q10, "median": q50, "p90": q90},

@@ -232,6 +232,7 @@ int32_t tqf_hip_grouped_gemm_device(tqf_hip_ctx *ctx, const tqf_hip_layer *layer
  * q4k entry points accept it (the Q4_0 ones reject it, and vice versa). */
 #define TQF_HIP_FORMAT_Q4_0 0
 #define TQF_HIP_FORMAT_Q4_K 1
+#define TQF_HIP_FORMAT_Q6_K 2
 /* Device bytes of a Q4_K upload of this shape; 0 unless cols is a positive
  * multiple of 256. */
 uint64_t tqf_hip_q4k_weights_bytes_for(uint32_t rows, uint32_t cols);
@@ -280,6 +281,42 @@ int32_t tqf_hip_q4k_expert_forward_device(tqf_hip_ctx *ctx, const tqf_hip_weight
                                           const tqf_hip_weights *down, const float *d_x,
                                           uint32_t m, float *d_y);
 
+/* ---- the LM head: canonical Q6_K matrices (GGML 210-byte super-blocks of
+ *      256, format/quant/dequant.rs:190-218), the checkpoint's lm_head
+ *      (model/qwen36/weights.rs:1744, runtime.rs:435) ---------------------- */
+/* Device bytes of a Q6_K upload of this shape (the GGML size, 210 bytes per
+ * 256 weights, plus padding); 0 unless cols is a positive multiple of 256. */
+uint64_t tqf_hip_q6k_weights_bytes_for(uint32_t rows, uint32_t cols);
+/* `q6_k` is rows x (cols/256) row-major 210-byte super-blocks; lossless
+ * repack.  Handles are format TQF_HIP_FORMAT_Q6_K (only the q6k / lm_head
+ * entry points accept them). */
+int32_t tqf_hip_q6k_weights_upload(tqf_hip_ctx *ctx, const uint8_t *q6_k, size_t len,
+                                   uint32_t rows, uint32_t cols, tqf_hip_weights **out);
+int32_t tqf_hip_q6k_weights_upload_device(tqf_hip_ctx *ctx, const void *d_q6_k, size_t len,
+                                          uint32_t rows, uint32_t cols, tqf_hip_weights **out);
+int32_t tqf_hip_q6k_weights_download(tqf_hip_ctx *ctx, const tqf_hip_weights *w, uint8_t *q6_k,
+                                     size_t len);
+/* matvec_payload for GgmlType::Q6K (weights.rs:680-735): quantize_q8_k per
+ * 256-element chunk of each x row, then q6_k_dot_pre per output row
+ * (:1023-1101).  Bit-identical to that scalar code.  x [m x cols], y
+ * [m x rows] f32, 1 <= m <= TQF_HIP_MAX_TOKENS. */
+int32_t tqf_hip_q6k_matvec(tqf_hip_ctx *ctx, const tqf_hip_weights *w, const float *x, uint32_t m,
+                           float *y);
+int32_t tqf_hip_q6k_matvec_device(tqf_hip_ctx *ctx, const tqf_hip_weights *w, const float *d_x,
+                                  uint32_t m, float *d_y);
+/* The LM head with the fused greedy candidates: logits [m x V] =
+ * tqf_hip_q6k_matvec(w [V x hidden], x [m x hidden]) (lm_head.matvec,
+ * runtime.rs:435; the Metal lm_head_logits, backend/metal/kernels.rs:
+ * 1080-1098, for Q6_K), and per row the four candidates of
+ * top_logit_candidates (runtime/decode.rs:48-64) -- tokens4 / logits4
+ * [m x 4], descending, ties to the lower token, NaN and -inf never taken
+ * (empty slots: token 0, -inf) -- from the same pass over the weights. */
+int32_t tqf_hip_lm_head_logits(tqf_hip_ctx *ctx, const tqf_hip_weights *w, const float *x,
+                               uint32_t m, float *logits, uint32_t *tokens4, float *logits4);
+int32_t tqf_hip_lm_head_logits_device(tqf_hip_ctx *ctx, const tqf_hip_weights *w,
+                                      const float *d_x, uint32_t m, float *d_logits,
+                                      uint32_t *d_tokens4, float *d_logits4);
+
 /* ---- one MTP verify step: the stack over the k+1 verify rows, then the
  *      acceptance, as one stream-ordered (graph-replayed) unit.  The verify
  *      loop the reference leaves unwired (runtime/mtp.rs:1-20). ------------- */
@@ -303,7 +340,8 @@ int32_t tqf_hip_verify_step_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack,
 #define TQF_HIP_KERNEL_GROUPED_AUX 8     /* grouped GEMM: sort plan + combine */
 #define TQF_HIP_KERNEL_Q4K_GEMV 9        /* Q4_K GEMV, fp32 semantics         */
 #define TQF_HIP_KERNEL_Q4K_MATVEC 10     /* Q4_K matvec, Q8_K semantics       */
-#define TQF_HIP_KERNEL_KINDS 11
+#define TQF_HIP_KERNEL_Q6K_MATVEC 11     /* Q6_K matvec / LM head (+ top-4)   */
+#define TQF_HIP_KERNEL_KINDS 12
 /* While enabled, eager (non-graph) launches of each kind are bracketed by HIP
  * events on the context stream.  Enabling clears the totals. */
 int32_t tqf_hip_profile_enable(tqf_hip_ctx *ctx, int32_t enable);

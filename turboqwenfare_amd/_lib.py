@@ -30,9 +30,11 @@ KERNEL_GROUPED_DOWN = 7
 KERNEL_GROUPED_AUX = 8
 KERNEL_Q4K_GEMV = 9
 KERNEL_Q4K_MATVEC = 10
-KERNEL_KINDS = 11
+KERNEL_Q6K_MATVEC = 11
+KERNEL_KINDS = 12
 FORMAT_Q4_0 = 0
 FORMAT_Q4_K = 1
+FORMAT_Q6_K = 2
 GROUPED_MAX_TOKENS = 4096
 
 _vp = C.c_void_p
@@ -98,6 +100,14 @@ SIGNATURES = {
     "tqf_hip_q4k_matvec_batched_device": (_i32, [_vp, _vp, _u32, _vp, _vp]),
     "tqf_hip_q4k_expert_forward": (_i32, [_vp, _vp, _vp, _vp, _vp, _u32, _vp]),
     "tqf_hip_q4k_expert_forward_device": (_i32, [_vp, _vp, _vp, _vp, _vp, _u32, _vp]),
+    "tqf_hip_q6k_weights_bytes_for": (_u64, [_u32, _u32]),
+    "tqf_hip_q6k_weights_upload": (_i32, [_vp, _vp, _sz, _u32, _u32, _pp]),
+    "tqf_hip_q6k_weights_upload_device": (_i32, [_vp, _vp, _sz, _u32, _u32, _pp]),
+    "tqf_hip_q6k_weights_download": (_i32, [_vp, _vp, _vp, _sz]),
+    "tqf_hip_q6k_matvec": (_i32, [_vp, _vp, _vp, _u32, _vp]),
+    "tqf_hip_q6k_matvec_device": (_i32, [_vp, _vp, _vp, _u32, _vp]),
+    "tqf_hip_lm_head_logits": (_i32, [_vp, _vp, _vp, _u32, _vp, _vp, _vp]),
+    "tqf_hip_lm_head_logits_device": (_i32, [_vp, _vp, _vp, _u32, _vp, _vp, _vp]),
     "tqf_hip_moe_layer_prepare": (_i32, [_vp, C.POINTER(MoeWeights), _pp]),
     "tqf_hip_moe_layer_free": (_i32, [_vp, _vp]),
     "tqf_hip_moe_layer": (_i32, [_vp, _vp, _vp, _u32, _vp, _vp, _vp]),

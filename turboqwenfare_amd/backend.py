@@ -48,6 +48,14 @@ class Q4KWeights:
 
 
 @dataclass
+class Q6KWeights:
+    """A Q6_K matrix on the device (GGML 210-byte super-blocks of 256)."""
+    handle: int
+    rows: int
+    cols: int
+
+
+@dataclass
 class F32Tensor:
     handle: int
     count: int
@@ -292,6 +300,60 @@ class HipBackend:
                                   d_x: DeviceBuffer, m: int, d_y: DeviceBuffer) -> None:
         self._check(self.lib.tqf_hip_q4k_expert_forward_device(
             self.ctx, gate.handle, up.handle, down.handle, d_x.ptr, m, d_y.ptr))
+
+    # ---- Q6_K / LM head ---------------------------------------------------------
+    @staticmethod
+    def q6k_weights_bytes_for(rows: int, cols: int) -> int:
+        return int(_lib.load().tqf_hip_q6k_weights_bytes_for(rows, cols))
+
+    def upload_q6_k(self, q6_k: np.ndarray | bytes, rows: int, cols: int) -> Q6KWeights:
+        a = np.frombuffer(bytes(q6_k), dtype=np.uint8) if isinstance(q6_k, (bytes, bytearray)) \
+            else np.ascontiguousarray(q6_k, dtype=np.uint8)
+        h = C.c_void_p()
+        self._check(self.lib.tqf_hip_q6k_weights_upload(self.ctx, _ptr(a), a.nbytes, rows, cols,
+                                                        C.byref(h)))
+        return Q6KWeights(h.value, rows, cols)
+
+    def upload_q6_k_device(self, d_q6_k: DeviceBuffer, rows: int, cols: int) -> Q6KWeights:
+        h = C.c_void_p()
+        self._check(self.lib.tqf_hip_q6k_weights_upload_device(
+            self.ctx, d_q6_k.ptr, rows * (cols // 256) * 210, rows, cols, C.byref(h)))
+        return Q6KWeights(h.value, rows, cols)
+
+    def download_q6_k(self, w: Q6KWeights) -> np.ndarray:
+        out = np.empty(w.rows * (w.cols // 256) * 210, dtype=np.uint8)
+        self._check(self.lib.tqf_hip_q6k_weights_download(self.ctx, w.handle, _ptr(out),
+                                                          out.nbytes))
+        return out
+
+    def q6k_matvec(self, w: Q6KWeights, x: np.ndarray) -> np.ndarray:
+        """matvec_payload Q6_K semantics (Q8_K activations, q6_k_dot_pre)."""
+        return self._q4k_call(self.lib.tqf_hip_q6k_matvec, w, x)
+
+    def q6k_matvec_device(self, w: Q6KWeights, d_x: DeviceBuffer, m: int,
+                          d_y: DeviceBuffer) -> None:
+        self._check(self.lib.tqf_hip_q6k_matvec_device(self.ctx, w.handle, d_x.ptr, m, d_y.ptr))
+
+    def lm_head_logits(self, w: Q6KWeights, x: np.ndarray):
+        """logits [m, V] and the top_logit_candidates (tokens [m, 4], logits [m, 4])."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        x2 = x.reshape(1, -1) if x.ndim == 1 else x
+        if x2.shape[1] != w.cols:
+            raise ValueError(f"x has {x2.shape[1]} columns, matrix has {w.cols}")
+        m = x2.shape[0]
+        y = np.empty((m, w.rows), dtype=np.float32)
+        t4 = np.empty((m, 4), dtype=np.uint32)
+        l4 = np.empty((m, 4), dtype=np.float32)
+        self._check(self.lib.tqf_hip_lm_head_logits(self.ctx, w.handle, _ptr(x2), m, _ptr(y),
+                                                    _ptr(t4), _ptr(l4)))
+        return y, t4, l4
+
+    def lm_head_logits_device(self, w: Q6KWeights, d_x: DeviceBuffer, m: int,
+                              d_logits: DeviceBuffer, d_tokens4: DeviceBuffer,
+                              d_logits4: DeviceBuffer) -> None:
+        self._check(self.lib.tqf_hip_lm_head_logits_device(self.ctx, w.handle, d_x.ptr, m,
+                                                           d_logits.ptr, d_tokens4.ptr,
+                                                           d_logits4.ptr))
 
     # ---- MoE layer -------------------------------------------------------------
     def prepare_moe_layer(self, router: F32Tensor, shared_input_gate: F32Tensor,

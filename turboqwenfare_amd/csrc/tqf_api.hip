@@ -283,6 +283,9 @@ bool valid_weights(const tqf_hip_weights *w) {
 bool valid_q4k(const tqf_hip_weights *w) {
     return w && w->tiles && w->format == TQF_HIP_FORMAT_Q4_K;
 }
+bool valid_q6k(const tqf_hip_weights *w) {
+    return w && w->tiles && w->format == TQF_HIP_FORMAT_Q6_K;
+}
 
 // ---- the layer sequence ---------------------------------------------------
 // One MoE layer: route (optionally RMSNorm) -> gate/up -> down (+ residual).
@@ -504,6 +507,7 @@ extern "C" int32_t tqf_hip_destroy(tqf_hip_ctx *ctx) {
     (void)hipFree(ctx->d_table);
     (void)hipFree(ctx->d_gemv_xprep);
     (void)hipFree(ctx->d_q4k);
+    (void)hipFree(ctx->d_lm);
     (void)hipFree(ctx->d_grouped);
     (void)hipFree(const_cast<const uint8_t **>(ctx->d_adhoc_mats));
     for (Slab &s : ctx->slabs) (void)hipFree(s.base);
@@ -583,7 +587,9 @@ namespace {
 int32_t weights_alloc(tqf_hip_ctx *ctx, uint32_t rows, uint32_t cols, tqf_hip_weights **out,
                       int32_t format = TQF_HIP_FORMAT_Q4_0) {
     const MatrixDims d = matrix_dims(rows, cols);
-    const size_t bytes = format == TQF_HIP_FORMAT_Q4_K ? q4k_layout_bytes(d) : layout_bytes(d);
+    const size_t bytes = format == TQF_HIP_FORMAT_Q4_K   ? q4k_layout_bytes(d)
+                         : format == TQF_HIP_FORMAT_Q6_K ? q6k_layout_bytes(d)
+                                                         : layout_bytes(d);
     void *tiles = nullptr, *self = nullptr;
     hipError_t e = arena_alloc(ctx, bytes, &tiles);
     if (e != hipSuccess) return fail(ctx, TQF_HIP_ERR_NOMEM, "weights allocation failed");
@@ -1105,6 +1111,186 @@ extern "C" int32_t tqf_hip_q4k_expert_forward_device(tqf_hip_ctx *ctx,
     if (!d_x || !d_y) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
     if (int32_t rc = check_q4k_expert(ctx, gate, up, down, m)) return rc;
     return q4k_expert_enqueue(ctx, gate, up, down, d_x, m, d_y);
+}
+
+// ===========================================================================
+// Q6_K and the LM head
+// ===========================================================================
+namespace {
+double q6k_bytes_of(uint32_t rows, uint32_t cols) { return (double)rows * (cols / 256) * kQ6KBlock; }
+
+int32_t check_q6k_shape(tqf_hip_ctx *ctx, size_t len, uint32_t rows, uint32_t cols) {
+    if (rows == 0 || cols == 0 || cols % 256)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "Q6_K matrix needs rows > 0 and cols a positive multiple of 256");
+    if (len != (size_t)rows * (cols / 256) * kQ6KBlock)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "Q6_K byte length does not match rows x cols");
+    return TQF_HIP_OK;
+}
+
+int32_t q6k_upload_from(tqf_hip_ctx *ctx, const uint8_t *d_src, uint32_t rows, uint32_t cols,
+                        tqf_hip_weights **out) {
+    tqf_hip_weights *w = nullptr;
+    if (int32_t rc = weights_alloc(ctx, rows, cols, &w, TQF_HIP_FORMAT_Q6_K)) return rc;
+    hipError_t e = launch_q6k_repack(ctx->stream, d_src, w->dims, w->tiles);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        weights_release(ctx, w);
+        return hip_fail(ctx, "Q6_K weights upload", e);
+    }
+    *out = w;
+    return TQF_HIP_OK;
+}
+
+// Q8_K records of x, then the matvec (with the top-4 candidates when tokens4
+// is given).  Scratch: [records | candidates] in ctx->d_lm.
+int32_t q6k_enqueue(tqf_hip_ctx *ctx, const tqf_hip_weights *w, const float *d_x, uint32_t m,
+                    float *d_y, uint32_t *d_tokens4, float *d_logits4) {
+    const MatrixDims &d = w->dims;
+    const size_t rec = align_up((size_t)m * d.blocks_padded * kQ8KRecDwords * 4, kAlign);
+    const size_t cand = d_tokens4 ? q6k_top4_scratch_bytes(d, m) : 0;
+    if (!ctx->d_lm || ctx->lm_bytes < rec + cand) {
+        TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        drop_graphs(ctx);
+        TQF_HIP(ctx, grow(ctx->d_lm, ctx->lm_bytes, rec + cand));
+    }
+    uint32_t *q8 = reinterpret_cast<uint32_t *>(ctx->d_lm);
+    hipError_t e = launch_q8k_quantize(ctx->stream, d_x, m, d.cols, d.blocks_padded, q8);
+    if (e != hipSuccess) return hip_fail(ctx, "Q8_K quantize kernel launch", e);
+    Prof p(ctx);
+    e = launch_q6k_q8k_gemv(ctx->stream, w->d_self, 1, d, q8, m, d_y,
+                            d_tokens4 ? ctx->d_lm + rec : nullptr, d_tokens4, d_logits4);
+    if (e != hipSuccess) return hip_fail(ctx, "Q6_K matvec kernel launch", e);
+    p.end(TQF_HIP_KERNEL_Q6K_MATVEC,
+          q6k_bytes_of(d.rows, d.cols) + (double)m * d.rows * 4 + (double)m * d.cols * 4, 0, nullptr);
+    return TQF_HIP_OK;
+}
+
+int32_t check_q6k_call(tqf_hip_ctx *ctx, const tqf_hip_weights *w, uint32_t m) {
+    if (!valid_q6k(w)) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer or not Q6_K weights");
+    if (m == 0 || m > kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "m must be in 1..8");
+    return TQF_HIP_OK;
+}
+
+int32_t q6k_host_call(tqf_hip_ctx *ctx, const tqf_hip_weights *w, const float *x, uint32_t m,
+                      float *y, uint32_t *tokens4, float *logits4) {
+    if (!x || !y || (!tokens4) != (!logits4)) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (int32_t rc = check_q6k_call(ctx, w, m)) return rc;
+    const MatrixDims &d = w->dims;
+    const size_t xb = (size_t)m * d.cols * 4, yb = (size_t)m * d.rows * 4, cb = (size_t)m * 16;
+    if (int32_t rc = ensure_stage(ctx, align_up(xb, kAlign) + align_up(yb, kAlign) + 2 * cb)) return rc;
+    uint8_t *st = static_cast<uint8_t *>(ctx->d_stage);
+    float *dx = reinterpret_cast<float *>(st);
+    float *dy = reinterpret_cast<float *>(st + align_up(xb, kAlign));
+    uint32_t *dt = reinterpret_cast<uint32_t *>(st + align_up(xb, kAlign) + align_up(yb, kAlign));
+    float *dl = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(dt) + cb);
+    TQF_HIP(ctx, hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream));
+    if (int32_t rc = q6k_enqueue(ctx, w, dx, m, dy, tokens4 ? dt : nullptr, tokens4 ? dl : nullptr)) return rc;
+    TQF_HIP(ctx, hipMemcpyAsync(y, dy, yb, hipMemcpyDeviceToHost, ctx->stream));
+    if (tokens4) {
+        TQF_HIP(ctx, hipMemcpyAsync(tokens4, dt, cb, hipMemcpyDeviceToHost, ctx->stream));
+        TQF_HIP(ctx, hipMemcpyAsync(logits4, dl, cb, hipMemcpyDeviceToHost, ctx->stream));
+    }
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return TQF_HIP_OK;
+}
+}  // namespace
+
+extern "C" uint64_t tqf_hip_q6k_weights_bytes_for(uint32_t rows, uint32_t cols) {
+    if (rows == 0 || cols == 0 || cols % 256) return 0;
+    return align_up(q6k_layout_bytes(matrix_dims(rows, cols)), kAlign) + kAlign;
+}
+
+extern "C" int32_t tqf_hip_q6k_weights_upload(tqf_hip_ctx *ctx, const uint8_t *q6_k, size_t len,
+                                              uint32_t rows, uint32_t cols,
+                                              tqf_hip_weights **out) {
+    TQF_ENTER(ctx);
+    if (!q6_k || !out) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    *out = nullptr;
+    if (int32_t rc = check_q6k_shape(ctx, len, rows, cols)) return rc;
+    if (int32_t rc = ensure_stage(ctx, len)) return rc;
+    TQF_HIP(ctx, hipMemcpyAsync(ctx->d_stage, q6_k, len, hipMemcpyHostToDevice, ctx->stream));
+    return q6k_upload_from(ctx, static_cast<const uint8_t *>(ctx->d_stage), rows, cols, out);
+}
+
+extern "C" int32_t tqf_hip_q6k_weights_upload_device(tqf_hip_ctx *ctx, const void *d_q6_k,
+                                                     size_t len, uint32_t rows, uint32_t cols,
+                                                     tqf_hip_weights **out) {
+    TQF_ENTER(ctx);
+    if (!d_q6_k || !out) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    *out = nullptr;
+    if (int32_t rc = check_q6k_shape(ctx, len, rows, cols)) return rc;
+    return q6k_upload_from(ctx, static_cast<const uint8_t *>(d_q6_k), rows, cols, out);
+}
+
+extern "C" int32_t tqf_hip_q6k_weights_download(tqf_hip_ctx *ctx, const tqf_hip_weights *w,
+                                                uint8_t *q6_k, size_t len) {
+    TQF_ENTER(ctx);
+    if (!valid_q6k(w) || !q6_k) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer or not Q6_K weights");
+    const MatrixDims &d = w->dims;
+    const uint32_t nb = d.cols / 256;
+    if (len != (size_t)d.rows * nb * kQ6KBlock)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "Q6_K byte length does not match the matrix");
+    std::vector<uint8_t> tiles(w->bytes);
+    TQF_HIP(ctx, hipMemcpyAsync(tiles.data(), w->tiles, w->bytes, hipMemcpyDeviceToHost, ctx->stream));
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    for (uint32_t r = 0; r < d.rows; ++r) {
+        for (uint32_t s = 0; s < nb; ++s) {
+            uint8_t *dst = q6_k + ((size_t)r * nb + s) * kQ6KBlock;
+            std::memset(dst, 0, kQ6KBlock);
+            std::memcpy(dst + 208, tiles.data() + q6k_d_offset(d, r, s), 2);
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t b = s * 8 + j;
+                const size_t pr = q6k_slot_row(r, b);
+                const uint8_t *nib = tiles.data() + q6k_nibble_offset(d, pr, b);
+                const uint8_t *hb = tiles.data() + q6k_high_offset(d, pr, b);
+                const uint8_t *sc = tiles.data() + q6k_scale_offset(d, pr, b);
+                dst[192 + 2 * j] = sc[0];
+                dst[192 + 2 * j + 1] = sc[1];
+                const int h = j >> 2, grp = j & 3;
+                for (int e = 0; e < 32; ++e) {
+                    const int c = e & 7, t = e >> 3;
+                    const uint8_t byte = nib[4 * (c >> 1) + t];
+                    const int lo = (c & 1) ? (byte >> 4) : (byte & 15);
+                    const int hi = ((hb[4 * (c >> 2) + t] >> (2 * (c & 3))) & 3) ^ 2;
+                    uint8_t &q = dst[64 * h + ((grp & 1) ? 32 : 0) + e];
+                    q = (uint8_t)(q | (grp < 2 ? lo : lo << 4));
+                    dst[128 + 32 * h + e] = (uint8_t)(dst[128 + 32 * h + e] | (hi << (2 * grp)));
+                }
+            }
+        }
+    }
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_q6k_matvec(tqf_hip_ctx *ctx, const tqf_hip_weights *w, const float *x,
+                                      uint32_t m, float *y) {
+    TQF_ENTER(ctx);
+    return q6k_host_call(ctx, w, x, m, y, nullptr, nullptr);
+}
+
+extern "C" int32_t tqf_hip_q6k_matvec_device(tqf_hip_ctx *ctx, const tqf_hip_weights *w,
+                                             const float *d_x, uint32_t m, float *d_y) {
+    TQF_ENTER(ctx);
+    if (!d_x || !d_y) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (int32_t rc = check_q6k_call(ctx, w, m)) return rc;
+    return q6k_enqueue(ctx, w, d_x, m, d_y, nullptr, nullptr);
+}
+
+extern "C" int32_t tqf_hip_lm_head_logits(tqf_hip_ctx *ctx, const tqf_hip_weights *w,
+                                          const float *x, uint32_t m, float *logits,
+                                          uint32_t *tokens4, float *logits4) {
+    TQF_ENTER(ctx);
+    if (!tokens4 || !logits4) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    return q6k_host_call(ctx, w, x, m, logits, tokens4, logits4);
+}
+
+extern "C" int32_t tqf_hip_lm_head_logits_device(tqf_hip_ctx *ctx, const tqf_hip_weights *w,
+                                                 const float *d_x, uint32_t m, float *d_logits,
+                                                 uint32_t *d_tokens4, float *d_logits4) {
+    TQF_ENTER(ctx);
+    if (!d_x || !d_logits || !d_tokens4 || !d_logits4) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (int32_t rc = check_q6k_call(ctx, w, m)) return rc;
+    return q6k_enqueue(ctx, w, d_x, m, d_logits, d_tokens4, d_logits4);
 }
 
 // ===========================================================================

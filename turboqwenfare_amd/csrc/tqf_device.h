@@ -430,4 +430,27 @@ __device__ __forceinline__ float octet_scale(const uint4 s, int j) {
 }
 
 
+// ---- integer butterflies of the K-quant matvecs (tqf_q4k.hip, tqf_q6k.hip) ----
+// Wavefront-local LDS hand-off: this wavefront's LDS stores complete before
+// any of its lanes reads them.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int CTRL, int MASK, int K>
+__device__ __forceinline__ void xor_stage(int *v) {
+    // slots p < K/2 (in units of 8 values) keep p and add the partner's p ^ MASK
+#pragma unroll
+    for (int p = 0; p < K / 2; ++p)
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc) v[8 * p + cc] += dpp_i<CTRL>(v[8 * (p ^ MASK) + cc]);
+}
+template <int CTRL, int MASK, int K>
+__device__ __forceinline__ void xor_stage1(int *v) {
+#pragma unroll
+    for (int p = 0; p < K / 2; ++p) v[p] += dpp_i<CTRL>(v[p ^ MASK]);
+}
+
 }  // namespace tqf

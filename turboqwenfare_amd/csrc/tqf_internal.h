@@ -135,6 +135,42 @@ inline size_t q4k_layout_bytes(const MatrixDims &d) {
     return q4k_dm_base(d) + (size_t)d.rows_padded * (d.blocks_padded >> 3) * 4;
 }
 
+// Q6_K row-lane layout.  A GGML Q6_K super-block holds 256 weights in 210
+// bytes: ql[128] low nibbles, qh[64] two high bits each, sixteen int8 scales
+// of 16-element groups, f16 d (format/quant/dequant.rs:190-218); weight i
+// decodes to d * scale[i / 16] * (q_i - 32).  The device copy uses 32-element
+// sub-blocks (MatrixDims.blocks = cols / 32) and one contiguous chunk of
+// 13 * Bp * 16 bytes per row octet:
+//   planes 0..7   nibble slot p: [Bp][16 bytes] (class order)
+//   planes 8..11  high-bit slots 2q, 2q + 1: [Bp][8 + 8 bytes]
+//   plane 12      scales: [Bp][8 positions x 2 int8]
+// with the rows of sub-block b in the XOR-permuted positions of the Q4_K
+// layout (position p holds row p ^ (b mod 8)), then a d table of 16 bytes per
+// (octet, super-block) (8 rows x f16, row order).  210 bytes per 256 weights
+// and row, as GGML; tqf_hip_q6k_weights_download() re-packs the GGML bytes.
+constexpr int kQ6KBlock = 210;
+__host__ __device__ inline size_t q6k_slot_row(size_t row, size_t block) {
+    return (row & ~(size_t)7) | ((row ^ block) & 7);
+}
+__host__ __device__ inline size_t q6k_nibble_offset(const MatrixDims &d, size_t prow, size_t b) {
+    return (((prow >> 3) * 13 + (prow & 7)) * d.blocks_padded + b) * 16;
+}
+__host__ __device__ inline size_t q6k_high_offset(const MatrixDims &d, size_t prow, size_t b) {
+    return (((prow >> 3) * 13 + 8 + ((prow & 7) >> 1)) * d.blocks_padded + b) * 16 + (prow & 1) * 8;
+}
+__host__ __device__ inline size_t q6k_scale_offset(const MatrixDims &d, size_t prow, size_t b) {
+    return (((prow >> 3) * 13 + 12) * d.blocks_padded + b) * 16 + (prow & 7) * 2;
+}
+__host__ __device__ inline size_t q6k_d_base(const MatrixDims &d) {
+    return (size_t)(d.rows_padded >> 3) * 13 * d.blocks_padded * 16;
+}
+__host__ __device__ inline size_t q6k_d_offset(const MatrixDims &d, size_t row, size_t sb) {
+    return q6k_d_base(d) + (((row >> 3) * (d.blocks_padded >> 3) + sb) * 8 + (row & 7)) * 2;
+}
+inline size_t q6k_layout_bytes(const MatrixDims &d) {
+    return q6k_d_base(d) + (size_t)(d.rows_padded >> 3) * (d.blocks_padded >> 3) * 16;
+}
+
 // Route plan written by the route kernel and read by the expert kernels.
 // Work is planned per (expert, token) pair so that every workgroup carries
 // the same arithmetic: slots [0, M) are the shared expert for tokens 0..M-1
@@ -212,7 +248,7 @@ struct Slab {
 
 struct tqf_hip_weights {
     tqf::MatrixDims dims;
-    int32_t format;              // TQF_HIP_FORMAT_Q4_0 or TQF_HIP_FORMAT_Q4_K
+    int32_t format;              // TQF_HIP_FORMAT_Q4_0, _Q4_K or _Q6_K
     uint8_t *tiles;              // device: nibble plane, then scale plane
     size_t bytes;
     const uint8_t **d_self;      // device: one-entry table {tiles}
@@ -324,6 +360,9 @@ struct tqf_hip_ctx {
     // Q4_K expert forward: Q8_K records of x and h, gate/up outputs, h
     uint8_t *d_q4k = nullptr;
     size_t q4k_bytes = 0;
+    // LM head: Q8_K records of x, per-workgroup top-4 candidates
+    uint8_t *d_lm = nullptr;
+    size_t lm_bytes = 0;
     // host staging for the synchronous host-pointer entry points
     void *d_stage = nullptr;
     size_t stage_bytes = 0;
@@ -395,6 +434,17 @@ hipError_t launch_q8k_quantize(hipStream_t s, const float *x, uint32_t m, uint32
 hipError_t launch_q4k_q8k_gemv(hipStream_t s, const uint8_t *const *tables, uint32_t count,
                                const MatrixDims &d, const uint32_t *q8, uint32_t m, float *y);
 hipError_t launch_q4k_silu_mul(hipStream_t s, const float *gu, uint32_t m, uint32_t F, float *h);
+
+// ---- Q6_K (tqf_q6k.hip) ----------------------------------------------------
+hipError_t launch_q6k_repack(hipStream_t s, const uint8_t *d_aos, const MatrixDims &d,
+                             uint8_t *tiles);
+// Q8_K matvec over q8k_quantize records; with top4_scratch (count must be 1,
+// q6k_top4_scratch_bytes of it) also the per-row top-4 candidates
+// (tokens4 / logits4 [m x 4]).
+size_t q6k_top4_scratch_bytes(const MatrixDims &d, uint32_t m);
+hipError_t launch_q6k_q8k_gemv(hipStream_t s, const uint8_t *const *tables, uint32_t count,
+                               const MatrixDims &d, const uint32_t *q8, uint32_t m, float *y,
+                               void *top4_scratch, uint32_t *tokens4, float *logits4);
 
 // ---- grouped expert GEMM (tqf_grouped.hip) --------------------------------
 // Scratch views of one call over T tokens (P = 8 T pairs): the expert-sorted

@@ -382,26 +382,6 @@ hipError_t launch_q8k_quantize(hipStream_t s, const float *x, uint32_t m, uint32
 // step, minimum_sum + (-0.0 + lane_acc[0] + ... + lane_acc[7]), is taken by
 // the row's first lane.  Super-blocks past cols (padding) do not enter.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-template <int CTRL, int MASK, int K>
-__device__ __forceinline__ void xor_stage(int *v) {
-    // slots p < K/2 (in units of 8 values) keep p and add the partner's p ^ MASK
-#pragma unroll
-    for (int p = 0; p < K / 2; ++p)
-#pragma unroll
-        for (int cc = 0; cc < 8; ++cc) v[8 * p + cc] += dpp_i<CTRL>(v[8 * (p ^ MASK) + cc]);
-}
-template <int CTRL, int MASK, int K>
-__device__ __forceinline__ void xor_stage1(int *v) {
-#pragma unroll
-    for (int p = 0; p < K / 2; ++p) v[p] += dpp_i<CTRL>(v[p ^ MASK]);
-}
-
 template <int LPR, int TG>
 __global__ __launch_bounds__(kQ4KWaves * kWave) void q4k_q8k_gemv_kernel(
     const uint8_t *const *__restrict__ tables, MatrixDims d, const uint32_t *__restrict__ q8,

@@ -1,0 +1,378 @@
+// tqf_q6k.hip -- canonical Q6_K matrices (GGML super-blocks of 256 elements,
+// 210 bytes: ql[128] low nibbles, qh[64] two high bits, 16 signed group
+// scales, f16 d; format/quant/dequant.rs:190-218) on gfx950: the LM head of
+// the canonical checkpoint (model/qwen36/runtime.rs:435, weights.rs:
+// 1744).
+//
+//   * the lossless repack into the Q6_K row-lane layout (tqf_internal.h);
+//   * the Q8_K integer matvec of matvec_payload for GgmlType::Q6K
+//     (weights.rs:680-735, q6_k_dot_pre :1023-1101), bit-identical to the
+//     scalar loop: exact integer lane sums, then the f32 combine in the
+//     reference's order (per row, super-block after super-block, no fused
+//     multiply-adds, the final iterator sum from -0.0);
+//   * an optional fused top-4 epilogue with top_logit_candidates' semantics
+//     (runtime/decode.rs:48-64: strict >, NaN and -inf never selected, ties
+//     to the lower token), merged over workgroups by q6k_top4_merge_kernel.
+#include <hip/hip_runtime.h>
+
+#include "tqf_device.h"
+#include "tqf_internal.h"
+
+namespace tqf {
+
+// ---------------------------------------------------------------------------
+// Repack: GGML Q6_K -> Q6_K row-lane layout, one thread per (row, sub-block).
+// Sub-block j (elements 32j..32j+31) of a super-block is, in ggml's order,
+// group j mod 4 of half j / 4: element i takes the low nibble of ql[64 h +
+// i] (j mod 4 = 0), ql[64 h + 32 + i] (1), the high nibble of ql[64 h + i]
+// (2) or of ql[64 h + 32 + i] (3), and bits 2 (j mod 4) of qh[32 h + i];
+// its scales are groups 2j and 2j + 1.  Stored per (octet, sub-block), in
+// the XOR-permuted row positions of the Q4_K layout:
+//   nibble slot   16 bytes, class order (byte 4i + t: element 2i + 8t low,
+//                 2i + 1 + 8t high)
+//   high-bit slot 8 bytes: dword c / 4, byte t, bits 2 (c mod 4) hold the
+//                 high bits of element c + 8t with the upper bit flipped,
+//                 so that (low | high << 4) is the 6-bit two's complement
+//                 of q - 32
+//   scale slot    2 bytes (int8 scales of groups 2j, 2j + 1)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void q6k_repack_kernel(const uint8_t *__restrict__ aos,
+                                                         MatrixDims d, uint8_t *__restrict__ dst) {
+    const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (uint64_t)d.rows * d.blocks) return;
+    const uint32_t r = (uint32_t)(idx / d.blocks), b = (uint32_t)(idx % d.blocks);
+    const uint32_t s = b >> 3;
+    const int j = (int)(b & 7), h = j >> 2, grp = j & 3;
+    const uint8_t *src = aos + ((size_t)r * (d.blocks >> 3) + s) * kQ6KBlock;
+    const uint8_t *ql = src + 64 * h + ((grp & 1) ? 32 : 0);
+    const uint8_t *qh = src + 128 + 32 * h;
+    uint8_t lo[32], hi[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        lo[i] = (grp < 2) ? (ql[i] & 15) : (ql[i] >> 4);
+        hi[i] = ((qh[i] >> (2 * grp)) & 3) ^ 2;
+    }
+    const size_t pr = q6k_slot_row(r, b);
+    uint8_t *nib = dst + q6k_nibble_offset(d, pr, b);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) nib[4 * i + t] = (uint8_t)(lo[2 * i + 8 * t] | (lo[2 * i + 1 + 8 * t] << 4));
+    uint8_t *hb = dst + q6k_high_offset(d, pr, b);
+#pragma unroll
+    for (int w = 0; w < 2; ++w)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            uint32_t v = 0;
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) v |= (uint32_t)hi[4 * w + cc + 8 * t] << (2 * cc);
+            hb[4 * w + t] = (uint8_t)v;
+        }
+    uint8_t *sc = dst + q6k_scale_offset(d, pr, b);
+    sc[0] = src[192 + 2 * j];
+    sc[1] = src[192 + 2 * j + 1];
+    if (j == 0) {
+        uint8_t *dd = dst + q6k_d_offset(d, r, s);
+        dd[0] = src[208];
+        dd[1] = src[209];
+    }
+}
+
+hipError_t launch_q6k_repack(hipStream_t s, const uint8_t *d_aos, const MatrixDims &d,
+                             uint8_t *dst) {
+    const uint64_t n = (uint64_t)d.rows * d.blocks;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(q6k_repack_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s,
+                       d_aos, d, dst);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Q8_K integer matvec (q6_k_dot_pre per row) over the Q8_K records of
+// q8k_quantize_kernel (tqf_q4k.hip).  Geometry of the Q4_K matvec: lane b of
+// a lane group owns sub-block b of the chunk for the octet's eight rows,
+// register slot p holding row p ^ k (k = b mod 8).
+//
+// Per (slot, class c): the four signed values of the class as int8 bytes
+// 4 (q - 32) (the stored 6-bit two's complement shifted left by two), dotted
+// with the class's Q8_K dword masked to its first (group 2j) and second
+// (group 2j + 1) byte pair, each dot scaled by its group's int8 scale:
+// 4 x the reference's lane-sum term, exactly (|4 L| < 2^27).  The butterfly
+// of the Q4_K kernel sums a super-block's eight lanes; the combine
+// sums[c] += (d * q8scale) * lane_sum runs super-block after super-block
+// through LDS, and the row's first lane forms -0.0 + sums[0] + ... + sums[7].
+//
+// TOPK: the workgroup's rows also yield per-token top-4 candidates
+// (top_logit_candidates' order) at cand[(blockIdx.x * m + t) * 4 ..].
+// ---------------------------------------------------------------------------
+constexpr int kQ6KWaves = 8;
+
+struct Top4Cand {
+    uint32_t token;
+    float value;
+};
+
+// Top-4 of one value per lane over the wavefront (value, token), NaN and
+// -inf excluded; results in every lane, empty slots (0, -inf).
+__device__ __forceinline__ void wave_top4(float v, uint32_t tok, float (&bv)[4], uint32_t (&bt)[4]) {
+    bool live = v > -INFINITY;  // false for NaN and -inf
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const float mv = group_reduce<64>(live ? v : -INFINITY, MaxOp());
+        const int mt = group_reduce<64>((live && v == mv) ? (int)tok : 0x7FFFFFFF, MinOp());
+        const bool found = mv > -INFINITY;
+        bv[s] = found ? mv : -INFINITY;
+        bt[s] = found ? (uint32_t)mt : 0u;
+        if (found && live && v == mv && (int)tok == mt) live = false;
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ T pick4(const T (&a)[4], int s) {
+    return s == 0 ? a[0] : s == 1 ? a[1] : s == 2 ? a[2] : a[3];
+}
+
+// Folds one candidate per lane (lanes >= kTop4Lanes: ignored) into the
+// running top-4 `best` (uniform): the running entries ride in the last four
+// lanes of the same ranking.
+constexpr int kTop4Lanes = kWave - 4;
+__device__ __forceinline__ void fold_top4(float v, uint32_t tok, float (&best)[4], uint32_t (&btok)[4]) {
+    const int lane = threadIdx.x % kWave;
+    const int s = lane - kTop4Lanes;
+    const float fv = s >= 0 ? pick4(best, s) : v;
+    const uint32_t ft = s >= 0 ? pick4(btok, s) : tok;
+    wave_top4(fv, ft, best, btok);
+}
+
+template <int LPR, int TG, bool TOPK>
+__global__ __launch_bounds__(kQ6KWaves * kWave) void q6k_q8k_gemv_kernel(
+    const uint8_t *const *__restrict__ tables, MatrixDims d, const uint32_t *__restrict__ q8,
+    uint32_t m, float *__restrict__ y, Top4Cand *__restrict__ cand) {
+    constexpr int G = kWave / LPR;
+    constexpr int SB = LPR / 8;
+    constexpr int NCH = (8 + SB - 1) / SB;
+    __shared__ float lds[kQ6KWaves][kWave][8];
+    __shared__ float s_res[TOPK ? TG : 1][kQ6KWaves * 8 * G];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int lane = threadIdx.x % kWave;
+    const int jg = lane / LPR, b = lane % LPR, k = b & 7, g = b >> 3;
+    const uint32_t mat = blockIdx.y;
+    const uint32_t r0 = (blockIdx.x * kQ6KWaves + wave) * 8 * G;
+    const bool active = r0 < d.rows_padded;
+    if (!TOPK && !active) return;  // no workgroup barrier without TOPK
+    const uint8_t *base = tables[mat];
+    const uint32_t rl = active ? r0 + jg * 8 : 0;
+    const uint32_t nb = d.blocks >> 3;
+    const uint32_t chunks = d.blocks_padded / LPR;
+    const size_t rstride = (size_t)d.blocks_padded * kQ8KRecDwords;
+    const uint32_t bp = d.blocks_padded;
+    const uint8_t *oct = base + q6k_nibble_offset(d, rl, 0);  // the octet chunk
+    const uint8_t *d_row = base + q6k_d_offset(d, rl + k, 0);
+    float(*my)[8] = lds[wave];
+    const int gbase = jg * LPR;
+    for (uint32_t t0 = 0; t0 < m; t0 += TG) {
+        float acc[TG][NCH];
+#pragma unroll
+        for (int t = 0; t < TG; ++t)
+#pragma unroll
+            for (int q = 0; q < NCH; ++q) acc[t][q] = 0.0f;
+        for (uint32_t c = 0; active && c < chunks; ++c) {
+            const uint32_t blk = c * LPR + b;
+            uint4 nib[8], hiv[4];
+#pragma unroll
+            for (int p = 0; p < 8; ++p) nib[p] = load_global_u4(oct + ((size_t)p * bp + blk) * 16);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) hiv[q] = load_global_u4(oct + ((size_t)(8 + q) * bp + blk) * 16);
+            const uint4 scv = load_global_u4(oct + ((size_t)12 * bp + blk) * 16);
+            const uint32_t dw = *(const __attribute__((address_space(1))) uint16_t *)(d_row + (size_t)(blk >> 3) * 16);
+            uint4 xa[TG], xb[TG], xc[TG];
+#pragma unroll
+            for (int t = 0; t < TG; ++t) {
+                const uint32_t tt = t0 + t < m ? t0 + t : 0;
+                const uint32_t *xr = q8 + tt * rstride + 4 * blk;
+                xa[t] = load_global_u4(xr);
+                xb[t] = load_global_u4(xr + 4 * bp);
+                xc[t] = load_global_u4(xr + 8 * bp);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // signed class values 4 (q - 32), slot-major
+            int sv[64];
+#pragma unroll
+            for (int p = 0; p < 8; ++p) {
+                const uint32_t wv[4] = {nib[p].x, nib[p].y, nib[p].z, nib[p].w};
+                const uint4 hq = hiv[p >> 1];
+                const uint32_t hw[2] = {(p & 1) ? hq.z : hq.x, (p & 1) ? hq.w : hq.y};
+#pragma unroll
+                for (int cc = 0; cc < 8; ++cc) {
+                    const uint32_t w = wv[cc >> 1];
+                    const uint32_t lo = (cc & 1) ? ((w >> 2) & 0x3C3C3C3Cu) : ((w << 2) & 0x3C3C3C3Cu);
+                    const uint32_t hi = (hw[cc >> 2] << (6 - 2 * (cc & 3))) & 0xC0C0C0C0u;
+                    sv[8 * p + cc] = (int)(lo | hi);
+                }
+            }
+            const uint32_t scw[4] = {scv.x, scv.y, scv.z, scv.w};
+            const float ws = f16_to_f32(dw);
+#pragma unroll
+            for (int t = 0; t < TG; ++t) {
+                const uint32_t qd[8] = {xa[t].x, xa[t].y, xa[t].z, xa[t].w, xb[t].x, xb[t].y, xb[t].z, xb[t].w};
+                const float qscale = __uint_as_float(xc[t].y);
+                int D[64], L[32];
+#pragma unroll
+                for (int p = 0; p < 8; ++p) {
+                    const uint32_t h16 = scw[p >> 1] >> (16 * (p & 1));
+                    const int sa = (int)(int8_t)(h16 & 0xFF), sb = (int)(int8_t)((h16 >> 8) & 0xFF);
+#pragma unroll
+                    for (int cc = 0; cc < 8; ++cc) {
+                        const int da = __builtin_amdgcn_sdot4(sv[8 * p + cc], (int)(qd[cc] & 0x0000FFFFu), 0, false);
+                        const int db = __builtin_amdgcn_sdot4(sv[8 * p + cc], (int)(qd[cc] & 0xFFFF0000u), 0, false);
+                        D[8 * p + cc] = __mul24(sa, da) + __mul24(sb, db);
+                    }
+                }
+#pragma unroll
+                for (int p = 0; p < 4; ++p)
+#pragma unroll
+                    for (int cc = 0; cc < 8; ++cc) L[8 * p + cc] = D[8 * p + cc] + dpp_i<kDppHalfMirror>(D[8 * (p ^ 7) + cc]);
+                xor_stage<kDppQuadRev, 3, 4>(L);
+                xor_stage<kDppXor1, 1, 2>(L);
+                const float cs = __fmul_rn(ws, qscale);
+#pragma unroll
+                for (int cc = 0; cc < 8; ++cc) my[lane][cc] = __fmul_rn(cs, (float)(L[cc] >> 2));
+                wave_sync();
+#pragma unroll
+                for (int q = 0; q < NCH; ++q) {
+                    const int ch = g + q * SB;
+                    if (ch < 8) {
+#pragma unroll
+                        for (int gg = 0; gg < SB; ++gg)
+                            if (c * SB + gg < nb) acc[t][q] = __fadd_rn(acc[t][q], my[gbase + 8 * gg + k][ch]);
+                    }
+                }
+                wave_sync();
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TG; ++t) {
+            float res = 0.0f;
+            if (active) {
+#pragma unroll
+                for (int q = 0; q < NCH; ++q) my[lane][q] = acc[t][q];
+                wave_sync();
+                float total = -0.0f;  // Iterator::sum::<f32>() starts from -0.0
+#pragma unroll
+                for (int ch = 0; ch < 8; ++ch) total = __fadd_rn(total, my[gbase + 8 * (ch % SB) + k][ch / SB]);
+                res = total;
+                if (g == 0 && rl + k < d.rows && t0 + t < m)
+                    y[((size_t)mat * m + t0 + t) * d.rows + rl + k] = res;
+                wave_sync();
+            }
+            if constexpr (TOPK) {
+                if (g == 0) s_res[t][(wave * G + jg) * 8 + k] = (active && rl + k < d.rows) ? res : -INFINITY;
+            }
+        }
+        if constexpr (TOPK) {
+            __syncthreads();
+            // wavefront t ranks token t0 + t over the workgroup's rows
+            if (wave < TG && t0 + wave < m) {
+                constexpr int NR = kQ6KWaves * 8 * G;
+                float best[4];
+                uint32_t btok[4];
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    best[s] = -INFINITY;
+                    btok[s] = 0;
+                }
+                const uint32_t row0 = blockIdx.x * kQ6KWaves * 8 * G;
+                for (int i0 = 0; i0 < NR; i0 += kTop4Lanes) {
+                    const int i = i0 + lane;
+                    const bool in = lane < kTop4Lanes && i < NR;
+                    fold_top4(in ? s_res[wave][in ? i : 0] : -INFINITY, row0 + (uint32_t)i, best, btok);
+                }
+                if (lane < 4) cand[((size_t)blockIdx.x * m + t0 + wave) * 4 + lane] = Top4Cand{pick4(btok, lane), pick4(best, lane)};
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Per token: the top-4 of the workgroups' candidate lists (one workgroup of
+// 1024 threads per token; every list is sorted, so the union's top-4 in
+// top_logit_candidates' order is the answer).
+__global__ __launch_bounds__(1024) void q6k_top4_merge_kernel(const Top4Cand *__restrict__ cand,
+                                                               uint32_t n_groups, uint32_t m,
+                                                               uint32_t *__restrict__ tokens4,
+                                                               float *__restrict__ logits4) {
+    __shared__ Top4Cand s_best[16][4];
+    const uint32_t t = blockIdx.x;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    float best[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    uint32_t btok[4] = {0, 0, 0, 0};
+    const uint32_t n = n_groups * 4;
+    for (uint32_t base = (uint32_t)wave * kTop4Lanes; base < n; base += 16 * kTop4Lanes) {
+        const uint32_t i = base + (uint32_t)lane;
+        float v = -INFINITY;
+        uint32_t tk = 0;
+        if (lane < kTop4Lanes && i < n) {
+            const Top4Cand c = cand[((size_t)(i / 4) * m + t) * 4 + (i % 4)];
+            v = c.value;
+            tk = c.token;
+        }
+        fold_top4(v, tk, best, btok);
+    }
+    if (lane == 0)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) s_best[wave][s] = Top4Cand{btok[s], best[s]};
+    __syncthreads();
+    if (wave == 0) {
+        const Top4Cand c = s_best[lane / 4][lane % 4];
+        float bv[4];
+        uint32_t bt[4];
+        wave_top4(c.value, c.token, bv, bt);
+        if (lane < 4) {
+            tokens4[t * 4 + lane] = pick4(bt, lane);
+            logits4[t * 4 + lane] = pick4(bv, lane);
+        }
+    }
+}
+
+template <int LPR, bool TOPK>
+hipError_t launch_q6k_lpr(hipStream_t s, const uint8_t *const *tables, uint32_t count,
+                          const MatrixDims &d, const uint32_t *q8, uint32_t m, float *y,
+                          Top4Cand *cand) {
+    constexpr uint32_t rows_per_group = kQ6KWaves * 8 * (kWave / LPR);
+    const dim3 grid((d.rows_padded + rows_per_group - 1) / rows_per_group, count);
+    const dim3 block(kQ6KWaves * kWave);
+    if (m <= 1) hipLaunchKernelGGL((q6k_q8k_gemv_kernel<LPR, 1, TOPK>), grid, block, 0, s, tables, d, q8, m, y, cand);
+    else if (m <= 2) hipLaunchKernelGGL((q6k_q8k_gemv_kernel<LPR, 2, TOPK>), grid, block, 0, s, tables, d, q8, m, y, cand);
+    else hipLaunchKernelGGL((q6k_q8k_gemv_kernel<LPR, 4, TOPK>), grid, block, 0, s, tables, d, q8, m, y, cand);
+    return hipGetLastError();
+}
+
+uint32_t q6k_top4_groups(const MatrixDims &d) {
+    const uint32_t rows_per_group = kQ6KWaves * 8 * (kWave / d.lpr);
+    return (d.rows_padded + rows_per_group - 1) / rows_per_group;
+}
+
+size_t q6k_top4_scratch_bytes(const MatrixDims &d, uint32_t m) {
+    return (size_t)q6k_top4_groups(d) * m * 4 * sizeof(Top4Cand);
+}
+
+hipError_t launch_q6k_q8k_gemv(hipStream_t s, const uint8_t *const *tables, uint32_t count,
+                               const MatrixDims &d, const uint32_t *q8, uint32_t m, float *y,
+                               void *top4_scratch, uint32_t *tokens4, float *logits4) {
+    Top4Cand *cand = static_cast<Top4Cand *>(top4_scratch);
+    hipError_t e;
+    if (cand) {
+        if (d.lpr == 16) e = launch_q6k_lpr<16, true>(s, tables, count, d, q8, m, y, cand);
+        else if (d.lpr == 32) e = launch_q6k_lpr<32, true>(s, tables, count, d, q8, m, y, cand);
+        else e = launch_q6k_lpr<64, true>(s, tables, count, d, q8, m, y, cand);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(q6k_top4_merge_kernel, dim3(m), dim3(1024), 0, s, cand, q6k_top4_groups(d), m,
+                           tokens4, logits4);
+        return hipGetLastError();
+    }
+    if (d.lpr == 16) return launch_q6k_lpr<16, false>(s, tables, count, d, q8, m, y, nullptr);
+    if (d.lpr == 32) return launch_q6k_lpr<32, false>(s, tables, count, d, q8, m, y, nullptr);
+    return launch_q6k_lpr<64, false>(s, tables, count, d, q8, m, y, nullptr);
+}
+
+}  // namespace tqf
