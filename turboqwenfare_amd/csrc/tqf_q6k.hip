@@ -296,37 +296,94 @@ __global__ __launch_bounds__(kQ6KWaves * kWave) void q6k_q8k_gemv_kernel(
 
 // Per token: the top-4 of the workgroups' candidate lists (one workgroup of
 // 1024 threads per token; every list is sorted, so the union's top-4 in
-// top_logit_candidates' order is the answer).
-__global__ __launch_bounds__(1024) void q6k_top4_merge_kernel(const Top4Cand *__restrict__ cand,
-                                                               uint32_t n_groups, uint32_t m,
-                                                               uint32_t *__restrict__ tokens4,
-                                                               float *__restrict__ logits4) {
-    __shared__ Top4Cand s_best[16][4];
+// top_logit_candidates' order is the answer).  Every thread loads its share
+// first (one round trip), keeps a local top-4 by insertion, then the lists
+// are merged per wavefront (four rounds of "largest head, lowest token") and
+// across the 16 wavefronts in LDS.
+__device__ __forceinline__ bool cand_before(float va, uint32_t ta, float vb, uint32_t tb) {
+    return va > vb || (va == vb && ta < tb);
+}
+
+// Top-4 over the wavefront of per-lane sorted lists of four (value, token),
+// empty entries (0, -inf); results uniform.
+__device__ __forceinline__ void wave_merge4(float (&lv)[4], uint32_t (&lt)[4], float (&bv)[4],
+                                            uint32_t (&bt)[4]) {
+    int head = 0;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const float hv = head < 4 ? pick4(lv, head) : -INFINITY;
+        const uint32_t ht = head < 4 ? pick4(lt, head) : 0u;
+        const bool live = hv > -INFINITY;
+        const float mv = group_reduce<64>(live ? hv : -INFINITY, MaxOp());
+        const int mt = group_reduce<64>((live && hv == mv) ? (int)ht : 0x7FFFFFFF, MinOp());
+        const bool found = mv > -INFINITY;
+        bv[s] = found ? mv : -INFINITY;
+        bt[s] = found ? (uint32_t)mt : 0u;
+        if (found && live && hv == mv && (int)ht == mt) ++head;
+    }
+}
+
+constexpr int kMergeThreads = 1024;
+constexpr int kMergePer = 16;  // candidates per thread and pass
+
+__global__ __launch_bounds__(kMergeThreads) void q6k_top4_merge_kernel(const Top4Cand *__restrict__ cand,
+                                                                       uint32_t n_groups, uint32_t m,
+                                                                       uint32_t *__restrict__ tokens4,
+                                                                       float *__restrict__ logits4) {
+    __shared__ Top4Cand s_best[kMergeThreads / kWave][4];
     const uint32_t t = blockIdx.x;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    float best[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    uint32_t btok[4] = {0, 0, 0, 0};
+    float lv[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    uint32_t lt[4] = {0, 0, 0, 0};
     const uint32_t n = n_groups * 4;
-    for (uint32_t base = (uint32_t)wave * kTop4Lanes; base < n; base += 16 * kTop4Lanes) {
-        const uint32_t i = base + (uint32_t)lane;
-        float v = -INFINITY;
-        uint32_t tk = 0;
-        if (lane < kTop4Lanes && i < n) {
-            const Top4Cand c = cand[((size_t)(i / 4) * m + t) * 4 + (i % 4)];
-            v = c.value;
-            tk = c.token;
+    for (uint32_t base = 0; base < n; base += kMergeThreads * kMergePer) {
+        Top4Cand c[kMergePer];
+#pragma unroll
+        for (int q = 0; q < kMergePer; ++q) {
+            const uint32_t i = base + threadIdx.x + (uint32_t)q * kMergeThreads;
+            c[q] = i < n ? cand[((size_t)(i / 4) * m + t) * 4 + (i % 4)] : Top4Cand{0u, -INFINITY};
         }
-        fold_top4(v, tk, best, btok);
+#pragma unroll
+        for (int q = 0; q < kMergePer; ++q) {
+            const float v = c[q].value;
+            const uint32_t tk = c[q].token;
+            if (!(v > -INFINITY)) continue;  // NaN / -inf / empty
+            // insertion into the sorted local list
+            bool placed = false;
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+                const bool here = !placed && cand_before(v, tk, lv[s2], lt[s2]);
+                if (here) {
+#pragma unroll
+                    for (int u = 3; u > s2; --u) {
+                        lv[u] = lv[u - 1];
+                        lt[u] = lt[u - 1];
+                    }
+                    lv[s2] = v;
+                    lt[s2] = tk;
+                    placed = true;
+                }
+            }
+        }
     }
+    float bv[4];
+    uint32_t bt[4];
+    wave_merge4(lv, lt, bv, bt);
     if (lane == 0)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) s_best[wave][s] = Top4Cand{btok[s], best[s]};
+        for (int s2 = 0; s2 < 4; ++s2) s_best[wave][s2] = Top4Cand{bt[s2], bv[s2]};
     __syncthreads();
     if (wave == 0) {
-        const Top4Cand c = s_best[lane / 4][lane % 4];
-        float bv[4];
-        uint32_t bt[4];
-        wave_top4(c.value, c.token, bv, bt);
+        // lanes 0..15 hold the wavefronts' lists
+        float wv[4];
+        uint32_t wt[4];
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) {
+            const Top4Cand c = lane < kMergeThreads / kWave ? s_best[lane][s2] : Top4Cand{0u, -INFINITY};
+            wv[s2] = c.value;
+            wt[s2] = c.token;
+        }
+        wave_merge4(wv, wt, bv, bt);
         if (lane < 4) {
             tokens4[t * 4 + lane] = pick4(bt, lane);
             logits4[t * 4 + lane] = pick4(bv, lane);
@@ -366,7 +423,7 @@ hipError_t launch_q6k_q8k_gemv(hipStream_t s, const uint8_t *const *tables, uint
         else if (d.lpr == 32) e = launch_q6k_lpr<32, true>(s, tables, count, d, q8, m, y, cand);
         else e = launch_q6k_lpr<64, true>(s, tables, count, d, q8, m, y, cand);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(q6k_top4_merge_kernel, dim3(m), dim3(1024), 0, s, cand, q6k_top4_groups(d), m,
+        hipLaunchKernelGGL(q6k_top4_merge_kernel, dim3(m), dim3(kMergeThreads), 0, s, cand, q6k_top4_groups(d), m,
                            tokens4, logits4);
         return hipGetLastError();
     }
