@@ -127,9 +127,9 @@ int32_t tqf_hip_expert_forward(tqf_hip_ctx *ctx, const tqf_hip_weights *gate,
 typedef struct tqf_hip_moe_weights {
     const tqf_hip_tensor *router;            /* f32 [n_experts x hidden]   */
     const tqf_hip_tensor *shared_input_gate; /* f32 [hidden]               */
-    const tqf_hip_weights *shared_gate;      /* Q4_0 [width x hidden]      */
-    const tqf_hip_weights *shared_up;        /* Q4_0 [width x hidden]      */
-    const tqf_hip_weights *shared_down;      /* Q4_0 [hidden x width]      */
+    const tqf_hip_weights *shared_gate;      /* Q4_0|Q4_K [width x hidden] */
+    const tqf_hip_weights *shared_up;        /* Q4_0|Q4_K [width x hidden] */
+    const tqf_hip_weights *shared_down;      /* Q4_0|Q4_K [hidden x width] */
     const tqf_hip_weights *const *routed_gate; /* [n_experts]              */
     const tqf_hip_weights *const *routed_up;   /* [n_experts]              */
     const tqf_hip_weights *const *routed_down; /* [n_experts]              */
@@ -139,7 +139,14 @@ typedef struct tqf_hip_moe_weights {
 } tqf_hip_moe_weights;
 
 /* Builds the device-side expert table once (the analogue of pinning every
- * expert resident: experts/mod.rs:512-545 stage_expert_values). */
+ * expert resident: experts/mod.rs:512-545 stage_expert_values).  All
+ * 3 (n_experts + 1) expert matrices share one format: TQF_HIP_FORMAT_Q4_0
+ * (the group-32 configs) or TQF_HIP_FORMAT_Q4_K (the canonical checkpoint's
+ * experts, LoadedQwen36Expert::payload_parts, model/qwen36/weights.rs:
+ * 552-561), else TQF_HIP_ERR_INVALID.  A Q4_K layer runs every expert matvec
+ * on the Q8_K path of matvec_payload (weights.rs:680-735; bit-identical per
+ * matvec to tqf_hip_q4k_matvec), through the same layer, stack and
+ * verify-step entry points; tqf_hip_grouped_gemm reads Q4_0 layers only. */
 int32_t tqf_hip_moe_layer_prepare(tqf_hip_ctx *ctx, const tqf_hip_moe_weights *weights,
                                   tqf_hip_layer **out);
 int32_t tqf_hip_moe_layer_free(tqf_hip_ctx *ctx, tqf_hip_layer *layer);
@@ -169,7 +176,8 @@ int32_t tqf_hip_stack_free(tqf_hip_ctx *ctx, tqf_hip_stack *stack);
  * equal d_h to update d_h in place.  d_ids/d_w ([n_layers x m x 8], may be
  * NULL) receive every layer's route; *d_status (may be NULL, zeroed by the
  * caller) is set to TQF_HIP_ERR_ROUTER if any layer's routing fails.
- * For m <= 4 on the model geometry (hidden 2048, width <= 2048, <= 256
+ * Every layer of a stack has one expert format.  For Q4_0 layers with
+ * m <= 4 on the model geometry (hidden 2048, width <= 2048, <= 256
  * experts) the whole stack runs as one persistent cooperative launch (a
  * failed co-scheduling wait reports TQF_HIP_ERR_DEVICE in *d_status);
  * otherwise the per-layer kernels are captured once into a HIP graph per

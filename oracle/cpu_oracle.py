@@ -50,6 +50,7 @@ _SIGS = {
     "orc_sigmoid": (_f32, [_f32]),
     "orc_expert_forward": (_i32, [_vp, _vp, _vp, _u32, _u32, _vp, _vp]),
     "orc_moe_forward_batch": (_i32, [C.POINTER(_MoeLayer), _vp, _u32, _vp, _vp, _vp, C.c_int]),
+    "orc_moe_forward_batch_q4k": (_i32, [C.POINTER(_MoeLayer), _vp, _u32, _vp, _vp, _vp, C.c_int]),
     "orc_batch_union": (_u32, [_vp, _u32, _vp]),
     "orc_top_logit_candidates": (None, [_vp, _u32, _vp, _vp]),
     "orc_softmax_draw": (_u32, [_vp, _u32, _f32, _f32]),
@@ -197,10 +198,14 @@ def expert_forward(gate, up, down, hidden: int, width: int, x) -> np.ndarray:
 
 # ---- a11/a12 -----------------------------------------------------------------
 class MoeLayerHost:
-    """Host copies of one layer's tensors (Q4_0 byte planes, f32 router)."""
+    """Host copies of one layer's tensors (f32 router; expert matrices as
+    GGML Q4_0 bytes, or Q4_K bytes with fmt="q4_k")."""
 
     def __init__(self, router, shared_input_gate, shared_gate, shared_up, shared_down,
-                 routed_gate, routed_up, routed_down, hidden=2048, width=512):
+                 routed_gate, routed_up, routed_down, hidden=2048, width=512, fmt="q4_0"):
+        if fmt not in ("q4_0", "q4_k"):
+            raise ValueError("fmt must be 'q4_0' or 'q4_k'")
+        self.fmt = fmt
         self.router = _f32a(router)
         self.shared_input_gate = _f32a(shared_input_gate)
         self.shared = [np.ascontiguousarray(a, dtype=np.uint8)
@@ -226,8 +231,8 @@ class MoeLayerHost:
         y = np.empty((m, self.hidden), dtype=np.float32)
         ids = np.empty((m, 8), dtype=np.uint16)
         w = np.empty((m, 8), dtype=np.float32)
-        if lib().orc_moe_forward_batch(C.byref(self._s), _p(x), m, _p(y), _p(ids), _p(w),
-                                       nthreads) != 0:
+        fn = lib().orc_moe_forward_batch_q4k if self.fmt == "q4_k" else lib().orc_moe_forward_batch
+        if fn(C.byref(self._s), _p(x), m, _p(y), _p(ids), _p(w), nthreads) != 0:
             raise ValueError("router error")
         return y, ids, w
 
@@ -235,6 +240,8 @@ class MoeLayerHost:
     def routed_combine(self, x: np.ndarray, ids: np.ndarray, w: np.ndarray,
                        nthreads: int = 1) -> np.ndarray:
         """y[t] = sum_k w[t,k] * expert_{ids[t,k]}(x[t]) in route order."""
+        if self.fmt != "q4_0":
+            raise ValueError("routed_combine reads Q4_0 experts")
         x = _f32a(x)
         ids = np.ascontiguousarray(ids, dtype=np.uint16)
         w = _f32a(w)

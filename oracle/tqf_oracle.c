@@ -21,6 +21,8 @@
 #define ORC_TOP_K 8
 #define ORC_Q4_0_BLOCK_BYTES 18
 #define ORC_Q4_0_BLOCK_ELEMS 32
+#define ORC_Q4_K_BLOCK_BYTES 144
+#define ORC_Q4_K_BLOCK_ELEMS 256
 
 static inline uint32_t f32_bits(float v) { uint32_t b; memcpy(&b, &v, 4); return b; }
 static inline float bits_f32(uint32_t b) { float v; memcpy(&v, &b, 4); return v; }
@@ -325,8 +327,50 @@ static void q4_0_matvec_par(const uint8_t *w, uint32_t rows, uint32_t cols, cons
     (void)nthreads;
 }
 
-int orc_moe_forward_batch(const orc_moe_layer *L, const float *x, uint32_t m, float *y,
-                          uint16_t *ids_out, float *w_out, int nthreads)
+typedef int (*moe_matvec_fn)(const uint8_t *w, uint32_t rows, uint32_t cols, const float *x,
+                             float *y, int nthreads);
+
+static int q4_0_matvec_fn(const uint8_t *w, uint32_t rows, uint32_t cols, const float *x, float *y,
+                          int nthreads)
+{
+    q4_0_matvec_par(w, rows, cols, x, y, nthreads);
+    return 0;
+}
+
+/* matvec_payload's Q4_K arm (weights.rs:680-735): quantize_q8_k of x once,
+ * then q4_k_dot_pre per row (rows in parallel; each row's arithmetic is
+ * that of orc_q4_k_matvec). */
+static int q4_k_matvec_fn(const uint8_t *w, uint32_t rows, uint32_t cols, const float *x, float *y,
+                          int nthreads)
+{
+    if (cols % ORC_Q4_K_BLOCK_ELEMS != 0) return -1;
+    const uint32_t nb = cols / ORC_Q4_K_BLOCK_ELEMS;
+    int8_t *q8 = (int8_t *)malloc((size_t)nb * 256);
+    int16_t *sums = (int16_t *)malloc((size_t)nb * 16 * sizeof(int16_t));
+    float *scales = (float *)malloc((size_t)nb * sizeof(float));
+    if (!q8 || !sums || !scales) {
+        free(q8);
+        free(sums);
+        free(scales);
+        return -1;
+    }
+    for (uint32_t b = 0; b < nb; ++b)
+        orc_quantize_q8_k(x + (size_t)b * 256, q8 + (size_t)b * 256, sums + (size_t)b * 16, &scales[b]);
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(nthreads) if (nthreads > 1)
+#endif
+    for (int64_t r = 0; r < (int64_t)rows; ++r)
+        y[r] = orc_q4_k_dot_pre(w + (size_t)r * nb * ORC_Q4_K_BLOCK_BYTES, nb, q8, sums, scales);
+    (void)nthreads;
+    free(q8);
+    free(sums);
+    free(scales);
+    return 0;
+}
+
+static int moe_forward_batch_fmt(const orc_moe_layer *L, moe_matvec_fn matvec, const float *x,
+                                 uint32_t m, float *y, uint16_t *ids_out, float *w_out,
+                                 int nthreads)
 {
     const uint32_t H = L->hidden, F = L->width, E = L->n_experts;
     if (nthreads < 1) nthreads = 1;
@@ -357,20 +401,31 @@ int orc_moe_forward_batch(const orc_moe_layer *L, const float *x, uint32_t m, fl
     for (uint32_t t = 0; t < m; ++t) {
         const float *xt = x + (size_t)t * H;
         float *out = y + (size_t)t * H;
-        q4_0_matvec_par(L->shared_gate, F, H, xt, g, nthreads);
-        q4_0_matvec_par(L->shared_up, F, H, xt, u, nthreads);
+        if (matvec(L->shared_gate, F, H, xt, g, nthreads) || matvec(L->shared_up, F, H, xt, u, nthreads)) {
+            rc = -1;
+            goto done;
+        }
         orc_silu_mul(g, u, h, F);
-        q4_0_matvec_par(L->shared_down, H, F, h, out, nthreads);
+        if (matvec(L->shared_down, H, F, h, out, nthreads)) {
+            rc = -1;
+            goto done;
+        }
         float shared_gate_logit = f32_row_dot(L->shared_input_gate, H, xt);
         float scale = 1.0f / (1.0f + expf(-shared_gate_logit));
         for (uint32_t i = 0; i < H; ++i) out[i] *= scale;
         for (int k = 0; k < ORC_TOP_K; ++k) {
             uint32_t e = ids[t * ORC_TOP_K + k];
             float weight = wts[t * ORC_TOP_K + k];
-            q4_0_matvec_par(L->routed_gate[e], F, H, xt, g, nthreads);
-            q4_0_matvec_par(L->routed_up[e], F, H, xt, u, nthreads);
+            if (matvec(L->routed_gate[e], F, H, xt, g, nthreads) ||
+                matvec(L->routed_up[e], F, H, xt, u, nthreads)) {
+                rc = -1;
+                goto done;
+            }
             orc_silu_mul(g, u, h, F);
-            q4_0_matvec_par(L->routed_down[e], H, F, h, routed, nthreads);
+            if (matvec(L->routed_down[e], H, F, h, routed, nthreads)) {
+                rc = -1;
+                goto done;
+            }
             for (uint32_t i = 0; i < H; ++i) out[i] += routed[i] * weight;
         }
     }
@@ -379,6 +434,18 @@ int orc_moe_forward_batch(const orc_moe_layer *L, const float *x, uint32_t m, fl
 done:
     free(logits); free(g); free(u); free(h); free(routed); free(ids); free(wts);
     return rc;
+}
+
+int orc_moe_forward_batch(const orc_moe_layer *L, const float *x, uint32_t m, float *y,
+                          uint16_t *ids_out, float *w_out, int nthreads)
+{
+    return moe_forward_batch_fmt(L, q4_0_matvec_fn, x, m, y, ids_out, w_out, nthreads);
+}
+
+int orc_moe_forward_batch_q4k(const orc_moe_layer *L, const float *x, uint32_t m, float *y,
+                              uint16_t *ids_out, float *w_out, int nthreads)
+{
+    return moe_forward_batch_fmt(L, q4_k_matvec_fn, x, m, y, ids_out, w_out, nthreads);
 }
 
 int orc_routed_combine(const orc_moe_layer *L, const float *x, uint32_t t, const uint16_t *ids,
@@ -767,8 +834,6 @@ int orc_accept(const float *target, const float *draft, const int32_t *dtok, uin
 /* ======================================================================== */
 /* f1 / a4 / a20: Q4_K                                                      */
 /* ======================================================================== */
-#define ORC_Q4_K_BLOCK_BYTES 144
-#define ORC_Q4_K_BLOCK_ELEMS 256
 
 /* dequant.rs:139-148 -- get_scale_min_k4: the 6-bit (scale, min) of
  * sub-block j from the 12 packed bytes. */

@@ -114,6 +114,16 @@ typedef struct orc_moe_layer {
 int orc_moe_forward_batch(const orc_moe_layer *layer, const float *x, uint32_t m,
                           float *y, uint16_t *ids, float *w, int nthreads);
 
+/* The same layer with Q4_K expert matrices (GGML super-blocks; the plane
+ * pointers of orc_moe_layer then point at rows x cols/256 x 144 bytes):
+ * every expert matvec is matvec_payload's Q4_K arm (weights.rs:680-735,
+ * orc_q4_k_matvec's arithmetic), everything else as orc_moe_forward_batch.
+ * Pinned through its parts (router, orc_q4_k_matvec, silu_mul) and the
+ * composition tests of the oracle suite.  Returns 0, or -1 on a router
+ * error, a cols % 256 shape or an allocation failure. */
+int orc_moe_forward_batch_q4k(const orc_moe_layer *layer, const float *x, uint32_t m,
+                              float *y, uint16_t *ids, float *w, int nthreads);
+
 /* The routed accumulate of forward_batch (experts/mod.rs:1562-1566) for
  * given routes: y[t] = 0, then for k = 0..7 in route order
  * y[t] += expert_{ids[t,k]}(x_t) * w[t,k] (add_scaled_in_place, weights.rs:

@@ -684,6 +684,141 @@ def test_q4_k_matvec_within_the_q8_k_rounding_bound():
         assert abs(float(a[r]) - float(b[r])) <= bound * 1.001 + 1e-3
 
 
+def random_q4_k(rows: int, cols: int, seed: int, d_range=(0.002, 0.05)) -> np.ndarray:
+    """Random GGML Q4_K bytes whose f16 d and dmin are finite and modest."""
+    rng = np.random.default_rng(seed)
+    n = rows * (cols // 256)
+    blk = rng.integers(0, 256, size=(n, 144), dtype=np.uint8)
+    blk[:, 0:2] = rng.uniform(*d_range, size=n).astype(np.float16).view(np.uint8).reshape(n, 2)
+    blk[:, 2:4] = rng.uniform(*d_range, size=n).astype(np.float16).view(np.uint8).reshape(n, 2)
+    return blk.reshape(-1)
+
+
+def pack_q4_k_scales(sc, mn) -> np.ndarray:
+    """The 12 packed bytes holding eight 6-bit (scale, min) pairs, the
+    inverse of get_scale_min_k4 (dequant.rs:139-148): pairs 0-3 in the low
+    six bits of bytes 0-3 / 4-7; pairs 4-7 split into a low nibble (bytes
+    8-11) and two high bits (the top bits of bytes 0-3 / 4-7)."""
+    sc, mn = np.asarray(sc, np.int64), np.asarray(mn, np.int64)  # [..., 8]
+    b = np.zeros(sc.shape[:-1] + (12,), np.int64)
+    for j in range(4):
+        b[..., j] = sc[..., j] | ((sc[..., j + 4] >> 4) << 6)
+        b[..., j + 4] = mn[..., j] | ((mn[..., j + 4] >> 4) << 6)
+        b[..., j + 8] = (sc[..., j + 4] & 15) | ((mn[..., j + 4] & 15) << 4)
+    return b.astype(np.uint8)
+
+
+def centered_q4_k(rows: int, cols: int, seed: int, d_range=(1e-4, 4e-4)) -> np.ndarray:
+    """Random Q4_K bytes shaped like trained weights: per sub-block min equal
+    to its scale and dmin = 7.5 d, so the values d sc (q - 7.5) are centred
+    (up to the f16 rounding of dmin) with spread ~d sc."""
+    rng = np.random.default_rng(seed)
+    n = rows * (cols // 256)
+    blk = np.empty((n, 144), np.uint8)
+    d = rng.uniform(*d_range, size=n).astype(np.float16)
+    blk[:, 0:2] = d.view(np.uint8).reshape(n, 2)
+    blk[:, 2:4] = (d.astype(np.float32) * 7.5).astype(np.float16).view(np.uint8).reshape(n, 2)
+    sc = rng.integers(1, 64, size=(n, 8))
+    blk[:, 4:16] = pack_q4_k_scales(sc, sc)
+    blk[:, 16:] = rng.integers(0, 256, size=(n, 128), dtype=np.uint8)
+    return blk.reshape(-1)
+
+
+def test_pack_q4_k_scales_inverts_the_decoder():
+    # every 6-bit scale and min lands where the oracle's decoder (and the
+    # independent float64 decode) reads it
+    rng = np.random.default_rng(3)
+    for _ in range(20):
+        sc, mn = rng.integers(0, 64, size=8), rng.integers(0, 64, size=8)
+        b = np.zeros(144, np.uint8)
+        b[0:2] = (0x00, 0x3C)  # d = 1
+        b[2:4] = (0x00, 0x3C)  # dmin = 1
+        b[4:16] = pack_q4_k_scales(sc, mn)
+        b[16:] = 0x35  # q = 5 (low nibble) and 3 (high nibble)
+        want = np.concatenate([np.full(32, sc[j] * (5 if j % 2 == 0 else 3) - mn[j]) for j in range(8)])
+        assert np.array_equal(orc.dequantize_q4_k(b), want.astype(np.float32))
+        assert np.array_equal(q4_k_exact(b), want.astype(np.float64))
+    w = centered_q4_k(4, 512, 9)
+    v = q4_k_dense(w, 4, 512)
+    assert abs(v.mean()) < 0.05 * v.std()
+
+
+def q4_k_dense(w: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    nb = rows * (cols // 256)
+    return np.concatenate([q4_k_exact(w[i * 144:(i + 1) * 144]) for i in range(nb)]).reshape(rows, cols)
+
+
+@pytest.fixture(scope="module")
+def q4k_small_layer():
+    E, H, F = 256, 256, 256
+    rng = np.random.default_rng(61)
+    router = (rng.standard_normal((E, H)) / 16).astype(np.float32)
+    gate = (rng.standard_normal(H) / 16).astype(np.float32)
+    shapes = ((F, H), (F, H), (H, F))
+    mats = [tuple(random_q4_k(r, c, 5000 + 3 * e + i) for i, (r, c) in enumerate(shapes))
+            for e in range(E + 1)]
+    host = orc.MoeLayerHost(router, gate, *mats[E], [m[0] for m in mats[:E]],
+                            [m[1] for m in mats[:E]], [m[2] for m in mats[:E]], hidden=H,
+                            width=F, fmt="q4_k")
+    x = rng.standard_normal((4, H)).astype(np.float32)
+    return host, router, gate, x, mats
+
+
+def test_q4_k_moe_layer_is_the_composition_of_its_pinned_parts(q4k_small_layer):
+    # experts/mod.rs:1600-1634 with matvec_payload's Q4_K arm: bit-identical
+    # to the pinned pieces composed in f32 -- shared expert x sigmoid(gate .
+    # x) (scale_in_place), then + routed x weight per route in route order
+    # (add_scaled_in_place, weights.rs:267-281)
+    host, router, gate, x, mats = q4k_small_layer
+    H = F = 256
+    y, ids, w = host.forward_batch(x)
+    for t in range(4):
+        lid, lw = orc.router_from_logits(orc.f32_matvec(router, x[t]))
+        assert np.array_equal(ids[t], lid) and np.array_equal(w[t], lw)
+        logit = orc.f32_matvec(gate.reshape(1, -1), x[t])[0]
+        out = orc.q4_k_expert_forward(*mats[256], H, F, x[t]) * np.float32(orc.sigmoid(logit))
+        for k in range(8):
+            out = out + orc.q4_k_expert_forward(*mats[int(ids[t, k])], H, F, x[t]) * w[t, k]
+        assert out.dtype == np.float32 and np.array_equal(out.view(np.uint32), y[t].view(np.uint32))
+
+
+def q8_k_rounded(v: np.ndarray) -> np.ndarray:
+    """The values quantize_q8_k stands for (q x scale per 256-chunk), float64."""
+    v = np.asarray(v, np.float32)
+    out = np.empty(v.size)
+    for c in range(v.size // 256):
+        q, _, scale = orc.quantize_q8_k(v[c * 256:(c + 1) * 256])
+        out[c * 256:(c + 1) * 256] = q.astype(np.float64) * float(scale)
+    return out
+
+
+def test_q4_k_moe_layer_against_float64_of_the_exact_decode(q4k_small_layer):
+    # the same layer in float64 over the exactly decoded matrices (q4_k_exact)
+    # and the Q8_K-rounded activations (x, and h = SwiGLU of the float64 gate
+    # and up): only f32 rounding separates it from the oracle (~2e-7 here),
+    # while dropping one route moves the output by 7e-2 or more
+    host, router, gate, x, mats = q4k_small_layer
+    H = F = 256
+    y, ids, w = host.forward_batch(x)
+    dense = {}
+
+    def expert(e, xv):
+        if e not in dense:
+            dense[e] = (q4_k_dense(mats[e][0], F, H), q4_k_dense(mats[e][1], F, H),
+                        q4_k_dense(mats[e][2], H, F))
+        g, u, d = dense[e]
+        xq = q8_k_rounded(xv)
+        gv, uv = g @ xq, u @ xq
+        return d @ q8_k_rounded((gv / (1 + np.exp(-gv)) * uv).astype(np.float32))
+
+    for t in range(4):
+        want = expert(256, x[t]) / (1 + math.exp(-float(gate.astype(np.float64) @ x[t].astype(np.float64))))
+        for k in range(8):
+            want = want + float(w[t, k]) * expert(int(ids[t, k]), x[t])
+        err = np.max(np.abs(y[t] - want)) / max(np.max(np.abs(want)), 1.0)
+        assert err < 1e-5, err
+
+
 # ---- f3: Q6_K (the canonical LM head) -------------------------------------------
 def q6_k_values_np(block: np.ndarray) -> np.ndarray:
     """q - 32 of the 256 elements by array slicing (ggml's block_q6_K: two

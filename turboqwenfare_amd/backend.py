@@ -357,9 +357,13 @@ class HipBackend:
 
     # ---- MoE layer -------------------------------------------------------------
     def prepare_moe_layer(self, router: F32Tensor, shared_input_gate: F32Tensor,
-                          shared: tuple[Q4Weights, Q4Weights, Q4Weights],
-                          routed_gate: Sequence[Q4Weights], routed_up: Sequence[Q4Weights],
-                          routed_down: Sequence[Q4Weights]) -> MoeLayer:
+                          shared: tuple[Q4Weights, Q4Weights, Q4Weights] | tuple[Q4KWeights, Q4KWeights, Q4KWeights],
+                          routed_gate: Sequence[Q4Weights | Q4KWeights],
+                          routed_up: Sequence[Q4Weights | Q4KWeights],
+                          routed_down: Sequence[Q4Weights | Q4KWeights]) -> MoeLayer:
+        """One layer's device handle.  Every expert matrix is Q4_0 or every
+        one is Q4_K (the canonical checkpoint's experts); Q4_K layers run the
+        Q8_K integer matvecs of the reference's Q4_K path."""
         E = len(routed_gate)
         g = (C.c_void_p * E)(*[w.handle for w in routed_gate])
         u = (C.c_void_p * E)(*[w.handle for w in routed_up])
@@ -391,6 +395,14 @@ class HipBackend:
         self._check(self.lib.tqf_hip_moe_layer(self.ctx, layer.handle, _ptr(x), m, _ptr(y),
                                                _ptr(ids), _ptr(w)))
         return y, ids, w
+
+    def moe_layer_device(self, layer: MoeLayer, d_x: DeviceBuffer, m: int, d_y: DeviceBuffer,
+                         d_ids: DeviceBuffer | None = None, d_w: DeviceBuffer | None = None,
+                         d_status: DeviceBuffer | None = None) -> None:
+        """Enqueues one layer on device buffers (d_x [m, hidden] f32 -> d_y)."""
+        self._check(self.lib.tqf_hip_moe_layer_device(
+            self.ctx, layer.handle, d_x.ptr, m, d_y.ptr, d_ids.ptr if d_ids else None,
+            d_w.ptr if d_w else None, d_status.ptr if d_status else None))
 
     def moe_forward_batch_bf16(self, layer: MoeLayer, x_bf16: np.ndarray):
         x = np.ascontiguousarray(x_bf16, dtype=np.uint16)

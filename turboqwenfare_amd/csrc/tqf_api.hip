@@ -319,14 +319,111 @@ int32_t enqueue_layer(tqf_hip_ctx *ctx, const LayerDev &L, const float *h, const
     return TQF_HIP_OK;
 }
 
+// Device views of the Q4_K layer's buffers in ctx->d_q4k, sized for m rows.
+struct Q4KLayerBufs {
+    float *xnorm, *gu, *h, *dn;
+    uint32_t *q8x, *q8h;
+    size_t bytes;
+};
+Q4KLayerBufs q4k_layer_bufs(uint8_t *base, uint32_t H, uint32_t F, uint32_t m) {
+    const uint32_t S = m * (kTopK + 1);
+    const size_t xn = align_up((size_t)m * H * 4, kAlign);
+    const size_t qx = align_up((size_t)m * padded_blocks(H / 32) * kQ8KRecDwords * 4, kAlign);
+    const size_t gu = align_up((size_t)2 * S * F * 4, kAlign);
+    const size_t hb = align_up((size_t)S * F * 4, kAlign);
+    const size_t qh = align_up((size_t)S * padded_blocks(F / 32) * kQ8KRecDwords * 4, kAlign);
+    const size_t dn = align_up((size_t)S * H * 4, kAlign);
+    Q4KLayerBufs b;
+    b.xnorm = reinterpret_cast<float *>(base);
+    b.q8x = reinterpret_cast<uint32_t *>(base + xn);
+    b.gu = reinterpret_cast<float *>(base + xn + qx);
+    b.h = reinterpret_cast<float *>(base + xn + qx + gu);
+    b.q8h = reinterpret_cast<uint32_t *>(base + xn + qx + gu + hb);
+    b.dn = reinterpret_cast<float *>(base + xn + qx + gu + hb + qh);
+    b.bytes = xn + qx + gu + hb + qh + dn;
+    return b;
+}
+
+// Sized for kMaxTokens rows, so that a captured graph never needs to grow it.
+int32_t ensure_q4k_layer_scratch(tqf_hip_ctx *ctx, uint32_t H, uint32_t F) {
+    const size_t need = q4k_layer_bufs(nullptr, H, F, kMaxTokens).bytes;
+    if (ctx->d_q4k && ctx->q4k_bytes >= need) return TQF_HIP_OK;
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    drop_graphs(ctx);
+    TQF_HIP(ctx, grow(ctx->d_q4k, ctx->q4k_bytes, need));
+    return TQF_HIP_OK;
+}
+
+// One MoE layer with Q4_K experts, every expert matvec on the Q8_K path of
+// matvec_payload (weights.rs:680-735): (RMSNorm) -> route -> Q8_K(x) ->
+// gate and up of all 9 M slots -> silu_mul -> Q8_K(h) -> down of all slots
+// -> combine in route order (+ residual).  The caller has run
+// ensure_moe_scratch and ensure_q4k_layer_scratch.
+int32_t enqueue_layer_q4k(tqf_hip_ctx *ctx, const LayerDev &L, const float *h, const float *norm,
+                          uint32_t m, const float *resid, float *out, uint16_t *ids, float *w,
+                          int32_t *status) {
+    Scratch &sc = ctx->scratch;
+    const uint32_t H = L.hidden, F = L.width, S = m * (kTopK + 1);
+    const MatrixDims dgu = matrix_dims(F, H), dd = matrix_dims(H, F);
+    const Q4KLayerBufs b = q4k_layer_bufs(ctx->d_q4k, H, F, m);
+    if (!ctx->d_q4k || ctx->q4k_bytes < b.bytes) return fail(ctx, TQF_HIP_ERR_INVALID, "Q4_K layer scratch missing");
+    const float *x = h;
+    hipError_t e = hipSuccess;
+    if (norm) {
+        e = launch_q4k_rmsnorm(ctx->stream, h, norm, m, H, b.xnorm);
+        if (e != hipSuccess) return hip_fail(ctx, "RMSNorm kernel launch", e);
+        x = b.xnorm;
+    }
+    {
+        Prof p(ctx);
+        e = launch_route(ctx->stream, L, x, nullptr, m, sc, ids, w, status);
+        if (e != hipSuccess) return hip_fail(ctx, "route kernel launch", e);
+        p.end(TQF_HIP_KERNEL_ROUTE, (L.n_experts + 1) * (double)H * 4 + m * (double)H * 4, 0, nullptr);
+    }
+    e = launch_q8k_quantize(ctx->stream, x, m, H, dgu.blocks_padded, b.q8x);
+    if (e != hipSuccess) return hip_fail(ctx, "Q8_K quantize kernel launch", e);
+    {
+        Prof p(ctx);
+        e = launch_q4k_q8k_slots(ctx->stream, sc.plan, S, false, dgu, b.q8x, b.gu);
+        if (e != hipSuccess) return hip_fail(ctx, "Q4_K gate/up kernel launch", e);
+        p.end(TQF_HIP_KERNEL_Q4K_MATVEC, 2.0 * S * ((double)F * H / 256 * kQ4KBlock + F * 4.0), 0, nullptr);
+    }
+    e = launch_q4k_silu_mul(ctx->stream, b.gu, S, F, b.h);
+    if (e == hipSuccess) e = launch_q8k_quantize(ctx->stream, b.h, S, F, dd.blocks_padded, b.q8h);
+    if (e != hipSuccess) return hip_fail(ctx, "SwiGLU / Q8_K kernel launch", e);
+    {
+        Prof p(ctx);
+        e = launch_q4k_q8k_slots(ctx->stream, sc.plan, S, true, dd, b.q8h, b.dn);
+        if (e != hipSuccess) return hip_fail(ctx, "Q4_K down kernel launch", e);
+        p.end(TQF_HIP_KERNEL_Q4K_MATVEC, S * ((double)F * H / 256 * kQ4KBlock + H * 4.0), 0, nullptr);
+    }
+    e = launch_q4k_moe_combine(ctx->stream, sc.plan, b.dn, m, H, resid, out);
+    if (e != hipSuccess) return hip_fail(ctx, "combine kernel launch", e);
+    return TQF_HIP_OK;
+}
+
+int32_t enqueue_moe(tqf_hip_ctx *ctx, const tqf_hip_layer *layer, const float *h, const float *norm,
+                    uint32_t m, const float *resid, float *out, uint16_t *ids, float *w,
+                    int32_t *status) {
+    if (layer->format == TQF_HIP_FORMAT_Q4_K)
+        return enqueue_layer_q4k(ctx, layer->dev, h, norm, m, resid, out, ids, w, status);
+    return enqueue_layer(ctx, layer->dev, h, norm, m, resid, out, ids, w, status);
+}
+
+// Scratch of every kernel a layer's format runs (outside any graph capture).
+int32_t ensure_layer_scratch(tqf_hip_ctx *ctx, const LayerDev &L, int32_t format) {
+    if (int32_t rc = ensure_moe_scratch(ctx, L.hidden, L.width, L.n_experts)) return rc;
+    if (format == TQF_HIP_FORMAT_Q4_K) return ensure_q4k_layer_scratch(ctx, L.hidden, L.width);
+    return TQF_HIP_OK;
+}
+
 int32_t enqueue_stack(tqf_hip_ctx *ctx, const tqf_hip_stack *st, const float *d_h_in, float *d_h,
                       uint32_t m, uint16_t *d_ids, float *d_w, int32_t *d_status) {
     for (size_t l = 0; l < st->layers.size(); ++l) {
-        const LayerDev &L = st->layers[l]->dev;
         uint16_t *ids = d_ids ? d_ids + l * (size_t)m * kTopK : nullptr;
         float *w = d_w ? d_w + l * (size_t)m * kTopK : nullptr;
         const float *in = (l == 0 && d_h_in) ? d_h_in : d_h;
-        int32_t rc = enqueue_layer(ctx, L, in, st->norms[l], m, in, d_h, ids, w, d_status);
+        int32_t rc = enqueue_moe(ctx, st->layers[l], in, st->norms[l], m, in, d_h, ids, w, d_status);
         if (rc) return rc;
     }
     return TQF_HIP_OK;
@@ -337,6 +434,7 @@ int32_t enqueue_stack(tqf_hip_ctx *ctx, const tqf_hip_stack *st, const float *d_
 bool stack_persistent_ok(tqf_hip_ctx *ctx, const tqf_hip_stack *st, uint32_t m) {
     if (std::getenv("TQF_HIP_PERSISTENT") && std::string(std::getenv("TQF_HIP_PERSISTENT")) == "0")
         return false;
+    if (st->format != TQF_HIP_FORMAT_Q4_0) return false;  // the persistent kernel reads Q4_0
     if (!st->d_layers || m > (uint32_t)kStackMT || st->hidden != (uint32_t)kStackHidden ||
         st->experts == 0 || st->experts > 256 || st->width % 256 || st->width > 2048)
         return false;
@@ -1360,8 +1458,14 @@ extern "C" int32_t tqf_hip_moe_layer_prepare(tqf_hip_ctx *ctx, const tqf_hip_moe
         return fail(ctx, TQF_HIP_ERR_INVALID, "shared_input_gate must be f32 [hidden]");
     if (!mw->routed_gate || !mw->routed_up || !mw->routed_down)
         return fail(ctx, TQF_HIP_ERR_INVALID, "null routed expert table");
-    auto ok_gu = [&](const tqf_hip_weights *w) { return valid_weights(w) && w->dims.rows == F && w->dims.cols == H; };
-    auto ok_d = [&](const tqf_hip_weights *w) { return valid_weights(w) && w->dims.rows == H && w->dims.cols == F; };
+    // Every expert matrix of a layer has one format: Q4_0 (the configs'
+    // group-32 format) or Q4_K (the canonical checkpoint's experts).
+    const int32_t format = mw->shared_gate && mw->shared_gate->tiles ? mw->shared_gate->format : -1;
+    if (format != TQF_HIP_FORMAT_Q4_0 && format != TQF_HIP_FORMAT_Q4_K)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "expert matrices must be Q4_0 or Q4_K weights");
+    auto ok_fmt = [&](const tqf_hip_weights *w) { return w && w->tiles && w->format == format; };
+    auto ok_gu = [&](const tqf_hip_weights *w) { return ok_fmt(w) && w->dims.rows == F && w->dims.cols == H; };
+    auto ok_d = [&](const tqf_hip_weights *w) { return ok_fmt(w) && w->dims.rows == H && w->dims.cols == F; };
     std::vector<const uint8_t *> mats((size_t)(E + 1) * 3);
     for (uint32_t e = 0; e <= E; ++e) {
         const tqf_hip_weights *g = e < E ? mw->routed_gate[e] : mw->shared_gate;
@@ -1369,12 +1473,15 @@ extern "C" int32_t tqf_hip_moe_layer_prepare(tqf_hip_ctx *ctx, const tqf_hip_moe
         const tqf_hip_weights *d = e < E ? mw->routed_down[e] : mw->shared_down;
         if (!ok_gu(g) || !ok_gu(u) || !ok_d(d))
             return fail(ctx, TQF_HIP_ERR_INVALID,
-                        "expert " + std::to_string(e) + ": gate/up must be [width x hidden] and down [hidden x width]");
+                        "expert " + std::to_string(e) +
+                            ": gate/up must be [width x hidden] and down [hidden x width], all of one format");
         mats[(size_t)e * 3 + 0] = g->tiles;
         mats[(size_t)e * 3 + 1] = u->tiles;
         mats[(size_t)e * 3 + 2] = d->tiles;
     }
     if (int32_t rc = ensure_moe_scratch(ctx, H, F, E)) return rc;
+    if (format == TQF_HIP_FORMAT_Q4_K)
+        if (int32_t rc = ensure_q4k_layer_scratch(ctx, H, F)) return rc;
     void *dm = nullptr;
     if (arena_alloc(ctx, mats.size() * sizeof(void *), &dm) != hipSuccess)
         return fail(ctx, TQF_HIP_ERR_NOMEM, "layer table allocation failed");
@@ -1386,6 +1493,7 @@ extern "C" int32_t tqf_hip_moe_layer_prepare(tqf_hip_ctx *ctx, const tqf_hip_moe
     tqf_hip_layer *layer = new tqf_hip_layer();
     layer->d_mats = static_cast<const uint8_t **>(dm);
     layer->dev = LayerDev{mw->router->data, mw->shared_input_gate->data, layer->d_mats, E, H, F};
+    layer->format = format;
     *out = layer;
     return TQF_HIP_OK;
 }
@@ -1407,9 +1515,8 @@ extern "C" int32_t tqf_hip_moe_layer_device(tqf_hip_ctx *ctx, const tqf_hip_laye
     if (!layer || !d_x || !d_y) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
     if (m == 0 || m > kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "m must be in 1..8");
     if (d_x == d_y) return fail(ctx, TQF_HIP_ERR_INVALID, "x and y must not alias");
-    const LayerDev &L = layer->dev;
-    if (int32_t rc = ensure_moe_scratch(ctx, L.hidden, L.width, L.n_experts)) return rc;
-    return enqueue_layer(ctx, L, d_x, nullptr, m, nullptr, d_y, d_ids, d_w, d_status);
+    if (int32_t rc = ensure_layer_scratch(ctx, layer->dev, layer->format)) return rc;
+    return enqueue_moe(ctx, layer, d_x, nullptr, m, nullptr, d_y, d_ids, d_w, d_status);
 }
 
 extern "C" int32_t tqf_hip_moe_layer(tqf_hip_ctx *ctx, const tqf_hip_layer *layer, const float *x,
@@ -1418,7 +1525,7 @@ extern "C" int32_t tqf_hip_moe_layer(tqf_hip_ctx *ctx, const tqf_hip_layer *laye
     if (!layer || !x || !y) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
     if (m == 0 || m > kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "m must be in 1..8");
     const LayerDev &L = layer->dev;
-    if (int32_t rc = ensure_moe_scratch(ctx, L.hidden, L.width, L.n_experts)) return rc;
+    if (int32_t rc = ensure_layer_scratch(ctx, L, layer->format)) return rc;
     const size_t xb = align_up((size_t)m * L.hidden * 4, kAlign);
     const size_t ib = align_up((size_t)m * kTopK * 2, kAlign), wb = align_up((size_t)m * kTopK * 4, kAlign);
     if (int32_t rc = ensure_stage(ctx, 2 * xb + ib + wb + kAlign)) return rc;
@@ -1431,7 +1538,7 @@ extern "C" int32_t tqf_hip_moe_layer(tqf_hip_ctx *ctx, const tqf_hip_layer *laye
     const int32_t zero = 0;
     TQF_HIP(ctx, hipMemcpyAsync(dstatus, &zero, 4, hipMemcpyHostToDevice, ctx->stream));
     TQF_HIP(ctx, hipMemcpyAsync(dx, x, (size_t)m * L.hidden * 4, hipMemcpyHostToDevice, ctx->stream));
-    if (int32_t rc = enqueue_layer(ctx, L, dx, nullptr, m, nullptr, dy, dids, dw, dstatus)) return rc;
+    if (int32_t rc = enqueue_moe(ctx, layer, dx, nullptr, m, nullptr, dy, dids, dw, dstatus)) return rc;
     int32_t status = 0;
     TQF_HIP(ctx, hipMemcpyAsync(&status, dstatus, 4, hipMemcpyDeviceToHost, ctx->stream));
     TQF_HIP(ctx, hipMemcpyAsync(y, dy, (size_t)m * L.hidden * 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -1472,14 +1579,17 @@ extern "C" int32_t tqf_hip_stack_prepare(tqf_hip_ctx *ctx, const tqf_hip_layer *
     st->hidden = layers[0] ? layers[0]->dev.hidden : 0;
     st->width = layers[0] ? layers[0]->dev.width : 0;
     st->experts = layers[0] ? layers[0]->dev.n_experts : 0;
+    st->format = layers[0] ? layers[0]->format : TQF_HIP_FORMAT_Q4_0;
     for (uint32_t l = 0; l < n_layers; ++l) {
         const tqf_hip_layer *L = layers[l];
         const tqf_hip_tensor *nw = ffn_norms[l];
         if (!L || !nw || L->dev.hidden != st->hidden || L->dev.width != st->width ||
-            L->dev.n_experts != st->experts || nw->count != st->hidden) {
+            L->dev.n_experts != st->experts || nw->count != st->hidden ||
+            L->format != layers[0]->format) {
             delete st;
             return fail(ctx, TQF_HIP_ERR_INVALID,
-                        "layer " + std::to_string(l) + ": layers must share one geometry and norms be f32 [hidden]");
+                        "layer " + std::to_string(l) +
+                            ": layers must share one geometry and expert format, and norms be f32 [hidden]");
         }
         st->layers.push_back(L);
         st->norms.push_back(nw->data);
@@ -1518,7 +1628,7 @@ extern "C" int32_t tqf_hip_stack_forward_device(tqf_hip_ctx *ctx, const tqf_hip_
     if (m == 0 || m > kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "m must be in 1..8");
     if (stack_persistent_ok(ctx, stack, m))
         return enqueue_stack_persistent(ctx, stack, d_h_in, d_h, m, d_ids, d_w, d_status);
-    if (int32_t rc = ensure_moe_scratch(ctx, stack->hidden, stack->width, stack->experts)) return rc;
+    if (int32_t rc = ensure_layer_scratch(ctx, stack->layers[0]->dev, stack->format)) return rc;
     std::vector<uint64_t> key = {1, k64(stack), k64(d_h_in), k64(d_h), m, k64(d_ids), k64(d_w),
                                  k64(d_status)};
     return run_graphed(ctx, key, [&]() {
@@ -1644,6 +1754,8 @@ int32_t check_grouped(tqf_hip_ctx *ctx, const tqf_hip_layer *layer, uint32_t t) 
     if (t == 0 || t > TQF_HIP_GROUPED_MAX_TOKENS)
         return fail(ctx, TQF_HIP_ERR_INVALID, "t must be in 1..TQF_HIP_GROUPED_MAX_TOKENS");
     const LayerDev &L = layer->dev;
+    if (layer->format != TQF_HIP_FORMAT_Q4_0)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "the grouped GEMM reads Q4_0 expert matrices");
     if (L.hidden % 256 || L.width % 256 || L.n_experts == 0 || L.n_experts > 256)
         return fail(ctx, TQF_HIP_ERR_INVALID, "layer geometry unsupported by the grouped GEMM");
     return TQF_HIP_OK;
@@ -1756,7 +1868,7 @@ extern "C" int32_t tqf_hip_verify_step_device(tqf_hip_ctx *ctx, const tqf_hip_st
         return enqueue_accept(ctx, d_target, d_draft, d_dtok, k, vocab, temperature, greedy, d_u,
                               d_ures, d_accepted, d_tokens);
     }
-    if (int32_t rc = ensure_moe_scratch(ctx, stack->hidden, stack->width, stack->experts)) return rc;
+    if (int32_t rc = ensure_layer_scratch(ctx, stack->layers[0]->dev, stack->format)) return rc;
     uint32_t tbits;
     std::memcpy(&tbits, &temperature, 4);
     std::vector<uint64_t> key = {2,          k64(stack), k64(d_h_in), k64(d_h), m, k64(d_target),

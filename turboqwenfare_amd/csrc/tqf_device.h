@@ -453,4 +453,22 @@ __device__ __forceinline__ void xor_stage1(int *v) {
     for (int p = 0; p < K / 2; ++p) v[p] += dpp_i<CTRL>(v[p ^ MASK]);
 }
 
+// ---------------------------------------------------------------------------
+// Block-wide reduction of N floats per thread (256 threads); result valid in
+// every thread.
+// ---------------------------------------------------------------------------
+template <int N>
+__device__ __forceinline__ void block_sum_256(float (&v)[N], float (*lds)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = group_reduce<64>(v[i], AddOp());
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    __syncthreads();
+    if (lane == 0)
+#pragma unroll
+        for (int i = 0; i < N; ++i) lds[wave][i] = v[i];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = (lds[0][i] + lds[1][i]) + (lds[2][i] + lds[3][i]);
+}
+
 }  // namespace tqf

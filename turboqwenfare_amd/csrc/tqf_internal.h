@@ -206,6 +206,7 @@ struct Plan {
     float weights[kMaxTokens][kTopK];
     float gate_logit[kMaxTokens];
     int32_t union_ids[kMaxTokens * kTopK];
+    int32_t pair_slot[kMaxTokens * kTopK];  // slot of route (t, k) at index t * kTopK + k
 };
 
 // Device-side description of one MoE layer (passed by value to kernels).
@@ -262,6 +263,7 @@ struct tqf_hip_tensor {
 struct tqf_hip_layer {
     tqf::LayerDev dev;
     const uint8_t **d_mats;  // device array owned by the layer
+    int32_t format;          // TQF_HIP_FORMAT_Q4_0 or _Q4_K (every expert of the layer)
 };
 
 namespace tqf {
@@ -327,6 +329,7 @@ struct tqf_hip_stack {
     std::vector<const tqf_hip_layer *> layers;
     std::vector<const float *> norms;
     uint32_t hidden, width, experts;
+    int32_t format;                       // the layers' expert format
     tqf::StackLayer *d_layers = nullptr;  // device copy for the persistent kernel
 };
 
@@ -434,6 +437,19 @@ hipError_t launch_q8k_quantize(hipStream_t s, const float *x, uint32_t m, uint32
 hipError_t launch_q4k_q8k_gemv(hipStream_t s, const uint8_t *const *tables, uint32_t count,
                                const MatrixDims &d, const uint32_t *q8, uint32_t m, float *y);
 hipError_t launch_q4k_silu_mul(hipStream_t s, const float *gu, uint32_t m, uint32_t F, float *h);
+// The Q4_K MoE layer over a route plan (n_slots = 9 M slots of launch_route):
+// gate and up of every slot (y [2 x n_slots x rows]: gate rows, then up rows;
+// the records of the slot's token, q8 [M x 12 Bp]), or down of every slot
+// (records of the slot's own h, q8 [n_slots x 12 Bp]; y [n_slots x rows]).
+hipError_t launch_q4k_q8k_slots(hipStream_t s, const Plan *plan, uint32_t n_slots, bool down,
+                                const MatrixDims &d, const uint32_t *q8, float *y);
+// y[t] = resid[t] (if given) + (shared slot t's down x its coefficient, then
+// + route (t, k) down x weight for k = 0..7); nothing when routing failed.
+hipError_t launch_q4k_moe_combine(hipStream_t s, const Plan *plan, const float *dn, uint32_t m,
+                                  uint32_t hidden, const float *resid, float *y);
+// out[t] = qwen_rmsnorm(x[t], w) as f32 rows (hidden a multiple of 256, <= 2048).
+hipError_t launch_q4k_rmsnorm(hipStream_t s, const float *x, const float *w, uint32_t m,
+                              uint32_t hidden, float *out);
 
 // ---- Q6_K (tqf_q6k.hip) ----------------------------------------------------
 hipError_t launch_q6k_repack(hipStream_t s, const uint8_t *d_aos, const MatrixDims &d,

@@ -163,24 +163,6 @@ hipError_t launch_gemv(hipStream_t s, const uint8_t *const *d_tables, uint32_t c
 // ---------------------------------------------------------------------------
 
 // ---------------------------------------------------------------------------
-// Block-wide reduction of N floats per thread (256 threads); result valid in
-// every thread.
-// ---------------------------------------------------------------------------
-template <int N>
-__device__ __forceinline__ void block_sum_256(float (&v)[N], float (*lds)[N]) {
-#pragma unroll
-    for (int i = 0; i < N; ++i) v[i] = group_reduce<64>(v[i], AddOp());
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    __syncthreads();
-    if (lane == 0)
-#pragma unroll
-        for (int i = 0; i < N; ++i) lds[wave][i] = v[i];
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < N; ++i) v[i] = (lds[0][i] + lds[1][i]) + (lds[2][i] + lds[3][i]);
-}
-
-// ---------------------------------------------------------------------------
 // Route kernel.  One workgroup per two router rows (row n_experts is the
 // shared-expert input gate, experts/mod.rs:1614).  Each workgroup
 //   1. loads h [m x hidden], applies RMSNorm when `norm` is given
@@ -414,6 +396,7 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
             rec.coef = wv;
             plan->slots[slot] = rec;
             plan->slot_expert[slot] = e_i;
+            plan->pair_slot[lane] = slot;
             plan->ids[t][k] = (uint16_t)e_i;
             plan->weights[t][k] = wv;
             if (flag) plan->union_ids[upos] = e_i;

@@ -381,11 +381,20 @@ hipError_t launch_q8k_quantize(hipStream_t s, const float *x, uint32_t m, uint32
 // LPR/8) and advanced super-block after super-block through LDS.  The last
 // step, minimum_sum + (-0.0 + lane_acc[0] + ... + lane_acc[7]), is taken by
 // the row's first lane.  Super-blocks past cols (padding) do not enter.
+//
+// SRC says where workgroup row blockIdx.y takes its matrix and records:
+// kSrcTables -- tables[blockIdx.y], the m rows of q8; kSrcSlotGateUp --
+// matrix blockIdx.y / S (0 gate, 1 up) of plan slot blockIdx.y % S (S =
+// gridDim.y / 2), the records of the slot's token; kSrcSlotDown -- the down
+// matrix of slot blockIdx.y, the slot's own records.  The slot forms run one
+// row of records (m = 1) and skip slots without work (routing failed).
 // ---------------------------------------------------------------------------
-template <int LPR, int TG>
+constexpr int kSrcTables = 0, kSrcSlotGateUp = 1, kSrcSlotDown = 2;
+
+template <int LPR, int TG, int SRC>
 __global__ __launch_bounds__(kQ4KWaves * kWave) void q4k_q8k_gemv_kernel(
-    const uint8_t *const *__restrict__ tables, MatrixDims d, const uint32_t *__restrict__ q8,
-    uint32_t m, float *__restrict__ y) {
+    const uint8_t *const *__restrict__ tables, const Plan *__restrict__ plan, MatrixDims d,
+    const uint32_t *__restrict__ q8, uint32_t m, float *__restrict__ y) {
     constexpr int G = kWave / LPR;         // row octets per wavefront
     constexpr int SB = LPR / 8;            // super-blocks per lane group and chunk
     constexpr int NCH = (9 + SB - 1) / SB; // running sums per lane
@@ -396,7 +405,18 @@ __global__ __launch_bounds__(kQ4KWaves * kWave) void q4k_q8k_gemv_kernel(
     const uint32_t mat = blockIdx.y;
     const uint32_t r0 = (blockIdx.x * kQ4KWaves + wave) * 8 * G;
     if (r0 >= d.rows_padded) return;  // no workgroup barrier below
-    const uint8_t *base = tables[mat];
+    const uint8_t *base;
+    if constexpr (SRC == kSrcTables) {
+        base = tables[mat];
+    } else {
+        const uint32_t S = SRC == kSrcSlotGateUp ? gridDim.y / 2 : gridDim.y;
+        const uint32_t slot = mat % S;
+        const SlotRec rec = load_slot(&plan->slots[slot]);
+        if (rec.token < 0) return;  // routing failed: no work
+        base = rec.mat[SRC == kSrcSlotGateUp ? mat / S : 2];
+        q8 += (size_t)(SRC == kSrcSlotGateUp ? (uint32_t)rec.token : slot) * d.blocks_padded *
+              kQ8KRecDwords;
+    }
     const RowLane W = row_lane(base, d.blocks_padded);
     const uint32_t rl = r0 + jg * 8;
     const uint32_t nb = d.blocks >> 3;
@@ -511,9 +531,27 @@ hipError_t launch_q4k_q8k_lpr(hipStream_t s, const uint8_t *const *tables, uint3
     constexpr uint32_t rows_per_group = kQ4KWaves * 8 * (kWave / LPR);
     const dim3 grid((d.rows_padded + rows_per_group - 1) / rows_per_group, count);
     const dim3 block(kQ4KWaves * kWave);
-    if (m <= 1) hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 1>), grid, block, 0, s, tables, d, q8, m, y);
-    else if (m <= 2) hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 2>), grid, block, 0, s, tables, d, q8, m, y);
-    else hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 4>), grid, block, 0, s, tables, d, q8, m, y);
+    const Plan *none = nullptr;
+    if (m <= 1)
+        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 1, kSrcTables>), grid, block, 0, s, tables, none, d, q8, m, y);
+    else if (m <= 2)
+        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 2, kSrcTables>), grid, block, 0, s, tables, none, d, q8, m, y);
+    else
+        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 4, kSrcTables>), grid, block, 0, s, tables, none, d, q8, m, y);
+    return hipGetLastError();
+}
+
+template <int LPR>
+hipError_t launch_q4k_q8k_slots_lpr(hipStream_t s, const Plan *plan, uint32_t n_slots, bool down,
+                                    const MatrixDims &d, const uint32_t *q8, float *y) {
+    constexpr uint32_t rows_per_group = kQ4KWaves * 8 * (kWave / LPR);
+    const dim3 grid((d.rows_padded + rows_per_group - 1) / rows_per_group, down ? n_slots : 2 * n_slots);
+    const dim3 block(kQ4KWaves * kWave);
+    const uint8_t *const *none = nullptr;
+    if (down)
+        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 1, kSrcSlotDown>), grid, block, 0, s, none, plan, d, q8, 1u, y);
+    else
+        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 1, kSrcSlotGateUp>), grid, block, 0, s, none, plan, d, q8, 1u, y);
     return hipGetLastError();
 }
 
@@ -522,6 +560,14 @@ hipError_t launch_q4k_q8k_gemv(hipStream_t s, const uint8_t *const *tables, uint
     if (d.lpr == 16) return launch_q4k_q8k_lpr<16>(s, tables, count, d, q8, m, y);
     if (d.lpr == 32) return launch_q4k_q8k_lpr<32>(s, tables, count, d, q8, m, y);
     return launch_q4k_q8k_lpr<64>(s, tables, count, d, q8, m, y);
+}
+
+hipError_t launch_q4k_q8k_slots(hipStream_t s, const Plan *plan, uint32_t n_slots, bool down,
+                                const MatrixDims &d, const uint32_t *q8, float *y) {
+    if (n_slots == 0 || n_slots > (uint32_t)kMaxSlots) return hipErrorInvalidValue;
+    if (d.lpr == 16) return launch_q4k_q8k_slots_lpr<16>(s, plan, n_slots, down, d, q8, y);
+    if (d.lpr == 32) return launch_q4k_q8k_slots_lpr<32>(s, plan, n_slots, down, d, q8, y);
+    return launch_q4k_q8k_slots_lpr<64>(s, plan, n_slots, down, d, q8, y);
 }
 
 // ---------------------------------------------------------------------------
@@ -541,6 +587,71 @@ __global__ __launch_bounds__(256) void q4k_silu_mul_kernel(const float *__restri
 hipError_t launch_q4k_silu_mul(hipStream_t s, const float *gu, uint32_t m, uint32_t F, float *h) {
     const uint32_t n = m * F;
     hipLaunchKernelGGL(q4k_silu_mul_kernel, dim3((n + 255) / 256), dim3(256), 0, s, gu, m, F, h);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// The MoE layer's combine (experts/mod.rs:1556-1568 per row, the arithmetic
+// of :1610-1632): output = shared down x sigmoid(shared gate logit)
+// (scale_in_place), then output += routed down x weight for each route in
+// route order (add_scaled_in_place, weights.rs:267-281), each step one f32
+// multiply and one f32 add; the stack's residual is added last
+// (runtime.rs:777-802: h + moe(norm(h))).  One thread per (token, column).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void q4k_moe_combine_kernel(const Plan *__restrict__ plan,
+                                                              const float *__restrict__ dn,
+                                                              uint32_t m, uint32_t H,
+                                                              const float *resid, float *y) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= m * H || plan->status != 0) return;
+    const uint32_t t = i / H, c = i % H;
+    float o = __fmul_rn(dn[(size_t)t * H + c], plan->slots[t].coef);
+#pragma unroll
+    for (int k = 0; k < kTopK; ++k) {
+        const int slot = plan->pair_slot[t * kTopK + k];
+        o = __fadd_rn(o, __fmul_rn(dn[(size_t)slot * H + c], plan->weights[t][k]));
+    }
+    if (resid) o = __fadd_rn(resid[i], o);
+    y[i] = o;
+}
+
+hipError_t launch_q4k_moe_combine(hipStream_t s, const Plan *plan, const float *dn, uint32_t m,
+                                  uint32_t hidden, const float *resid, float *y) {
+    const uint32_t n = m * hidden;
+    hipLaunchKernelGGL(q4k_moe_combine_kernel, dim3((n + 255) / 256), dim3(256), 0, s, plan, dn, m,
+                       hidden, resid, y);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Qwen RMSNorm to f32 rows (Qwen36Activation::rmsnorm, weights.rs:203-239):
+// x * (1 / sqrt(mean(x^2) + 1e-6)) * w, one workgroup per row, the sum of
+// squares as a tree over the row (the route kernel's order).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void q4k_rmsnorm_kernel(const float *__restrict__ x,
+                                                          const float *__restrict__ w, uint32_t H,
+                                                          float *__restrict__ out) {
+    __shared__ float part[4][1];
+    const uint32_t t = blockIdx.x, tid = threadIdx.x;
+    const int vpt = (int)(H / 256);
+    const float *xr = x + (size_t)t * H + tid * vpt;
+    float v[8], ss[1] = {0.0f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        v[j] = j < vpt ? xr[j] : 0.0f;
+        ss[0] += v[j] * v[j];
+    }
+    block_sum_256<1>(ss, part);
+    const float inv = 1.0f / sqrtf(ss[0] / (float)H + 1e-6f);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        if (j < vpt) out[(size_t)t * H + tid * vpt + j] = v[j] * inv * w[tid * vpt + j];
+}
+
+hipError_t launch_q4k_rmsnorm(hipStream_t s, const float *x, const float *w, uint32_t m,
+                              uint32_t hidden, float *out) {
+    if (hidden == 0 || hidden % 256 || hidden > 2048) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(q4k_rmsnorm_kernel, dim3(m), dim3(256), 0, s, x, w, hidden, out);
     return hipGetLastError();
 }
 
