@@ -224,6 +224,82 @@ def q4k_pool_bench(be, pool_size: int, seed: int, iters: int = 10):
     return out
 
 
+def q4k_verify_bench(be, n_layers: int, seed: int, inputs, steps: int = 50, warmup: int = 5):
+    """Config 4 with the canonical checkpoint's expert format: the same
+    n_layers verify step (RMSNorm, route, experts, residual per layer, then
+    the acceptance) with Q4_K experts, every expert matvec on the Q8_K
+    integer path (bit-identical per matvec to q4_k_dot_pre).  The experts are
+    device repacks of 8 seeded centred GGML Q4_K matrices per shape, each at
+    its own HBM address."""
+    from turboqwenfare_amd import _lib, mtp, synth
+
+    target, draft, dtok, u, ur, h0 = inputs
+    shapes = ((F, H), (F, H), (H, F))
+    staging = [[be.to_device(synth.centered_q4_k(r, c, seed * 1000 + 10 * i + j)) for j in range(8)]
+               for i, (r, c) in enumerate(shapes)]
+    layers, norms, weights = [], [], []
+    for l in range(n_layers):
+        base = 3_000_000 * (l + 1)
+        mats = [tuple(be.upload_q4_k_device(staging[i][(l * 5 + e * 3 + i) % 8], r, c)
+                      for i, (r, c) in enumerate(shapes)) for e in range(E + 1)]
+        weights += [w for m in mats for w in m]
+        router = be.upload_f32(synth.normal((E, H), seed=base + 7, std=H ** -0.5))
+        gate = be.upload_f32(synth.normal((H,), seed=base + 8, std=H ** -0.5))
+        layers.append(be.prepare_moe_layer(router, gate, mats[E], [m[0] for m in mats[:E]],
+                                           [m[1] for m in mats[:E]], [m[2] for m in mats[:E]]))
+        norms.append(be.upload_f32((1.0 + 0.05 * synth.normal((H,), seed=base + 9)).astype(np.float32)))
+    for b in (b for row in staging for b in row):
+        be.free(b)
+    st = be.prepare_stack(layers, norms)
+    d = {k: be.to_device(v) for k, v in dict(t=target, d=draft, dt=dtok, u=u, ur=ur, h0=h0,
+                                              h=h0).items()}
+    d_acc, d_tok = be.alloc(4), be.alloc(4 * M)
+
+    def step():
+        be.verify_step_device(st, d["h0"], d["h"], M, d["t"], d["d"], d["dt"], V, TEMPERATURE,
+                              False, d["u"], d["ur"], d_acc, d_tok)
+
+    for _ in range(warmup):
+        step()
+    be.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    be.synchronize()
+    elapsed = (time.perf_counter() - t0) / steps
+    be.profile_enable(True)
+    for _ in range(5):
+        step()
+    be.synchronize()
+    prof = {}
+    for kind, nm in ((_lib.KERNEL_ROUTE, "route"), (_lib.KERNEL_Q4K_MATVEC, "q4k_matvec"),
+                     (_lib.KERNEL_ACCEPT, "accept")):
+        n, ms, by = be.profile_read(kind)
+        if n:
+            prof[nm] = dict(launches=n, avg_us=ms / n * 1e3)
+    be.profile_enable(False)
+    # algorithmic bytes of one stack pass: each layer's router, norm and the
+    # GGML bytes of its (union + shared) experts
+    d_ids = be.alloc(n_layers * M * 8 * 2)
+    d_tmp = be.alloc(M * H * 4)
+    be.stack_forward_device(st, d_tmp, M, d_ids, d_h_in=d["h0"])
+    ids = be.read(d_ids, np.uint16, (n_layers, M, 8))
+    unions = [len(mtp.routes_union(ids[l])) for l in range(n_layers)]
+    stack_bytes = sum((un + 1) * 3 * F * (H // 256) * 144 + (E + 1) * H * 4 + H * 4
+                      for un in unions) + 2 * M * H * 4
+    out = dict(layers=n_layers, m=M, format="q4_k", steps_per_s=1.0 / elapsed,
+               ms_per_step=elapsed * 1e3, expert_union_mean=float(np.mean(unions)),
+               stack_bytes_per_step=stack_bytes, kernels=prof)
+    for b in list(d.values()) + [d_acc, d_tok, d_ids, d_tmp]:
+        be.free(b)
+    be.free_stack(st)
+    for L in layers:
+        be.free_moe_layer(L)
+    for w in weights:
+        be.free_weights(w)
+    return out
+
+
 def lm_head_bench(be, seed: int, iters: int = 20):
     """The LM head at the configs' vocabulary: Q6_K [151,936 x 2048] (255 MB,
     the canonical checkpoint's lm_head format) against the M = 4 verify rows,
@@ -282,10 +358,21 @@ def main():
     ap.add_argument("--lm-head-only", action="store_true",
                     help="only run the Q6_K LM head (the command its rocprofv3 profiles are "
                          "taken with) and exit")
+    ap.add_argument("--q4k-verify-only", action="store_true",
+                    help="only the verify step with Q4_K expert layers")
     ap.add_argument("--q4k-only", action="store_true",
                     help="only run the Q4_K config-1 GEMV pools (the command their rocprofv3 "
                          "profiles are taken with) and exit")
     args = ap.parse_args()
+    if args.q4k_verify_only:
+        from turboqwenfare_amd.backend import HipBackend
+
+        be = HipBackend(0)
+        r = q4k_verify_bench(be, args.layers, args.seed, verify_inputs(args.seed),
+                             steps=min(args.steps, 100))
+        log("bench: Q4_K verify step " + json.dumps(r))
+        be.close()
+        return
     if args.lm_head_only:
         from turboqwenfare_amd.backend import HipBackend
 
@@ -434,6 +521,8 @@ def main():
     log("bench: LM head " + json.dumps(lm))
     grouped = grouped_gemm_bench(be, layers[0], args.seed)
     log("bench: config-5 grouped GEMM " + json.dumps(grouped))
+    q4k_verify = q4k_verify_bench(be, args.layers, args.seed, inputs, steps=min(args.steps, 100))
+    log("bench: Q4_K verify step " + json.dumps(q4k_verify))
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -485,6 +574,7 @@ def main():
         "q4k_config1": q4k,
         "lm_head_q6k": lm,
         "grouped_gemm_config5": grouped,
+        "q4k_verify": q4k_verify,
         "eager_profiled_ms_per_step": eager_ms,
         "synchronised_step_ms": {"p10": q10, "median": q50, "p90": q90},
         "cpu_baseline": cpu,

@@ -16,8 +16,8 @@ import pytest
 
 import cpu_oracle as orc
 from conftest import rel_err
-from test_oracle import centered_q4_k
 from turboqwenfare_amd import synth
+from turboqwenfare_amd.synth import centered_q4_k
 from turboqwenfare_amd._lib import ERR_INVALID, ERR_ROUTER, HipError
 
 pytestmark = pytest.mark.gpu

@@ -321,7 +321,7 @@ int32_t enqueue_layer(tqf_hip_ctx *ctx, const LayerDev &L, const float *h, const
 
 // Device views of the Q4_K layer's buffers in ctx->d_q4k, sized for m rows.
 struct Q4KLayerBufs {
-    float *xnorm, *gu, *h, *dn;
+    float *xnorm, *gu, *dn;
     uint32_t *q8x, *q8h;
     size_t bytes;
 };
@@ -330,17 +330,15 @@ Q4KLayerBufs q4k_layer_bufs(uint8_t *base, uint32_t H, uint32_t F, uint32_t m) {
     const size_t xn = align_up((size_t)m * H * 4, kAlign);
     const size_t qx = align_up((size_t)m * padded_blocks(H / 32) * kQ8KRecDwords * 4, kAlign);
     const size_t gu = align_up((size_t)2 * S * F * 4, kAlign);
-    const size_t hb = align_up((size_t)S * F * 4, kAlign);
     const size_t qh = align_up((size_t)S * padded_blocks(F / 32) * kQ8KRecDwords * 4, kAlign);
     const size_t dn = align_up((size_t)S * H * 4, kAlign);
     Q4KLayerBufs b;
     b.xnorm = reinterpret_cast<float *>(base);
     b.q8x = reinterpret_cast<uint32_t *>(base + xn);
     b.gu = reinterpret_cast<float *>(base + xn + qx);
-    b.h = reinterpret_cast<float *>(base + xn + qx + gu);
-    b.q8h = reinterpret_cast<uint32_t *>(base + xn + qx + gu + hb);
-    b.dn = reinterpret_cast<float *>(base + xn + qx + gu + hb + qh);
-    b.bytes = xn + qx + gu + hb + qh + dn;
+    b.q8h = reinterpret_cast<uint32_t *>(base + xn + qx + gu);
+    b.dn = reinterpret_cast<float *>(base + xn + qx + gu + qh);
+    b.bytes = xn + qx + gu + qh + dn;
     return b;
 }
 
@@ -355,9 +353,9 @@ int32_t ensure_q4k_layer_scratch(tqf_hip_ctx *ctx, uint32_t H, uint32_t F) {
 }
 
 // One MoE layer with Q4_K experts, every expert matvec on the Q8_K path of
-// matvec_payload (weights.rs:680-735): (RMSNorm) -> route -> Q8_K(x) ->
-// gate and up of all 9 M slots -> silu_mul -> Q8_K(h) -> down of all slots
-// -> combine in route order (+ residual).  The caller has run
+// matvec_payload (weights.rs:680-735): (RMSNorm +) Q8_K(x) -> route ->
+// gate and up of all 9 M slots -> Q8_K(silu_mul(gate, up)) -> down of all
+// slots -> combine in route order (+ residual).  The caller has run
 // ensure_moe_scratch and ensure_q4k_layer_scratch.
 int32_t enqueue_layer_q4k(tqf_hip_ctx *ctx, const LayerDev &L, const float *h, const float *norm,
                           uint32_t m, const float *resid, float *out, uint16_t *ids, float *w,
@@ -368,28 +366,24 @@ int32_t enqueue_layer_q4k(tqf_hip_ctx *ctx, const LayerDev &L, const float *h, c
     const Q4KLayerBufs b = q4k_layer_bufs(ctx->d_q4k, H, F, m);
     if (!ctx->d_q4k || ctx->q4k_bytes < b.bytes) return fail(ctx, TQF_HIP_ERR_INVALID, "Q4_K layer scratch missing");
     const float *x = h;
-    hipError_t e = hipSuccess;
-    if (norm) {
-        e = launch_q4k_rmsnorm(ctx->stream, h, norm, m, H, b.xnorm);
-        if (e != hipSuccess) return hip_fail(ctx, "RMSNorm kernel launch", e);
-        x = b.xnorm;
-    }
+    hipError_t e = norm ? launch_q8k_rmsnorm_quantize(ctx->stream, h, norm, m, H, dgu.blocks_padded,
+                                                      b.xnorm, b.q8x)
+                        : launch_q8k_quantize(ctx->stream, h, m, H, dgu.blocks_padded, b.q8x);
+    if (e != hipSuccess) return hip_fail(ctx, "RMSNorm / Q8_K quantize kernel launch", e);
+    if (norm) x = b.xnorm;
     {
         Prof p(ctx);
         e = launch_route(ctx->stream, L, x, nullptr, m, sc, ids, w, status);
         if (e != hipSuccess) return hip_fail(ctx, "route kernel launch", e);
         p.end(TQF_HIP_KERNEL_ROUTE, (L.n_experts + 1) * (double)H * 4 + m * (double)H * 4, 0, nullptr);
     }
-    e = launch_q8k_quantize(ctx->stream, x, m, H, dgu.blocks_padded, b.q8x);
-    if (e != hipSuccess) return hip_fail(ctx, "Q8_K quantize kernel launch", e);
     {
         Prof p(ctx);
         e = launch_q4k_q8k_slots(ctx->stream, sc.plan, S, false, dgu, b.q8x, b.gu);
         if (e != hipSuccess) return hip_fail(ctx, "Q4_K gate/up kernel launch", e);
         p.end(TQF_HIP_KERNEL_Q4K_MATVEC, 2.0 * S * ((double)F * H / 256 * kQ4KBlock + F * 4.0), 0, nullptr);
     }
-    e = launch_q4k_silu_mul(ctx->stream, b.gu, S, F, b.h);
-    if (e == hipSuccess) e = launch_q8k_quantize(ctx->stream, b.h, S, F, dd.blocks_padded, b.q8h);
+    e = launch_q8k_swiglu_quantize(ctx->stream, b.gu, S, F, dd.blocks_padded, b.q8h);
     if (e != hipSuccess) return hip_fail(ctx, "SwiGLU / Q8_K kernel launch", e);
     {
         Prof p(ctx);
@@ -1147,8 +1141,7 @@ int32_t q4k_expert_enqueue(tqf_hip_ctx *ctx, const tqf_hip_weights *gate,
     const size_t qx = align_up((size_t)m * dg.blocks_padded * kQ8KRecDwords * 4, kAlign);
     const size_t qh = align_up((size_t)m * dd.blocks_padded * kQ8KRecDwords * 4, kAlign);
     const size_t gu = align_up((size_t)2 * m * F * 4, kAlign);
-    const size_t hb = align_up((size_t)m * F * 4, kAlign);
-    const size_t need = qx + qh + gu + hb;
+    const size_t need = qx + qh + gu;
     if (!ctx->d_q4k || ctx->q4k_bytes < need) {
         TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
         drop_graphs(ctx);
@@ -1157,13 +1150,11 @@ int32_t q4k_expert_enqueue(tqf_hip_ctx *ctx, const tqf_hip_weights *gate,
     uint32_t *q8x = reinterpret_cast<uint32_t *>(ctx->d_q4k);
     uint32_t *q8h = reinterpret_cast<uint32_t *>(ctx->d_q4k + qx);
     float *dgu = reinterpret_cast<float *>(ctx->d_q4k + qx + qh);
-    float *dh = reinterpret_cast<float *>(ctx->d_q4k + qx + qh + gu);
     hipError_t e = launch_q8k_quantize(ctx->stream, d_x, m, H, dg.blocks_padded, q8x);
     if (e == hipSuccess) e = launch_q4k_q8k_gemv(ctx->stream, gate->d_self, 1, dg, q8x, m, dgu);
     if (e == hipSuccess)
         e = launch_q4k_q8k_gemv(ctx->stream, up->d_self, 1, up->dims, q8x, m, dgu + (size_t)m * F);
-    if (e == hipSuccess) e = launch_q4k_silu_mul(ctx->stream, dgu, m, F, dh);
-    if (e == hipSuccess) e = launch_q8k_quantize(ctx->stream, dh, m, F, dd.blocks_padded, q8h);
+    if (e == hipSuccess) e = launch_q8k_swiglu_quantize(ctx->stream, dgu, m, F, dd.blocks_padded, q8h);
     if (e == hipSuccess) e = launch_q4k_q8k_gemv(ctx->stream, down->d_self, 1, dd, q8h, m, d_y);
     if (e != hipSuccess) return hip_fail(ctx, "Q4_K expert kernels", e);
     (void)H;

@@ -436,7 +436,14 @@ hipError_t launch_q8k_quantize(hipStream_t s, const float *x, uint32_t m, uint32
                                uint32_t bp, uint32_t *q8);
 hipError_t launch_q4k_q8k_gemv(hipStream_t s, const uint8_t *const *tables, uint32_t count,
                                const MatrixDims &d, const uint32_t *q8, uint32_t m, float *y);
-hipError_t launch_q4k_silu_mul(hipStream_t s, const float *gu, uint32_t m, uint32_t F, float *h);
+// quantize_q8_k of h = silu_mul(gate, up) for m rows, gu = [gate rows | up
+// rows] ([2 x m x cols]).
+hipError_t launch_q8k_swiglu_quantize(hipStream_t s, const float *gu, uint32_t m, uint32_t cols,
+                                      uint32_t bp, uint32_t *q8);
+// xnorm[t] = qwen_rmsnorm(x[t], w) (f32 rows) and its Q8_K records (hidden a
+// multiple of 256, at most 2048).
+hipError_t launch_q8k_rmsnorm_quantize(hipStream_t s, const float *x, const float *w, uint32_t m,
+                                       uint32_t hidden, uint32_t bp, float *xnorm, uint32_t *q8);
 // The Q4_K MoE layer over a route plan (n_slots = 9 M slots of launch_route):
 // gate and up of every slot (y [2 x n_slots x rows]: gate rows, then up rows;
 // the records of the slot's token, q8 [M x 12 Bp]), or down of every slot
@@ -447,9 +454,6 @@ hipError_t launch_q4k_q8k_slots(hipStream_t s, const Plan *plan, uint32_t n_slot
 // + route (t, k) down x weight for k = 0..7); nothing when routing failed.
 hipError_t launch_q4k_moe_combine(hipStream_t s, const Plan *plan, const float *dn, uint32_t m,
                                   uint32_t hidden, const float *resid, float *y);
-// out[t] = qwen_rmsnorm(x[t], w) as f32 rows (hidden a multiple of 256, <= 2048).
-hipError_t launch_q4k_rmsnorm(hipStream_t s, const float *x, const float *w, uint32_t m,
-                              uint32_t hidden, float *out);
 
 // ---- Q6_K (tqf_q6k.hip) ----------------------------------------------------
 hipError_t launch_q6k_repack(hipStream_t s, const uint8_t *d_aos, const MatrixDims &d,

@@ -197,6 +197,17 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
     const int vpt = (int)(H / 256);  // 1..8 elements per thread
     const uint32_t col0 = (uint32_t)tid * vpt;
 
+    // this workgroup's router rows, loaded first so that their latency
+    // overlaps the activation loads and the records below
+    float wv[kRouteRows][8];
+#pragma unroll
+    for (int rr = 0; rr < kRouteRows; ++rr) {
+        const uint32_t r = blockIdx.x * kRouteRows + rr;
+        const float *wrow = (r < E) ? L.router + (size_t)r * H : L.shared_input_gate;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) wv[rr][v] = (r <= E && v < vpt) ? wrow[col0 + v] : 0.0f;
+    }
+
     float x[MT][8];
 #pragma unroll
     for (int t = 0; t < MT; ++t)
@@ -258,16 +269,11 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
     float dots[MT * kRouteRows];
 #pragma unroll
     for (int rr = 0; rr < kRouteRows; ++rr) {
-        const uint32_t r = blockIdx.x * kRouteRows + rr;
-        float wv[8];
-        const float *wrow = (r < E) ? L.router + (size_t)r * H : L.shared_input_gate;
-#pragma unroll
-        for (int v = 0; v < 8; ++v) wv[v] = (r <= E && v < vpt) ? wrow[col0 + v] : 0.0f;
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
             float s = 0.0f;
 #pragma unroll
-            for (int v = 0; v < 8; ++v) s = fmaf(x[t][v], wv[v], s);
+            for (int v = 0; v < 8; ++v) s = fmaf(x[t][v], wv[rr][v], s);
             dots[rr * MT + t] = s;
         }
     }

@@ -299,17 +299,12 @@ hipError_t launch_q4k_gemv(hipStream_t s, const uint8_t *const *tables, uint32_t
 //   round_ties_even(v * inverse), then f32::min(127) (NaN -> 127) and the
 //   saturating cast to i8.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void q8k_quantize_kernel(const float *__restrict__ x,
-                                                           uint32_t cols, uint32_t bp,
-                                                           uint32_t *__restrict__ q8) {
-    const uint32_t t = blockIdx.y;
-    const uint32_t chunk = (blockIdx.x * blockDim.x + threadIdx.x) / kWave;
-    if (chunk >= cols / 256) return;  // whole wavefronts
+// The quantization of one chunk by one wavefront from the lane's four values
+// v[i] = element 32k + c + 8i of the chunk, into the record row `row` at
+// sub-blocks 8 chunk .. 8 chunk + 7.
+__device__ __forceinline__ void q8k_quantize_values(const float (&v)[4], uint32_t *row, uint32_t bp,
+                                                    uint32_t chunk) {
     const int lane = threadIdx.x & 63, k = lane >> 3, c = lane & 7;
-    const float *src = x + (size_t)t * cols + (size_t)chunk * 256 + 32 * k + c;
-    float v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = src[8 * i];
     float am = -1.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -317,7 +312,6 @@ __global__ __launch_bounds__(256) void q8k_quantize_kernel(const float *__restri
         am = (a == a && a > am) ? a : am;
     }
     const float amax = group_reduce<64>(am, MaxOp());
-    uint32_t *row = q8 + (size_t)t * bp * kQ8KRecDwords;
     const uint32_t blk = chunk * 8 + (uint32_t)k;
     uint32_t word = 0;
     int sum = 0;
@@ -352,10 +346,102 @@ __global__ __launch_bounds__(256) void q8k_quantize_kernel(const float *__restri
     }
 }
 
+__global__ __launch_bounds__(256) void q8k_quantize_kernel(const float *__restrict__ x,
+                                                           uint32_t cols, uint32_t bp,
+                                                           uint32_t *__restrict__ q8) {
+    const uint32_t t = blockIdx.y;
+    const uint32_t chunk = (blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+    if (chunk >= cols / 256) return;  // whole wavefronts
+    const int lane = threadIdx.x & 63, k = lane >> 3, c = lane & 7;
+    const float *src = x + (size_t)t * cols + (size_t)chunk * 256 + 32 * k + c;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = src[8 * i];
+    q8k_quantize_values(v, q8 + (size_t)t * bp * kQ8KRecDwords, bp, chunk);
+}
+
+// SwiGLU fused into the quantization of h: h = (g / (1 + exp(-g))) * u per
+// element (Qwen36Activation::silu_mul, weights.rs:241-260), g and u the
+// gate and up rows of row t (gu = [gate rows | up rows], up_offset floats
+// apart), then quantize_q8_k of h as above.
+__global__ __launch_bounds__(256) void q8k_swiglu_quantize_kernel(const float *__restrict__ gu,
+                                                                  size_t up_offset, uint32_t cols,
+                                                                  uint32_t bp,
+                                                                  uint32_t *__restrict__ q8) {
+    const uint32_t t = blockIdx.y;
+    const uint32_t chunk = (blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+    if (chunk >= cols / 256) return;  // whole wavefronts
+    const int lane = threadIdx.x & 63, k = lane >> 3, c = lane & 7;
+    const size_t e0 = (size_t)t * cols + (size_t)chunk * 256 + 32 * k + c;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float g = gu[e0 + 8 * i], u = gu[up_offset + e0 + 8 * i];
+        v[i] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
+    }
+    q8k_quantize_values(v, q8 + (size_t)t * bp * kQ8KRecDwords, bp, chunk);
+}
+
+// Qwen RMSNorm (Qwen36Activation::rmsnorm, weights.rs:203-239: x * (1 /
+// sqrt(mean(x^2) + 1e-6)) * w) fused with the quantization of the normed
+// row: one workgroup per row, the sum of squares as a tree over the row;
+// the normed row is written to xnorm (the router's input) and staged in LDS
+// for the four wavefronts, which quantize chunks w, w + 4, ...
+__global__ __launch_bounds__(256) void q8k_rmsnorm_quantize_kernel(const float *__restrict__ x,
+                                                                   const float *__restrict__ w,
+                                                                   uint32_t H, uint32_t bp,
+                                                                   float *__restrict__ xnorm,
+                                                                   uint32_t *__restrict__ q8) {
+    __shared__ float part[4][1];
+    __shared__ float s_x[2048];
+    const uint32_t t = blockIdx.x, tid = threadIdx.x;
+    const int vpt = (int)(H / 256);
+    const float *xr = x + (size_t)t * H + tid * vpt;
+    float v8[8], ss[1] = {0.0f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        v8[j] = j < vpt ? xr[j] : 0.0f;
+        ss[0] += v8[j] * v8[j];
+    }
+    block_sum_256<1>(ss, part);
+    const float inv = 1.0f / sqrtf(ss[0] / (float)H + 1e-6f);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        if (j < vpt) {
+            const float o = v8[j] * inv * w[tid * vpt + j];
+            s_x[tid * vpt + j] = o;
+            xnorm[(size_t)t * H + tid * vpt + j] = o;
+        }
+    __syncthreads();
+    const int wave = (int)tid / kWave, lane = (int)tid & 63, k = lane >> 3, c = lane & 7;
+    for (uint32_t chunk = (uint32_t)wave; chunk < H / 256; chunk += 4) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = s_x[chunk * 256 + 32 * k + c + 8 * i];
+        q8k_quantize_values(v, q8 + (size_t)t * bp * kQ8KRecDwords, bp, chunk);
+    }
+}
+
 hipError_t launch_q8k_quantize(hipStream_t s, const float *x, uint32_t m, uint32_t cols,
                                uint32_t bp, uint32_t *q8) {
     const uint32_t waves = cols / 256;
     hipLaunchKernelGGL(q8k_quantize_kernel, dim3((waves + 3) / 4, m), dim3(256), 0, s, x, cols, bp,
+                       q8);
+    return hipGetLastError();
+}
+
+hipError_t launch_q8k_swiglu_quantize(hipStream_t s, const float *gu, uint32_t m, uint32_t cols,
+                                      uint32_t bp, uint32_t *q8) {
+    const uint32_t waves = cols / 256;
+    hipLaunchKernelGGL(q8k_swiglu_quantize_kernel, dim3((waves + 3) / 4, m), dim3(256), 0, s, gu,
+                       (size_t)m * cols, cols, bp, q8);
+    return hipGetLastError();
+}
+
+hipError_t launch_q8k_rmsnorm_quantize(hipStream_t s, const float *x, const float *w, uint32_t m,
+                                       uint32_t hidden, uint32_t bp, float *xnorm, uint32_t *q8) {
+    if (hidden == 0 || hidden % 256 || hidden > 2048) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(q8k_rmsnorm_quantize_kernel, dim3(m), dim3(256), 0, s, x, w, hidden, bp, xnorm,
                        q8);
     return hipGetLastError();
 }
@@ -413,7 +499,8 @@ __global__ __launch_bounds__(kQ4KWaves * kWave) void q4k_q8k_gemv_kernel(
         const uint32_t slot = mat % S;
         const SlotRec rec = load_slot(&plan->slots[slot]);
         if (rec.token < 0) return;  // routing failed: no work
-        base = rec.mat[SRC == kSrcSlotGateUp ? mat / S : 2];
+        // a select, not an index: a dynamic index would move the record to LDS
+        base = SRC == kSrcSlotDown ? rec.mat[2] : (mat < S ? rec.mat[0] : rec.mat[1]);
         q8 += (size_t)(SRC == kSrcSlotGateUp ? (uint32_t)rec.token : slot) * d.blocks_padded *
               kQ8KRecDwords;
     }
@@ -571,26 +658,6 @@ hipError_t launch_q4k_q8k_slots(hipStream_t s, const Plan *plan, uint32_t n_slot
 }
 
 // ---------------------------------------------------------------------------
-// SwiGLU between the Q4_K expert's up and down matvecs (Qwen36Activation::
-// silu_mul, weights.rs:241-260): h = (g / (1 + exp(-g))) * u per element,
-// written as f32 for the next quantize_q8_k.  gu holds gate rows then up
-// rows ([2 x m x F]).
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void q4k_silu_mul_kernel(const float *__restrict__ gu, uint32_t m,
-                                                           uint32_t F, float *__restrict__ h) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= m * F) return;
-    const float g = gu[i], u = gu[(size_t)m * F + i];
-    h[i] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
-}
-
-hipError_t launch_q4k_silu_mul(hipStream_t s, const float *gu, uint32_t m, uint32_t F, float *h) {
-    const uint32_t n = m * F;
-    hipLaunchKernelGGL(q4k_silu_mul_kernel, dim3((n + 255) / 256), dim3(256), 0, s, gu, m, F, h);
-    return hipGetLastError();
-}
-
-// ---------------------------------------------------------------------------
 // The MoE layer's combine (experts/mod.rs:1556-1568 per row, the arithmetic
 // of :1610-1632): output = shared down x sigmoid(shared gate logit)
 // (scale_in_place), then output += routed down x weight for each route in
@@ -620,38 +687,6 @@ hipError_t launch_q4k_moe_combine(hipStream_t s, const Plan *plan, const float *
     const uint32_t n = m * hidden;
     hipLaunchKernelGGL(q4k_moe_combine_kernel, dim3((n + 255) / 256), dim3(256), 0, s, plan, dn, m,
                        hidden, resid, y);
-    return hipGetLastError();
-}
-
-// ---------------------------------------------------------------------------
-// Qwen RMSNorm to f32 rows (Qwen36Activation::rmsnorm, weights.rs:203-239):
-// x * (1 / sqrt(mean(x^2) + 1e-6)) * w, one workgroup per row, the sum of
-// squares as a tree over the row (the route kernel's order).
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void q4k_rmsnorm_kernel(const float *__restrict__ x,
-                                                          const float *__restrict__ w, uint32_t H,
-                                                          float *__restrict__ out) {
-    __shared__ float part[4][1];
-    const uint32_t t = blockIdx.x, tid = threadIdx.x;
-    const int vpt = (int)(H / 256);
-    const float *xr = x + (size_t)t * H + tid * vpt;
-    float v[8], ss[1] = {0.0f};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        v[j] = j < vpt ? xr[j] : 0.0f;
-        ss[0] += v[j] * v[j];
-    }
-    block_sum_256<1>(ss, part);
-    const float inv = 1.0f / sqrtf(ss[0] / (float)H + 1e-6f);
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-        if (j < vpt) out[(size_t)t * H + tid * vpt + j] = v[j] * inv * w[tid * vpt + j];
-}
-
-hipError_t launch_q4k_rmsnorm(hipStream_t s, const float *x, const float *w, uint32_t m,
-                              uint32_t hidden, float *out) {
-    if (hidden == 0 || hidden % 256 || hidden > 2048) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(q4k_rmsnorm_kernel, dim3(m), dim3(256), 0, s, x, w, hidden, out);
     return hipGetLastError();
 }
 

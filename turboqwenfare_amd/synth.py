@@ -106,3 +106,33 @@ def bf16_round(x: np.ndarray) -> np.ndarray:
 
 def bf16_to_f32(x: np.ndarray) -> np.ndarray:
     return (np.ascontiguousarray(x, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def pack_q4_k_scales(sc, mn) -> np.ndarray:
+    """The 12 packed bytes holding eight 6-bit (scale, min) pairs, the
+    inverse of get_scale_min_k4 (dequant.rs:139-148): pairs 0-3 in the low
+    six bits of bytes 0-3 / 4-7; pairs 4-7 split into a low nibble (bytes
+    8-11) and two high bits (the top bits of bytes 0-3 / 4-7)."""
+    sc, mn = np.asarray(sc, np.int64), np.asarray(mn, np.int64)  # [..., 8]
+    b = np.zeros(sc.shape[:-1] + (12,), np.int64)
+    for j in range(4):
+        b[..., j] = sc[..., j] | ((sc[..., j + 4] >> 4) << 6)
+        b[..., j + 4] = mn[..., j] | ((mn[..., j + 4] >> 4) << 6)
+        b[..., j + 8] = (sc[..., j + 4] & 15) | ((mn[..., j + 4] & 15) << 4)
+    return b.astype(np.uint8)
+
+
+def centered_q4_k(rows: int, cols: int, seed: int, d_range=(1e-4, 4e-4)) -> np.ndarray:
+    """Random Q4_K bytes shaped like trained weights: per sub-block min equal
+    to its scale and dmin = 7.5 d, so the values d sc (q - 7.5) are centred
+    (up to the f16 rounding of dmin) with spread ~d sc."""
+    rng = np.random.default_rng(seed)
+    n = rows * (cols // 256)
+    blk = np.empty((n, 144), np.uint8)
+    d = rng.uniform(*d_range, size=n).astype(np.float16)
+    blk[:, 0:2] = d.view(np.uint8).reshape(n, 2)
+    blk[:, 2:4] = (d.astype(np.float32) * 7.5).astype(np.float16).view(np.uint8).reshape(n, 2)
+    sc = rng.integers(1, 64, size=(n, 8))
+    blk[:, 4:16] = pack_q4_k_scales(sc, sc)
+    blk[:, 16:] = rng.integers(0, 256, size=(n, 128), dtype=np.uint8)
+    return blk.reshape(-1)
