@@ -373,7 +373,7 @@ int32_t enqueue_layer_q4k(tqf_hip_ctx *ctx, const LayerDev &L, const float *h, c
     if (norm) x = b.xnorm;
     {
         Prof p(ctx);
-        e = launch_route(ctx->stream, L, x, nullptr, m, sc, ids, w, status);
+        e = launch_route(ctx->stream, L, x, nullptr, m, sc, ids, w, status, false);
         if (e != hipSuccess) return hip_fail(ctx, "route kernel launch", e);
         p.end(TQF_HIP_KERNEL_ROUTE, (L.n_experts + 1) * (double)H * 4 + m * (double)H * 4, 0, nullptr);
     }

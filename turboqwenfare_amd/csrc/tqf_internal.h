@@ -400,9 +400,11 @@ hipError_t launch_gemv(hipStream_t s, const uint8_t *const *d_tiles, uint32_t co
                        const MatrixDims &d, const uint32_t *xprep, uint32_t m, float *y);
 // status_out (may be null) is set to TQF_HIP_ERR_ROUTER when routing fails and
 // left untouched otherwise (a sticky flag the caller zeroes).
+// records = false skips the Q4_0 activation records (xprep), which only the
+// Q4_0 gate/up kernel reads.
 hipError_t launch_route(hipStream_t s, const LayerDev &L, const float *h, const float *norm,
                         uint32_t m, Scratch &sc, uint16_t *ids_out, float *w_out,
-                        int32_t *status_out);
+                        int32_t *status_out, bool records = true);
 // gate/up needs the gate/up matrices' padded block count (hidden / 32) and the
 // down matrix's (width / 32) in {16, 32, 64}; other shapes return
 // hipErrorInvalidValue (callers validate first).

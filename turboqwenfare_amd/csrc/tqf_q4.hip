@@ -235,9 +235,35 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
         }
     }
 
-    // 2. xprep of block kb is held by threads [kb * 32/vpt, (kb+1) * 32/vpt);
-    //    records are strided by the gate/up matrices' padded block count bp.
-    const uint32_t KB = H / 32;
+    // 2. logits of this workgroup's rows.
+    float dots[MT * kRouteRows];
+#pragma unroll
+    for (int rr = 0; rr < kRouteRows; ++rr) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            float s = 0.0f;
+#pragma unroll
+            for (int v = 0; v < 8; ++v) s = fmaf(x[t][v], wv[rr][v], s);
+            dots[rr * MT + t] = s;
+        }
+    }
+    block_sum_256<MT * kRouteRows>(dots, lds_red);
+    if (tid == 0) {
+#pragma unroll
+        for (int rr = 0; rr < kRouteRows; ++rr) {
+            const uint32_t r = blockIdx.x * kRouteRows + rr;
+            if (r <= E)
+                for (int t = 0; t < (int)m; ++t)
+                    store_coherent(&logits[(size_t)t * (E + 1) + r], dots[rr * MT + t]);
+        }
+        wait_own_stores();
+        s_last = (counter_arrive(counter) == gridDim.x - 1) ? 1 : 0;
+    }
+    // 3. xprep (when asked for) of block kb is held by threads [kb * 32/vpt,
+    //    (kb+1) * 32/vpt); records are strided by the gate/up matrices' padded
+    //    block count bp.  Written after the arrival, off the routing's
+    //    critical path: the kernels that read them start after this one ends.
+    const uint32_t KB = xprep ? H / 32 : 0;
     for (uint32_t kb = blockIdx.x; kb < KB; kb += gridDim.x) {
         const int lpb = 32 / vpt;
         const int first = (int)kb * lpb;
@@ -265,30 +291,6 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
         }
     }
 
-    // 3. logits of this workgroup's rows.
-    float dots[MT * kRouteRows];
-#pragma unroll
-    for (int rr = 0; rr < kRouteRows; ++rr) {
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            float s = 0.0f;
-#pragma unroll
-            for (int v = 0; v < 8; ++v) s = fmaf(x[t][v], wv[rr][v], s);
-            dots[rr * MT + t] = s;
-        }
-    }
-    block_sum_256<MT * kRouteRows>(dots, lds_red);
-    if (tid == 0) {
-#pragma unroll
-        for (int rr = 0; rr < kRouteRows; ++rr) {
-            const uint32_t r = blockIdx.x * kRouteRows + rr;
-            if (r <= E)
-                for (int t = 0; t < (int)m; ++t)
-                    store_coherent(&logits[(size_t)t * (E + 1) + r], dots[rr * MT + t]);
-        }
-        wait_own_stores();
-        s_last = (counter_arrive(counter) == gridDim.x - 1) ? 1 : 0;
-    }
     __syncthreads();
     if (!s_last) return;
 
@@ -433,12 +435,13 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
 
 hipError_t launch_route(hipStream_t s, const LayerDev &L, const float *h, const float *norm,
                         uint32_t m, Scratch &sc, uint16_t *ids_out, float *w_out,
-                        int32_t *status_out) {
+                        int32_t *status_out, bool records) {
     const uint32_t grid = (L.n_experts + 1 + kRouteRows - 1) / kRouteRows;
     const uint32_t bp = padded_blocks(L.hidden / 32);
     uint32_t *counter = sc.counters;
 #define TQF_ROUTE(MT)                                                                        \
-    hipLaunchKernelGGL(route_kernel<MT>, dim3(grid), dim3(256), 0, s, L, h, norm, m, bp, sc.xprep, \
+    hipLaunchKernelGGL(route_kernel<MT>, dim3(grid), dim3(256), 0, s, L, h, norm, m, bp,          \
+                       records ? sc.xprep : nullptr,                                               \
                        sc.logits, sc.plan, counter, ids_out, w_out, status_out)
     if (m <= 1) TQF_ROUTE(1);
     else if (m <= 2) TQF_ROUTE(2);
