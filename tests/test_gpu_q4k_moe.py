@@ -32,11 +32,11 @@ class Q4KLayer:
     expert weights), router and shared input gate ~N(0, 1/2048), resident on the
     device, with the GGML bytes kept for the oracle."""
 
-    def __init__(self, be, layer_id: int):
+    def __init__(self, be, layer_id: int, hidden: int = H, width: int = F):
         base = 70_000 + 1_000 * layer_id
-        self.router = synth.normal((E, H), seed=base + 1, std=H ** -0.5)
-        self.gate_vec = synth.normal((H,), seed=base + 2, std=H ** -0.5)
-        shapes = ((F, H), (F, H), (H, F))
+        self.router = synth.normal((E, hidden), seed=base + 1, std=hidden ** -0.5)
+        self.gate_vec = synth.normal((hidden,), seed=base + 2, std=hidden ** -0.5)
+        shapes = ((width, hidden), (width, hidden), (hidden, width))
         host = [tuple(centered_q4_k(r, c, base + 10 + 3 * e + i)
                       for i, (r, c) in enumerate(shapes)) for e in range(E + 1)]
         mats = [tuple(be.upload_q4_k(q, r, c) for q, (r, c) in zip(h, shapes)) for h in host]
@@ -45,7 +45,8 @@ class Q4KLayer:
                                         [m[1] for m in mats[:E]], [m[2] for m in mats[:E]])
         self.host = orc.MoeLayerHost(self.router, self.gate_vec, *host[E],
                                      [h[0] for h in host[:E]], [h[1] for h in host[:E]],
-                                     [h[2] for h in host[:E]], hidden=H, width=F, fmt="q4_k")
+                                     [h[2] for h in host[:E]], hidden=hidden, width=width,
+                                     fmt="q4_k")
         self.mats = mats
 
 
@@ -74,6 +75,23 @@ def test_q4k_moe_layer_parity_over_seeds(backend, q4k_layers, seed):
     yc, idc, _ = L.host.forward_batch(x, nthreads=8)
     assert np.array_equal(ids, idc)
     assert rel_err(y, yc) < FFN_TOL
+
+
+@pytest.mark.parametrize("hidden,width", [(256, 256), (512, 768)])
+def test_q4k_moe_layer_small_geometries(backend, hidden, width):
+    # one super-block per row (the layout pads to 16 sub-blocks) and an odd
+    # super-block count: padding sub-blocks never enter the combine
+    L = Q4KLayer(backend, 7, hidden, width)
+    for m in (1, 3, 8):
+        x = synth.normal((m, hidden), seed=700 + m)
+        y, ids, _ = backend.moe_forward_batch(L.dev, x)
+        yc, idc, _ = L.host.forward_batch(x, nthreads=8)
+        assert np.array_equal(ids, idc)
+        assert rel_err(y, yc) < FFN_TOL
+    backend.free_moe_layer(L.dev)
+    for m3 in L.mats:
+        for w in m3:
+            backend.free_weights(w)
 
 
 def test_q4k_moe_layer_bf16_input(backend, q4k_layers):
@@ -162,7 +180,7 @@ def oracle_q4k_stack(layers, norms, h):
     return h, routes
 
 
-@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("m", [1, 4, 8])
 def test_q4k_stack_forward_parity(backend, q4k_stack, m):
     layers, norms, st = q4k_stack
     h0 = synth.normal((m, H), seed=500 + m)
