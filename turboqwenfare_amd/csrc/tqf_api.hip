@@ -321,24 +321,22 @@ int32_t enqueue_layer(tqf_hip_ctx *ctx, const LayerDev &L, const float *h, const
 
 // Device views of the Q4_K layer's buffers in ctx->d_q4k, sized for m rows.
 struct Q4KLayerBufs {
-    float *xnorm, *gu, *dn;
+    float *gu, *dn;
     uint32_t *q8x, *q8h;
     size_t bytes;
 };
 Q4KLayerBufs q4k_layer_bufs(uint8_t *base, uint32_t H, uint32_t F, uint32_t m) {
     const uint32_t S = m * (kTopK + 1);
-    const size_t xn = align_up((size_t)m * H * 4, kAlign);
     const size_t qx = align_up((size_t)m * padded_blocks(H / 32) * kQ8KRecDwords * 4, kAlign);
     const size_t gu = align_up((size_t)2 * S * F * 4, kAlign);
     const size_t qh = align_up((size_t)S * padded_blocks(F / 32) * kQ8KRecDwords * 4, kAlign);
     const size_t dn = align_up((size_t)S * H * 4, kAlign);
     Q4KLayerBufs b;
-    b.xnorm = reinterpret_cast<float *>(base);
-    b.q8x = reinterpret_cast<uint32_t *>(base + xn);
-    b.gu = reinterpret_cast<float *>(base + xn + qx);
-    b.q8h = reinterpret_cast<uint32_t *>(base + xn + qx + gu);
-    b.dn = reinterpret_cast<float *>(base + xn + qx + gu + qh);
-    b.bytes = xn + qx + gu + qh + dn;
+    b.q8x = reinterpret_cast<uint32_t *>(base);
+    b.gu = reinterpret_cast<float *>(base + qx);
+    b.q8h = reinterpret_cast<uint32_t *>(base + qx + gu);
+    b.dn = reinterpret_cast<float *>(base + qx + gu + qh);
+    b.bytes = qx + gu + qh + dn;
     return b;
 }
 
@@ -353,9 +351,10 @@ int32_t ensure_q4k_layer_scratch(tqf_hip_ctx *ctx, uint32_t H, uint32_t F) {
 }
 
 // One MoE layer with Q4_K experts, every expert matvec on the Q8_K path of
-// matvec_payload (weights.rs:680-735): (RMSNorm +) Q8_K(x) -> route ->
-// gate and up of all 9 M slots -> Q8_K(silu_mul(gate, up)) -> down of all
-// slots -> combine in route order (+ residual).  The caller has run
+// matvec_payload (weights.rs:680-735): route (with the RMSNorm and the Q8_K
+// records of the rows) -> gate and up of all 9 M slots ->
+// Q8_K(silu_mul(gate, up)) -> down of all slots -> combine in route order
+// (+ residual).  The caller has run
 // ensure_moe_scratch and ensure_q4k_layer_scratch.
 int32_t enqueue_layer_q4k(tqf_hip_ctx *ctx, const LayerDev &L, const float *h, const float *norm,
                           uint32_t m, const float *resid, float *out, uint16_t *ids, float *w,
@@ -365,15 +364,10 @@ int32_t enqueue_layer_q4k(tqf_hip_ctx *ctx, const LayerDev &L, const float *h, c
     const MatrixDims dgu = matrix_dims(F, H), dd = matrix_dims(H, F);
     const Q4KLayerBufs b = q4k_layer_bufs(ctx->d_q4k, H, F, m);
     if (!ctx->d_q4k || ctx->q4k_bytes < b.bytes) return fail(ctx, TQF_HIP_ERR_INVALID, "Q4_K layer scratch missing");
-    const float *x = h;
-    hipError_t e = norm ? launch_q8k_rmsnorm_quantize(ctx->stream, h, norm, m, H, dgu.blocks_padded,
-                                                      b.xnorm, b.q8x)
-                        : launch_q8k_quantize(ctx->stream, h, m, H, dgu.blocks_padded, b.q8x);
-    if (e != hipSuccess) return hip_fail(ctx, "RMSNorm / Q8_K quantize kernel launch", e);
-    if (norm) x = b.xnorm;
+    hipError_t e = hipSuccess;
     {
         Prof p(ctx);
-        e = launch_route(ctx->stream, L, x, nullptr, m, sc, ids, w, status, false);
+        e = launch_route(ctx->stream, L, h, norm, m, sc, ids, w, status, false, b.q8x, dgu.blocks_padded);
         if (e != hipSuccess) return hip_fail(ctx, "route kernel launch", e);
         p.end(TQF_HIP_KERNEL_ROUTE, (L.n_experts + 1) * (double)H * 4 + m * (double)H * 4, 0, nullptr);
     }

@@ -471,4 +471,52 @@ __device__ __forceinline__ void block_sum_256(float (&v)[N], float (*lds)[N]) {
     for (int i = 0; i < N; ++i) v[i] = (lds[0][i] + lds[1][i]) + (lds[2][i] + lds[3][i]);
 }
 
+// quantize_q8_k (model/qwen36/weights.rs:898-931) of one 256-element chunk
+// by one wavefront, from lane 8k + c's four values v[i] = element 32k + c +
+// 8i of the chunk, into the Q8_K record row `row` (12 dwords per sub-block,
+// row stride 12 bp) at sub-blocks 8 chunk .. 8 chunk + 7.
+__device__ __forceinline__ void q8k_quantize_values(const float (&v)[4], uint32_t *row, uint32_t bp,
+                                                    uint32_t chunk) {
+    const int lane = threadIdx.x & 63, k = lane >> 3, c = lane & 7;
+    float am = -1.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a = fabsf(v[i]);
+        am = (a == a && a > am) ? a : am;
+    }
+    const float amax = group_reduce<64>(am, MaxOp());
+    const uint32_t blk = chunk * 8 + (uint32_t)k;
+    uint32_t word = 0;
+    int sum = 0;
+    float scale = 0.0f;
+    if (amax > 0.0f) {
+        int idx = 256;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (fabsf(v[i]) == amax) idx = min(idx, 32 * k + c + 8 * i);
+        idx = group_reduce<64>(idx, MinOp());
+        const int slot = (idx >> 3) & 3;
+        const float vs = slot == 0 ? v[0] : slot == 1 ? v[1] : slot == 2 ? v[2] : v[3];
+        const float smax = readlane_f(vs, 8 * (idx >> 5) + (idx & 7));
+        const float inv = __fdiv_rn(-127.0f, smax);
+        scale = __frcp_rn(inv);
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float q = __builtin_rintf(__fmul_rn(v[i], inv));
+            if (!(q <= 127.0f)) q = 127.0f;
+            if (q < -128.0f) q = -128.0f;
+            const int qi = (int)q;
+            s += qi;
+            word |= ((uint32_t)qi & 0xFFu) << (8 * i);
+        }
+        sum = group_reduce<8>(s, AddOp());
+    }
+    row[(size_t)(c >> 2) * 4 * bp + 4 * blk + (c & 3)] = word;
+    if (c == 0) {
+        row[(size_t)8 * bp + 4 * blk] = (uint32_t)sum;
+        row[(size_t)8 * bp + 4 * blk + 1] = __float_as_uint(scale);
+    }
+}
+
 }  // namespace tqf

@@ -401,10 +401,13 @@ hipError_t launch_gemv(hipStream_t s, const uint8_t *const *d_tiles, uint32_t co
 // status_out (may be null) is set to TQF_HIP_ERR_ROUTER when routing fails and
 // left untouched otherwise (a sticky flag the caller zeroes).
 // records = false skips the Q4_0 activation records (xprep), which only the
-// Q4_0 gate/up kernel reads.
+// Q4_0 gate/up kernel reads; q8 (with its record stride bp8 = the gate/up
+// matrices' padded block count) asks for the Q8_K records of the (normed)
+// rows as well, which the Q4_K gate/up reads.
 hipError_t launch_route(hipStream_t s, const LayerDev &L, const float *h, const float *norm,
                         uint32_t m, Scratch &sc, uint16_t *ids_out, float *w_out,
-                        int32_t *status_out, bool records = true);
+                        int32_t *status_out, bool records = true, uint32_t *q8 = nullptr,
+                        uint32_t bp8 = 0);
 // gate/up needs the gate/up matrices' padded block count (hidden / 32) and the
 // down matrix's (width / 32) in {16, 32, 64}; other shapes return
 // hipErrorInvalidValue (callers validate first).
@@ -442,10 +445,6 @@ hipError_t launch_q4k_q8k_gemv(hipStream_t s, const uint8_t *const *tables, uint
 // rows] ([2 x m x cols]).
 hipError_t launch_q8k_swiglu_quantize(hipStream_t s, const float *gu, uint32_t m, uint32_t cols,
                                       uint32_t bp, uint32_t *q8);
-// xnorm[t] = qwen_rmsnorm(x[t], w) (f32 rows) and its Q8_K records (hidden a
-// multiple of 256, at most 2048).
-hipError_t launch_q8k_rmsnorm_quantize(hipStream_t s, const float *x, const float *w, uint32_t m,
-                                       uint32_t hidden, uint32_t bp, float *xnorm, uint32_t *q8);
 // The Q4_K MoE layer over a route plan (n_slots = 9 M slots of launch_route):
 // gate and up of every slot (y [2 x n_slots x rows]: gate rows, then up rows;
 // the records of the slot's token, q8 [M x 12 Bp]), or down of every slot

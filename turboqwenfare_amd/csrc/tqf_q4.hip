@@ -184,7 +184,8 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
                                                     uint32_t *__restrict__ counter,
                                                     uint16_t *__restrict__ ids_out,
                                                     float *__restrict__ w_out,
-                                                    int32_t *__restrict__ status_out) {
+                                                    int32_t *__restrict__ status_out,
+                                                    uint32_t *__restrict__ q8, uint32_t bp8) {
     __shared__ float lds_red[4][MT * kRouteRows];
     __shared__ float lds_norm[4][MT];
     __shared__ int s_last;
@@ -288,6 +289,31 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
                     prep_block<1>(v1, tid - first, rec, bp, kb);
                 }
             }
+        }
+    }
+
+    // 4. Q8_K records (when asked for): workgroup j < m * H / 256 quantizes
+    //    chunk c = j % (H / 256) of row t = j / (H / 256), staged in LDS in
+    //    the quantizer's lane order.  Also after the arrival.
+    const uint32_t cpr = H / 256;
+    if (q8 != nullptr && blockIdx.x < m * cpr) {
+        __shared__ float s_chunk[256];
+        const uint32_t t = blockIdx.x / cpr, c = blockIdx.x % cpr;
+#pragma unroll
+        for (int tt = 0; tt < MT; ++tt)
+            if (tt == (int)t)
+#pragma unroll
+                for (int v = 0; v < 8; ++v) {
+                    const uint32_t e = col0 + (uint32_t)v;
+                    if (v < vpt && e >= 256 * c && e < 256 * c + 256) s_chunk[e - 256 * c] = x[tt][v];
+                }
+        __syncthreads();
+        if (tid < kWave) {
+            const int k = tid >> 3, cc = tid & 7;
+            float v4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v4[i] = s_chunk[32 * k + cc + 8 * i];
+            q8k_quantize_values(v4, q8 + (size_t)t * bp8 * kQ8KRecDwords, bp8, c);
         }
     }
 
@@ -435,14 +461,16 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
 
 hipError_t launch_route(hipStream_t s, const LayerDev &L, const float *h, const float *norm,
                         uint32_t m, Scratch &sc, uint16_t *ids_out, float *w_out,
-                        int32_t *status_out, bool records) {
+                        int32_t *status_out, bool records, uint32_t *q8, uint32_t bp8) {
+    if (q8 && (m * (L.hidden / 256) > (L.n_experts + 1 + kRouteRows - 1) / kRouteRows || bp8 < L.hidden / 32))
+        return hipErrorInvalidValue;
     const uint32_t grid = (L.n_experts + 1 + kRouteRows - 1) / kRouteRows;
     const uint32_t bp = padded_blocks(L.hidden / 32);
     uint32_t *counter = sc.counters;
 #define TQF_ROUTE(MT)                                                                        \
     hipLaunchKernelGGL(route_kernel<MT>, dim3(grid), dim3(256), 0, s, L, h, norm, m, bp,          \
                        records ? sc.xprep : nullptr,                                               \
-                       sc.logits, sc.plan, counter, ids_out, w_out, status_out)
+                       sc.logits, sc.plan, counter, ids_out, w_out, status_out, q8, bp8)
     if (m <= 1) TQF_ROUTE(1);
     else if (m <= 2) TQF_ROUTE(2);
     else if (m <= 4) TQF_ROUTE(4);

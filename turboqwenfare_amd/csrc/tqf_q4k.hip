@@ -299,53 +299,6 @@ hipError_t launch_q4k_gemv(hipStream_t s, const uint8_t *const *tables, uint32_t
 //   round_ties_even(v * inverse), then f32::min(127) (NaN -> 127) and the
 //   saturating cast to i8.
 // ---------------------------------------------------------------------------
-// The quantization of one chunk by one wavefront from the lane's four values
-// v[i] = element 32k + c + 8i of the chunk, into the record row `row` at
-// sub-blocks 8 chunk .. 8 chunk + 7.
-__device__ __forceinline__ void q8k_quantize_values(const float (&v)[4], uint32_t *row, uint32_t bp,
-                                                    uint32_t chunk) {
-    const int lane = threadIdx.x & 63, k = lane >> 3, c = lane & 7;
-    float am = -1.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float a = fabsf(v[i]);
-        am = (a == a && a > am) ? a : am;
-    }
-    const float amax = group_reduce<64>(am, MaxOp());
-    const uint32_t blk = chunk * 8 + (uint32_t)k;
-    uint32_t word = 0;
-    int sum = 0;
-    float scale = 0.0f;
-    if (amax > 0.0f) {
-        int idx = 256;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (fabsf(v[i]) == amax) idx = min(idx, 32 * k + c + 8 * i);
-        idx = group_reduce<64>(idx, MinOp());
-        const int slot = (idx >> 3) & 3;
-        const float vs = slot == 0 ? v[0] : slot == 1 ? v[1] : slot == 2 ? v[2] : v[3];
-        const float smax = readlane_f(vs, 8 * (idx >> 5) + (idx & 7));
-        const float inv = __fdiv_rn(-127.0f, smax);
-        scale = __frcp_rn(inv);
-        int s = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float q = __builtin_rintf(__fmul_rn(v[i], inv));
-            if (!(q <= 127.0f)) q = 127.0f;
-            if (q < -128.0f) q = -128.0f;
-            const int qi = (int)q;
-            s += qi;
-            word |= ((uint32_t)qi & 0xFFu) << (8 * i);
-        }
-        sum = group_reduce<8>(s, AddOp());
-    }
-    row[(size_t)(c >> 2) * 4 * bp + 4 * blk + (c & 3)] = word;
-    if (c == 0) {
-        row[(size_t)8 * bp + 4 * blk] = (uint32_t)sum;
-        row[(size_t)8 * bp + 4 * blk + 1] = __float_as_uint(scale);
-    }
-}
-
 __global__ __launch_bounds__(256) void q8k_quantize_kernel(const float *__restrict__ x,
                                                            uint32_t cols, uint32_t bp,
                                                            uint32_t *__restrict__ q8) {
@@ -382,46 +335,6 @@ __global__ __launch_bounds__(256) void q8k_swiglu_quantize_kernel(const float *_
     q8k_quantize_values(v, q8 + (size_t)t * bp * kQ8KRecDwords, bp, chunk);
 }
 
-// Qwen RMSNorm (Qwen36Activation::rmsnorm, weights.rs:203-239: x * (1 /
-// sqrt(mean(x^2) + 1e-6)) * w) fused with the quantization of the normed
-// row: one workgroup per row, the sum of squares as a tree over the row;
-// the normed row is written to xnorm (the router's input) and staged in LDS
-// for the four wavefronts, which quantize chunks w, w + 4, ...
-__global__ __launch_bounds__(256) void q8k_rmsnorm_quantize_kernel(const float *__restrict__ x,
-                                                                   const float *__restrict__ w,
-                                                                   uint32_t H, uint32_t bp,
-                                                                   float *__restrict__ xnorm,
-                                                                   uint32_t *__restrict__ q8) {
-    __shared__ float part[4][1];
-    __shared__ float s_x[2048];
-    const uint32_t t = blockIdx.x, tid = threadIdx.x;
-    const int vpt = (int)(H / 256);
-    const float *xr = x + (size_t)t * H + tid * vpt;
-    float v8[8], ss[1] = {0.0f};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        v8[j] = j < vpt ? xr[j] : 0.0f;
-        ss[0] += v8[j] * v8[j];
-    }
-    block_sum_256<1>(ss, part);
-    const float inv = 1.0f / sqrtf(ss[0] / (float)H + 1e-6f);
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-        if (j < vpt) {
-            const float o = v8[j] * inv * w[tid * vpt + j];
-            s_x[tid * vpt + j] = o;
-            xnorm[(size_t)t * H + tid * vpt + j] = o;
-        }
-    __syncthreads();
-    const int wave = (int)tid / kWave, lane = (int)tid & 63, k = lane >> 3, c = lane & 7;
-    for (uint32_t chunk = (uint32_t)wave; chunk < H / 256; chunk += 4) {
-        float v[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = s_x[chunk * 256 + 32 * k + c + 8 * i];
-        q8k_quantize_values(v, q8 + (size_t)t * bp * kQ8KRecDwords, bp, chunk);
-    }
-}
-
 hipError_t launch_q8k_quantize(hipStream_t s, const float *x, uint32_t m, uint32_t cols,
                                uint32_t bp, uint32_t *q8) {
     const uint32_t waves = cols / 256;
@@ -435,14 +348,6 @@ hipError_t launch_q8k_swiglu_quantize(hipStream_t s, const float *gu, uint32_t m
     const uint32_t waves = cols / 256;
     hipLaunchKernelGGL(q8k_swiglu_quantize_kernel, dim3((waves + 3) / 4, m), dim3(256), 0, s, gu,
                        (size_t)m * cols, cols, bp, q8);
-    return hipGetLastError();
-}
-
-hipError_t launch_q8k_rmsnorm_quantize(hipStream_t s, const float *x, const float *w, uint32_t m,
-                                       uint32_t hidden, uint32_t bp, float *xnorm, uint32_t *q8) {
-    if (hidden == 0 || hidden % 256 || hidden > 2048) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(q8k_rmsnorm_quantize_kernel, dim3(m), dim3(256), 0, s, x, w, hidden, bp, xnorm,
-                       q8);
     return hipGetLastError();
 }
 
