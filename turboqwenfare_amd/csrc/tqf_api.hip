@@ -352,9 +352,9 @@ int32_t ensure_q4k_layer_scratch(tqf_hip_ctx *ctx, uint32_t H, uint32_t F) {
 
 // One MoE layer with Q4_K experts, every expert matvec on the Q8_K path of
 // matvec_payload (weights.rs:680-735): route (with the RMSNorm and the Q8_K
-// records of the rows) -> gate and up of all 9 M slots ->
-// Q8_K(silu_mul(gate, up)) -> down of all slots -> combine in route order
-// (+ residual).  The caller has run
+// records of the rows) -> gate and up of all 9 M slots -> down of all slots
+// (each workgroup first quantizes its slot's silu_mul(gate, up) in LDS) ->
+// combine in route order (+ residual).  The caller has run
 // ensure_moe_scratch and ensure_q4k_layer_scratch.
 int32_t enqueue_layer_q4k(tqf_hip_ctx *ctx, const LayerDev &L, const float *h, const float *norm,
                           uint32_t m, const float *resid, float *out, uint16_t *ids, float *w,
@@ -377,11 +377,9 @@ int32_t enqueue_layer_q4k(tqf_hip_ctx *ctx, const LayerDev &L, const float *h, c
         if (e != hipSuccess) return hip_fail(ctx, "Q4_K gate/up kernel launch", e);
         p.end(TQF_HIP_KERNEL_Q4K_MATVEC, 2.0 * S * ((double)F * H / 256 * kQ4KBlock + F * 4.0), 0, nullptr);
     }
-    e = launch_q8k_swiglu_quantize(ctx->stream, b.gu, S, F, dd.blocks_padded, b.q8h);
-    if (e != hipSuccess) return hip_fail(ctx, "SwiGLU / Q8_K kernel launch", e);
     {
         Prof p(ctx);
-        e = launch_q4k_q8k_slots(ctx->stream, sc.plan, S, true, dd, b.q8h, b.dn);
+        e = launch_q4k_q8k_slots(ctx->stream, sc.plan, S, true, dd, nullptr, b.dn, b.gu);
         if (e != hipSuccess) return hip_fail(ctx, "Q4_K down kernel launch", e);
         p.end(TQF_HIP_KERNEL_Q4K_MATVEC, S * ((double)F * H / 256 * kQ4KBlock + H * 4.0), 0, nullptr);
     }

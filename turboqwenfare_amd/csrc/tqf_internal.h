@@ -449,8 +449,11 @@ hipError_t launch_q8k_swiglu_quantize(hipStream_t s, const float *gu, uint32_t m
 // gate and up of every slot (y [2 x n_slots x rows]: gate rows, then up rows;
 // the records of the slot's token, q8 [M x 12 Bp]), or down of every slot
 // (records of the slot's own h, q8 [n_slots x 12 Bp]; y [n_slots x rows]).
+// Down with gu (the gate/up output, [2 x n_slots x cols]) makes each slot's
+// records of h = silu_mul(gate, up) in the workgroup instead (q8 unused).
 hipError_t launch_q4k_q8k_slots(hipStream_t s, const Plan *plan, uint32_t n_slots, bool down,
-                                const MatrixDims &d, const uint32_t *q8, float *y);
+                                const MatrixDims &d, const uint32_t *q8, float *y,
+                                const float *gu = nullptr);
 // y[t] = resid[t] (if given) + (shared slot t's down x its coefficient, then
 // + route (t, k) down x weight for k = 0..7); nothing when routing failed.
 hipError_t launch_q4k_moe_combine(hipStream_t s, const Plan *plan, const float *dn, uint32_t m,

@@ -379,21 +379,45 @@ hipError_t launch_q8k_swiglu_quantize(hipStream_t s, const float *gu, uint32_t m
 // gridDim.y / 2), the records of the slot's token; kSrcSlotDown -- the down
 // matrix of slot blockIdx.y, the slot's own records.  The slot forms run one
 // row of records (m = 1) and skip slots without work (routing failed).
+// kSrcSlotDownSwiglu -- as kSrcSlotDown, but the workgroup first makes the
+// slot's records itself, in LDS: quantize_q8_k of h = silu_mul(gate, up) from
+// gu ([gate rows | up rows] of every slot, gridDim.y slots, d.cols each),
+// the arithmetic of q8k_swiglu_quantize_kernel.
 // ---------------------------------------------------------------------------
-constexpr int kSrcTables = 0, kSrcSlotGateUp = 1, kSrcSlotDown = 2;
+constexpr int kSrcTables = 0, kSrcSlotGateUp = 1, kSrcSlotDown = 2, kSrcSlotDownSwiglu = 3;
+constexpr int kMaxRecBp = 64;  // padded sub-blocks of a record row made in LDS (cols <= 2048)
 
 template <int LPR, int TG, int SRC>
 __global__ __launch_bounds__(kQ4KWaves * kWave) void q4k_q8k_gemv_kernel(
     const uint8_t *const *__restrict__ tables, const Plan *__restrict__ plan, MatrixDims d,
-    const uint32_t *__restrict__ q8, uint32_t m, float *__restrict__ y) {
+    const uint32_t *__restrict__ q8, uint32_t m, float *__restrict__ y, const float *__restrict__ gu) {
     constexpr int G = kWave / LPR;         // row octets per wavefront
     constexpr int SB = LPR / 8;            // super-blocks per lane group and chunk
     constexpr int NCH = (9 + SB - 1) / SB; // running sums per lane
     __shared__ float lds[kQ4KWaves][kWave][9];
+    __shared__ uint4 s_rec[SRC == kSrcSlotDownSwiglu ? 3 * kMaxRecBp : 1];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x % kWave;
     const int jg = lane / LPR, b = lane % LPR, k = b & 7, g = b >> 3;
     const uint32_t mat = blockIdx.y;
+    if constexpr (SRC == kSrcSlotDownSwiglu) {
+        // before any wavefront can leave: every wavefront reaches the barrier
+        if (plan->slots[mat].token >= 0) {
+            const uint32_t cols = d.cols, S = gridDim.y;
+            const int kk = lane >> 3, cc = lane & 7;
+            for (uint32_t ch = (uint32_t)wave; ch < cols / 256; ch += kQ4KWaves) {
+                const size_t e0 = (size_t)mat * cols + (size_t)ch * 256 + 32 * kk + cc;
+                float v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float gv = gu[e0 + 8 * i], uv = gu[(size_t)S * cols + e0 + 8 * i];
+                    v[i] = __fmul_rn(__fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv))), uv);
+                }
+                q8k_quantize_values(v, reinterpret_cast<uint32_t *>(s_rec), d.blocks_padded, ch);
+            }
+        }
+        __syncthreads();
+    }
     const uint32_t r0 = (blockIdx.x * kQ4KWaves + wave) * 8 * G;
     if (r0 >= d.rows_padded) return;  // no workgroup barrier below
     const uint8_t *base;
@@ -405,9 +429,10 @@ __global__ __launch_bounds__(kQ4KWaves * kWave) void q4k_q8k_gemv_kernel(
         const SlotRec rec = load_slot(&plan->slots[slot]);
         if (rec.token < 0) return;  // routing failed: no work
         // a select, not an index: a dynamic index would move the record to LDS
-        base = SRC == kSrcSlotDown ? rec.mat[2] : (mat < S ? rec.mat[0] : rec.mat[1]);
-        q8 += (size_t)(SRC == kSrcSlotGateUp ? (uint32_t)rec.token : slot) * d.blocks_padded *
-              kQ8KRecDwords;
+        base = SRC == kSrcSlotGateUp ? (mat < S ? rec.mat[0] : rec.mat[1]) : rec.mat[2];
+        if constexpr (SRC != kSrcSlotDownSwiglu)
+            q8 += (size_t)(SRC == kSrcSlotGateUp ? (uint32_t)rec.token : slot) * d.blocks_padded *
+                  kQ8KRecDwords;
     }
     const RowLane W = row_lane(base, d.blocks_padded);
     const uint32_t rl = r0 + jg * 8;
@@ -434,11 +459,17 @@ __global__ __launch_bounds__(kQ4KWaves * kWave) void q4k_q8k_gemv_kernel(
             uint4 xa[TG], xb[TG], xc[TG];
 #pragma unroll
             for (int t = 0; t < TG; ++t) {
-                const uint32_t tt = t0 + t < m ? t0 + t : 0;
-                const uint32_t *xr = q8 + tt * rstride + 4 * blk;
-                xa[t] = load_global_u4(xr);
-                xb[t] = load_global_u4(xr + 4 * bp);
-                xc[t] = load_global_u4(xr + 8 * bp);
+                if constexpr (SRC == kSrcSlotDownSwiglu) {
+                    xa[t] = s_rec[blk];
+                    xb[t] = s_rec[bp + blk];
+                    xc[t] = s_rec[2 * bp + blk];
+                } else {
+                    const uint32_t tt = t0 + t < m ? t0 + t : 0;
+                    const uint32_t *xr = q8 + tt * rstride + 4 * blk;
+                    xa[t] = load_global_u4(xr);
+                    xb[t] = load_global_u4(xr + 4 * bp);
+                    xc[t] = load_global_u4(xr + 8 * bp);
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
             uint32_t scp[8], mnp[8];  // (sc, m) of row p ^ k, stored in position p
@@ -524,26 +555,32 @@ hipError_t launch_q4k_q8k_lpr(hipStream_t s, const uint8_t *const *tables, uint3
     const dim3 grid((d.rows_padded + rows_per_group - 1) / rows_per_group, count);
     const dim3 block(kQ4KWaves * kWave);
     const Plan *none = nullptr;
+    const float *nogu = nullptr;
     if (m <= 1)
-        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 1, kSrcTables>), grid, block, 0, s, tables, none, d, q8, m, y);
+        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 1, kSrcTables>), grid, block, 0, s, tables, none, d, q8, m, y, nogu);
     else if (m <= 2)
-        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 2, kSrcTables>), grid, block, 0, s, tables, none, d, q8, m, y);
+        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 2, kSrcTables>), grid, block, 0, s, tables, none, d, q8, m, y, nogu);
     else
-        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 4, kSrcTables>), grid, block, 0, s, tables, none, d, q8, m, y);
+        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 4, kSrcTables>), grid, block, 0, s, tables, none, d, q8, m, y, nogu);
     return hipGetLastError();
 }
 
 template <int LPR>
 hipError_t launch_q4k_q8k_slots_lpr(hipStream_t s, const Plan *plan, uint32_t n_slots, bool down,
-                                    const MatrixDims &d, const uint32_t *q8, float *y) {
+                                    const MatrixDims &d, const uint32_t *q8, float *y, const float *gu) {
     constexpr uint32_t rows_per_group = kQ4KWaves * 8 * (kWave / LPR);
     const dim3 grid((d.rows_padded + rows_per_group - 1) / rows_per_group, down ? n_slots : 2 * n_slots);
     const dim3 block(kQ4KWaves * kWave);
     const uint8_t *const *none = nullptr;
-    if (down)
-        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 1, kSrcSlotDown>), grid, block, 0, s, none, plan, d, q8, 1u, y);
+    if (down && gu)
+        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 1, kSrcSlotDownSwiglu>), grid, block, 0, s, none, plan, d,
+                           q8, 1u, y, gu);
+    else if (down)
+        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 1, kSrcSlotDown>), grid, block, 0, s, none, plan, d, q8, 1u, y,
+                           gu);
     else
-        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 1, kSrcSlotGateUp>), grid, block, 0, s, none, plan, d, q8, 1u, y);
+        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 1, kSrcSlotGateUp>), grid, block, 0, s, none, plan, d, q8, 1u,
+                           y, gu);
     return hipGetLastError();
 }
 
@@ -555,11 +592,12 @@ hipError_t launch_q4k_q8k_gemv(hipStream_t s, const uint8_t *const *tables, uint
 }
 
 hipError_t launch_q4k_q8k_slots(hipStream_t s, const Plan *plan, uint32_t n_slots, bool down,
-                                const MatrixDims &d, const uint32_t *q8, float *y) {
+                                const MatrixDims &d, const uint32_t *q8, float *y, const float *gu) {
     if (n_slots == 0 || n_slots > (uint32_t)kMaxSlots) return hipErrorInvalidValue;
-    if (d.lpr == 16) return launch_q4k_q8k_slots_lpr<16>(s, plan, n_slots, down, d, q8, y);
-    if (d.lpr == 32) return launch_q4k_q8k_slots_lpr<32>(s, plan, n_slots, down, d, q8, y);
-    return launch_q4k_q8k_slots_lpr<64>(s, plan, n_slots, down, d, q8, y);
+    if (gu && (!down || d.blocks_padded > (uint32_t)kMaxRecBp || d.cols % 256)) return hipErrorInvalidValue;
+    if (d.lpr == 16) return launch_q4k_q8k_slots_lpr<16>(s, plan, n_slots, down, d, q8, y, gu);
+    if (d.lpr == 32) return launch_q4k_q8k_slots_lpr<32>(s, plan, n_slots, down, d, q8, y, gu);
+    return launch_q4k_q8k_slots_lpr<64>(s, plan, n_slots, down, d, q8, y, gu);
 }
 
 // ---------------------------------------------------------------------------
