@@ -200,21 +200,42 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
 
     // this workgroup's router rows, loaded first so that their latency
     // overlaps the activation loads and the records below
+    // (the model geometry, hidden 2048, loads 8 contiguous floats per thread
+    // as two 16-byte loads; other widths element by element)
     float wv[kRouteRows][8];
-#pragma unroll
-    for (int rr = 0; rr < kRouteRows; ++rr) {
-        const uint32_t r = blockIdx.x * kRouteRows + rr;
-        const float *wrow = (r < E) ? L.router + (size_t)r * H : L.shared_input_gate;
-#pragma unroll
-        for (int v = 0; v < 8; ++v) wv[rr][v] = (r <= E && v < vpt) ? wrow[col0 + v] : 0.0f;
-    }
-
     float x[MT][8];
+    if (vpt == 8) {
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
+        for (int rr = 0; rr < kRouteRows; ++rr) {
+            const uint32_t r = blockIdx.x * kRouteRows + rr;
+            const float *wrow = (r < E) ? L.router + (size_t)r * H : L.shared_input_gate;
+            const float4 a = r <= E ? *reinterpret_cast<const float4 *>(wrow + col0) : make_float4(0, 0, 0, 0);
+            const float4 b = r <= E ? *reinterpret_cast<const float4 *>(wrow + col0 + 4) : make_float4(0, 0, 0, 0);
+            wv[rr][0] = a.x; wv[rr][1] = a.y; wv[rr][2] = a.z; wv[rr][3] = a.w;
+            wv[rr][4] = b.x; wv[rr][5] = b.y; wv[rr][6] = b.z; wv[rr][7] = b.w;
+        }
 #pragma unroll
-        for (int v = 0; v < 8; ++v)
-            x[t][v] = (t < (int)m && v < vpt) ? h[(size_t)t * H + col0 + v] : 0.0f;
+        for (int t = 0; t < MT; ++t) {
+            const float *xr = h + (size_t)t * H + col0;
+            const float4 a = t < (int)m ? *reinterpret_cast<const float4 *>(xr) : make_float4(0, 0, 0, 0);
+            const float4 b = t < (int)m ? *reinterpret_cast<const float4 *>(xr + 4) : make_float4(0, 0, 0, 0);
+            x[t][0] = a.x; x[t][1] = a.y; x[t][2] = a.z; x[t][3] = a.w;
+            x[t][4] = b.x; x[t][5] = b.y; x[t][6] = b.z; x[t][7] = b.w;
+        }
+    } else {
+#pragma unroll
+        for (int rr = 0; rr < kRouteRows; ++rr) {
+            const uint32_t r = blockIdx.x * kRouteRows + rr;
+            const float *wrow = (r < E) ? L.router + (size_t)r * H : L.shared_input_gate;
+#pragma unroll
+            for (int v = 0; v < 8; ++v) wv[rr][v] = (r <= E && v < vpt) ? wrow[col0 + v] : 0.0f;
+        }
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int v = 0; v < 8; ++v)
+                x[t][v] = (t < (int)m && v < vpt) ? h[(size_t)t * H + col0 + v] : 0.0f;
+    }
 
     if (norm != nullptr) {
         float ss[MT];
