@@ -206,6 +206,10 @@ __device__ void phase_a(const StackArgs &a, const StackLayer &L, const float *hi
     const uint32_t m = a.m, E = a.E;
     const uint32_t col = 256 * wave + 4 * lane;
     const float4 nw = load_global_f4(L.norm + col);
+    // this workgroup's first router row (gridDim.x <= E + 1), issued ahead of
+    // the h staging so that the two round trips overlap
+    const uint32_t e0 = blockIdx.x;
+    const float4 r_first = load_global_f4((e0 < E ? L.router + (size_t)e0 * H : L.gate_vec) + col);
     float sq[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t)
@@ -228,7 +232,7 @@ __device__ void phase_a(const StackArgs &a, const StackLayer &L, const float *hi
         xn[t] = make_float4(hv.x * inv * nw.x, hv.y * inv * nw.y, hv.z * inv * nw.z, hv.w * inv * nw.w);
     }
     for (uint32_t e = blockIdx.x; e <= E; e += gridDim.x) {
-        const float4 r = load_global_f4((e < E ? L.router + (size_t)e * H : L.gate_vec) + col);
+        const float4 r = e == e0 ? r_first : load_global_f4((e < E ? L.router + (size_t)e * H : L.gate_vec) + col);
         float dot[MT];
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
