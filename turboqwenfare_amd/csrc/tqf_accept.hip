@@ -497,15 +497,17 @@ __global__ __launch_bounds__(kAccThreads) void acc_sums_kernel(AccArgs a) {
     __shared__ float s_lt[kMaxTokens], s_ld[kMaxTokens];
     __shared__ uint32_t s_istar;
     __shared__ int32_t s_tok;
+    // the chunk's loads first: their round trip overlaps wavefront 0's reads
+    // of the row maxima
+    float v[kAccPerThread];
+    uint32_t xs[kAccPerThread];
+    load_chunk(acc_row(a, r), a.vocab, c, tid, v, xs);
     if (wave == 0) {
         float M = -__builtin_inff();
         for (uint32_t cc = lane; cc < A.L.nch; cc += 64) M = fmaxf(M, A.pmax[(size_t)r * A.L.nch + cc]);
         M = group_reduce<64>(M, MaxOp());
         if (lane == 0) s_M = M;
     }
-    float v[kAccPerThread];
-    uint32_t xs[kAccPerThread];
-    load_chunk(acc_row(a, r), a.vocab, c, tid, v, xs);
     __syncthreads();
     const float M = s_M;
     uint64_t s = 0;
@@ -571,6 +573,12 @@ __global__ __launch_bounds__(kAccThreads) void acc_residual_kernel(AccArgs a) {
     __shared__ uint64_t s_red[4];
     __shared__ int s_last;
     __shared__ int32_t s_tok;
+    // the chunk's loads first: their round trip overlaps the row statistics
+    const float *tr = a.target + (size_t)istar * a.vocab, *dr = a.draft + (size_t)istar * a.vocab;
+    float vt[kAccPerThread], vd[kAccPerThread];
+    uint32_t xs[kAccPerThread];
+    load_chunk(tr, a.vocab, blockIdx.x, tid, vt, xs);
+    load_chunk(dr, a.vocab, blockIdx.x, tid, vd, xs);
     if (wave < 2) {
         const RowStat st = wave_row_stat(A, wave == 0 ? istar : a.k + 1 + istar, false, lane);
         if (lane == 0) {
@@ -579,12 +587,7 @@ __global__ __launch_bounds__(kAccThreads) void acc_residual_kernel(AccArgs a) {
         }
     }
     __syncthreads();
-    const SampleRows srow{a.target + (size_t)istar * a.vocab, a.draft + (size_t)istar * a.vocab,
-                          s_sp, s_sq, true};
-    float vt[kAccPerThread], vd[kAccPerThread];
-    uint32_t xs[kAccPerThread];
-    load_chunk(srow.tr, a.vocab, blockIdx.x, tid, vt, xs);
-    load_chunk(srow.dr, a.vocab, blockIdx.x, tid, vd, xs);
+    const SampleRows srow{tr, dr, s_sp, s_sq, true};
     uint64_t s = 0;
 #pragma unroll
     for (int i = 0; i < kAccPerThread; ++i)
