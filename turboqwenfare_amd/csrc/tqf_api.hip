@@ -377,14 +377,19 @@ int32_t enqueue_layer_q4k(tqf_hip_ctx *ctx, const LayerDev &L, const float *h, c
         if (e != hipSuccess) return hip_fail(ctx, "Q4_K gate/up kernel launch", e);
         p.end(TQF_HIP_KERNEL_Q4K_MATVEC, 2.0 * S * ((double)F * H / 256 * kQ4KBlock + F * 4.0), 0, nullptr);
     }
+    const bool fold = q4k_fold_ok(dd);  // the combine folded into the down launch
     {
         Prof p(ctx);
-        e = launch_q4k_q8k_slots(ctx->stream, sc.plan, S, true, dd, nullptr, b.dn, b.gu);
+        e = fold ? launch_q4k_q8k_slots(ctx->stream, sc.plan, S, true, dd, nullptr, b.dn, b.gu, out, resid,
+                                        sc.counters + counter_fold_offset(H))
+                 : launch_q4k_q8k_slots(ctx->stream, sc.plan, S, true, dd, nullptr, b.dn, b.gu);
         if (e != hipSuccess) return hip_fail(ctx, "Q4_K down kernel launch", e);
         p.end(TQF_HIP_KERNEL_Q4K_MATVEC, S * ((double)F * H / 256 * kQ4KBlock + H * 4.0), 0, nullptr);
     }
-    e = launch_q4k_moe_combine(ctx->stream, sc.plan, b.dn, m, H, resid, out);
-    if (e != hipSuccess) return hip_fail(ctx, "combine kernel launch", e);
+    if (!fold) {
+        e = launch_q4k_moe_combine(ctx->stream, sc.plan, b.dn, m, H, resid, out);
+        if (e != hipSuccess) return hip_fail(ctx, "combine kernel launch", e);
+    }
     return TQF_HIP_OK;
 }
 

@@ -386,7 +386,12 @@ namespace tqf {
 // hidden / 16)].  Every counter returns to zero in the workgroup that
 // finishes its kernel.
 constexpr int kCounterDown = 64;
-inline size_t counter_count(uint32_t hidden) { return kCounterDown + hidden / 16; }
+// [0, 64) route; [64, 64 + hidden / 16) the Q4_0 down kernel; then the Q4_K
+// down launch's combine fold, kMaxTokens x (hidden / 64) (token, row tile)
+inline size_t counter_fold_offset(uint32_t hidden) { return kCounterDown + hidden / 16; }
+inline size_t counter_count(uint32_t hidden) {
+    return counter_fold_offset(hidden) + (size_t)kMaxTokens * (hidden / 64);
+}
 
 // ---- launchers (defined in the .hip translation units) -------------------
 // All are asynchronous on ctx->stream and return a hipError_t.
@@ -451,9 +456,15 @@ hipError_t launch_q8k_swiglu_quantize(hipStream_t s, const float *gu, uint32_t m
 // (records of the slot's own h, q8 [n_slots x 12 Bp]; y [n_slots x rows]).
 // Down with gu (the gate/up output, [2 x n_slots x cols]) makes each slot's
 // records of h = silu_mul(gate, up) in the workgroup instead (q8 unused).
+// With out (and counters [M x q4k_fold_tiles(d)], zero between launches),
+// the down form also folds in launch_q4k_moe_combine's work (+ resid), so
+// out receives the layer output without a combine launch.
 hipError_t launch_q4k_q8k_slots(hipStream_t s, const Plan *plan, uint32_t n_slots, bool down,
                                 const MatrixDims &d, const uint32_t *q8, float *y,
-                                const float *gu = nullptr);
+                                const float *gu = nullptr, float *out = nullptr,
+                                const float *resid = nullptr, uint32_t *counters = nullptr);
+uint32_t q4k_fold_tiles(const MatrixDims &d);
+bool q4k_fold_ok(const MatrixDims &d);  // the down matrix's shape allows the fold
 // y[t] = resid[t] (if given) + (shared slot t's down x its coefficient, then
 // + route (t, k) down x weight for k = 0..7); nothing when routing failed.
 hipError_t launch_q4k_moe_combine(hipStream_t s, const Plan *plan, const float *dn, uint32_t m,

@@ -383,14 +383,27 @@ hipError_t launch_q8k_swiglu_quantize(hipStream_t s, const float *gu, uint32_t m
 // slot's records itself, in LDS: quantize_q8_k of h = silu_mul(gate, up) from
 // gu ([gate rows | up rows] of every slot, gridDim.y slots, d.cols each),
 // the arithmetic of q8k_swiglu_quantize_kernel.
+// With fold.out set (kSrcSlotDownSwiglu only; every wavefront of a
+// workgroup has rows), the layer's combine is folded in: each slot
+// workgroup writes its rows of y with device-coherent stores and arrives on
+// the counter of (its token, its row tile); the last of the token's nine
+// slots to arrive sums them for the tile in q4k_moe_combine_kernel's order
+// and arithmetic, adds the residual, writes fold.out, and resets the counter.
 // ---------------------------------------------------------------------------
 constexpr int kSrcTables = 0, kSrcSlotGateUp = 1, kSrcSlotDown = 2, kSrcSlotDownSwiglu = 3;
 constexpr int kMaxRecBp = 64;  // padded sub-blocks of a record row made in LDS (cols <= 2048)
 
+struct Fold {
+    float *out;             // [M x rows] layer output (may alias resid)
+    const float *resid;     // [M x rows] or null
+    uint32_t *counters;     // [M x tiles], zero between launches
+};
+
 template <int LPR, int TG, int SRC>
 __global__ __launch_bounds__(kQ4KWaves * kWave) void q4k_q8k_gemv_kernel(
     const uint8_t *const *__restrict__ tables, const Plan *__restrict__ plan, MatrixDims d,
-    const uint32_t *__restrict__ q8, uint32_t m, float *__restrict__ y, const float *__restrict__ gu) {
+    const uint32_t *__restrict__ q8, uint32_t m, float *__restrict__ y, const float *__restrict__ gu,
+    Fold fold) {
     constexpr int G = kWave / LPR;         // row octets per wavefront
     constexpr int SB = LPR / 8;            // super-blocks per lane group and chunk
     constexpr int NCH = (9 + SB - 1) / SB; // running sums per lane
@@ -541,10 +554,39 @@ __global__ __launch_bounds__(kQ4KWaves * kWave) void q4k_q8k_gemv_kernel(
 #pragma unroll
                 for (int ch = 0; ch < 8; ++ch) total = __fadd_rn(total, my[gbase + 8 * (ch % SB) + k][ch / SB]);
                 const float minimum = my[gbase + 8 * (8 % SB) + k][8 / SB];
-                y[((size_t)mat * m + t0 + t) * d.rows + rl + k] = __fadd_rn(minimum, total);
+                float *dst = &y[((size_t)mat * m + t0 + t) * d.rows + rl + k];
+                if (SRC == kSrcSlotDownSwiglu && fold.out) store_coherent(dst, __fadd_rn(minimum, total));
+                else *dst = __fadd_rn(minimum, total);
             }
             wave_sync();
         }
+    }
+    if constexpr (SRC == kSrcSlotDownSwiglu) {
+        if (!fold.out) return;
+        __shared__ int s_last;
+        const uint32_t tile = blockIdx.x, tiles = gridDim.x;
+        const int token = plan->slots[mat].token;  // >= 0: slots without work left above
+        wait_own_stores();
+        __syncthreads();
+        if (threadIdx.x == 0)
+            s_last = counter_arrive(&fold.counters[(uint32_t)token * tiles + tile]) == (uint32_t)kTopK ? 1 : 0;
+        __syncthreads();
+        if (!s_last) return;
+        const uint32_t H = d.rows, rows_per_tile = H / tiles;
+        const float coef = plan->slots[token].coef;
+        for (uint32_t r = threadIdx.x; r < rows_per_tile; r += blockDim.x) {
+            const uint32_t c = tile * rows_per_tile + r;
+            float o = __fmul_rn(load_coherent(&y[(size_t)token * H + c]), coef);
+#pragma unroll
+            for (int kk = 0; kk < kTopK; ++kk) {
+                const int slot = plan->pair_slot[token * kTopK + kk];
+                o = __fadd_rn(o, __fmul_rn(load_coherent(&y[(size_t)slot * H + c]), plan->weights[token][kk]));
+            }
+            const size_t i = (size_t)token * H + c;
+            if (fold.resid) o = __fadd_rn(fold.resid[i], o);
+            fold.out[i] = o;
+        }
+        if (threadIdx.x == 0) counter_reset(&fold.counters[(uint32_t)token * tiles + tile]);
     }
 }
 
@@ -557,30 +599,33 @@ hipError_t launch_q4k_q8k_lpr(hipStream_t s, const uint8_t *const *tables, uint3
     const Plan *none = nullptr;
     const float *nogu = nullptr;
     if (m <= 1)
-        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 1, kSrcTables>), grid, block, 0, s, tables, none, d, q8, m, y, nogu);
+        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 1, kSrcTables>), grid, block, 0, s, tables, none, d, q8, m, y, nogu, Fold{});
     else if (m <= 2)
-        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 2, kSrcTables>), grid, block, 0, s, tables, none, d, q8, m, y, nogu);
+        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 2, kSrcTables>), grid, block, 0, s, tables, none, d, q8, m, y, nogu, Fold{});
     else
-        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 4, kSrcTables>), grid, block, 0, s, tables, none, d, q8, m, y, nogu);
+        hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 4, kSrcTables>), grid, block, 0, s, tables, none, d, q8, m, y, nogu, Fold{});
     return hipGetLastError();
 }
 
 template <int LPR>
 hipError_t launch_q4k_q8k_slots_lpr(hipStream_t s, const Plan *plan, uint32_t n_slots, bool down,
-                                    const MatrixDims &d, const uint32_t *q8, float *y, const float *gu) {
+                                    const MatrixDims &d, const uint32_t *q8, float *y, const float *gu,
+                                    const Fold &fold) {
     constexpr uint32_t rows_per_group = kQ4KWaves * 8 * (kWave / LPR);
     const dim3 grid((d.rows_padded + rows_per_group - 1) / rows_per_group, down ? n_slots : 2 * n_slots);
     const dim3 block(kQ4KWaves * kWave);
     const uint8_t *const *none = nullptr;
+    // the fold needs every wavefront of every workgroup to own rows
+    if (fold.out && (!down || !gu || d.rows % rows_per_group || d.rows_padded != d.rows)) return hipErrorInvalidValue;
     if (down && gu)
         hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 1, kSrcSlotDownSwiglu>), grid, block, 0, s, none, plan, d,
-                           q8, 1u, y, gu);
+                           q8, 1u, y, gu, fold);
     else if (down)
         hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 1, kSrcSlotDown>), grid, block, 0, s, none, plan, d, q8, 1u, y,
-                           gu);
+                           gu, Fold{});
     else
         hipLaunchKernelGGL((q4k_q8k_gemv_kernel<LPR, 1, kSrcSlotGateUp>), grid, block, 0, s, none, plan, d, q8, 1u,
-                           y, gu);
+                           y, gu, Fold{});
     return hipGetLastError();
 }
 
@@ -592,12 +637,26 @@ hipError_t launch_q4k_q8k_gemv(hipStream_t s, const uint8_t *const *tables, uint
 }
 
 hipError_t launch_q4k_q8k_slots(hipStream_t s, const Plan *plan, uint32_t n_slots, bool down,
-                                const MatrixDims &d, const uint32_t *q8, float *y, const float *gu) {
+                                const MatrixDims &d, const uint32_t *q8, float *y, const float *gu,
+                                float *out, const float *resid, uint32_t *counters) {
     if (n_slots == 0 || n_slots > (uint32_t)kMaxSlots) return hipErrorInvalidValue;
     if (gu && (!down || d.blocks_padded > (uint32_t)kMaxRecBp || d.cols % 256)) return hipErrorInvalidValue;
-    if (d.lpr == 16) return launch_q4k_q8k_slots_lpr<16>(s, plan, n_slots, down, d, q8, y, gu);
-    if (d.lpr == 32) return launch_q4k_q8k_slots_lpr<32>(s, plan, n_slots, down, d, q8, y, gu);
-    return launch_q4k_q8k_slots_lpr<64>(s, plan, n_slots, down, d, q8, y, gu);
+    if (out && (!counters || n_slots % (kTopK + 1))) return hipErrorInvalidValue;
+    const Fold fold{out, resid, counters};
+    if (d.lpr == 16) return launch_q4k_q8k_slots_lpr<16>(s, plan, n_slots, down, d, q8, y, gu, fold);
+    if (d.lpr == 32) return launch_q4k_q8k_slots_lpr<32>(s, plan, n_slots, down, d, q8, y, gu, fold);
+    return launch_q4k_q8k_slots_lpr<64>(s, plan, n_slots, down, d, q8, y, gu, fold);
+}
+
+uint32_t q4k_fold_tiles(const MatrixDims &d) {
+    const uint32_t rows_per_group = kQ4KWaves * 8 * (kWave / d.lpr);
+    return (d.rows_padded + rows_per_group - 1) / rows_per_group;
+}
+
+bool q4k_fold_ok(const MatrixDims &d) {
+    const uint32_t rows_per_group = kQ4KWaves * 8 * (kWave / d.lpr);
+    return d.rows % rows_per_group == 0 && d.rows_padded == d.rows && d.blocks_padded <= (uint32_t)kMaxRecBp &&
+           d.cols % 256 == 0 && q4k_fold_tiles(d) <= d.rows / 64;
 }
 
 // ---------------------------------------------------------------------------
