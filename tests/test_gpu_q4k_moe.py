@@ -245,3 +245,33 @@ def test_q4k_verify_step_graph_replays_match_eager(backend, q4k_stack):
         assert (a, [int(v) for v in tk[: a + 1]]) == want
     for b in list(bufs.values()) + [acc, toks, dh, dh_e]:
         backend.free(b)
+
+
+
+def test_q4k_folded_combine_equals_the_combine_launch(backend, q4k_stack):
+    """The down launch's folded combine and q4k_moe_combine_kernel run the same
+    arithmetic in the same order: a layer and a 2-layer stack give the same
+    bits with the fold switched off (TQF_HIP_Q4K_FOLD=0, read per call)."""
+    import os
+
+    layers, norms, st = q4k_stack
+    x = synth.normal((4, H), seed=808)
+    outs = []
+    old = os.environ.get("TQF_HIP_Q4K_FOLD")
+    try:
+        for fold in ("1", "0"):
+            os.environ["TQF_HIP_Q4K_FOLD"] = fold
+            y, _, _ = backend.moe_forward_batch(layers[0].dev, x)
+            dh = backend.to_device(x)
+            backend.profile_enable(True)  # eager launches: a graph keeps its first capture
+            backend.stack_forward_device(st, dh, 4)
+            backend.profile_enable(False)
+            outs.append((y, backend.read(dh, np.float32, (4, H))))
+            backend.free(dh)
+    finally:
+        if old is None:
+            del os.environ["TQF_HIP_Q4K_FOLD"]
+        else:
+            os.environ["TQF_HIP_Q4K_FOLD"] = old
+    for a, b in zip(outs[0], outs[1]):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

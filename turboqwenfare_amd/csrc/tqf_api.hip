@@ -377,7 +377,10 @@ int32_t enqueue_layer_q4k(tqf_hip_ctx *ctx, const LayerDev &L, const float *h, c
         if (e != hipSuccess) return hip_fail(ctx, "Q4_K gate/up kernel launch", e);
         p.end(TQF_HIP_KERNEL_Q4K_MATVEC, 2.0 * S * ((double)F * H / 256 * kQ4KBlock + F * 4.0), 0, nullptr);
     }
-    const bool fold = q4k_fold_ok(dd);  // the combine folded into the down launch
+    // the combine folded into the down launch; TQF_HIP_Q4K_FOLD=0 in the
+    // environment keeps the separate combine launch (the same arithmetic)
+    const char *fold_env = std::getenv("TQF_HIP_Q4K_FOLD");
+    const bool fold = !(fold_env && fold_env[0] == '0') && q4k_fold_ok(dd);
     {
         Prof p(ctx);
         e = fold ? launch_q4k_q8k_slots(ctx->stream, sc.plan, S, true, dd, nullptr, b.dn, b.gu, out, resid,
