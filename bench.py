@@ -8,6 +8,13 @@ stacked MoE FFN layers h <- h + MoE_l(rmsnorm_l(h)) (model/qwen36/runtime.rs:
 SwiGLU experts, followed by acceptance sampling over fp32 logits [4, 151936]
 at T = 0.7 with Philox uniforms.  Inputs are resident in HBM before timing.
 
+The headline experts use the zero-mean nibble recipe (q - 8 symmetric on
+[-7, 7]), under which the four rows keep routing apart (expert union ~30 per
+layer, the i.i.d. expectation).  The literal recipe (nibbles uniform on
+0..15, E[q - 8] = -0.5) gives every matrix a common-mode component that
+collapses the rows onto one direction within a few layers (union ~10); its
+figure is reported beside the headline as a side key.
+
 Prints ONE JSON line (progress goes to stderr).  `value` is verify steps/s.
 The roofline object is for the dominant kernel (the persistent stack kernel,
 one cooperative launch per step) timed with HIP events on the library's
@@ -39,26 +46,11 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def build_model(be, n_layers: int, seed: int):
-    """Seeded synthetic 40-layer weight set generated directly in HBM."""
-    from turboqwenfare_amd import synth
+def build_model(be, n_layers: int, seed: int, recipe: str):
+    """Seeded synthetic n_layers-layer weight set generated directly in HBM."""
+    from turboqwenfare_amd.workloads import SyntheticStack
 
-    layers, norms, host_f32 = [], [], []
-    for l in range(n_layers):
-        base = 1_000_000 * (l + 1)
-        mats = [(be.synth_q4_0(F, H, base + 3 * e, seed), be.synth_q4_0(F, H, base + 3 * e + 1, seed),
-                 be.synth_q4_0(H, F, base + 3 * e + 2, seed)) for e in range(E + 1)]
-        router = synth.normal((E, H), seed=base + 7, std=H ** -0.5)
-        gate = synth.normal((H,), seed=base + 8, std=H ** -0.5)
-        norm = (1.0 + 0.05 * synth.normal((H,), seed=base + 9)).astype(np.float32)
-        layers.append(be.prepare_moe_layer(be.upload_f32(router), be.upload_f32(gate), mats[E],
-                                           [m[0] for m in mats[:E]], [m[1] for m in mats[:E]],
-                                           [m[2] for m in mats[:E]]))
-        norms.append(be.upload_f32(norm))
-        host_f32.append((router, gate, norm) if l < 4 else None)
-        if (l + 1) % 10 == 0:
-            log(f"bench: {l + 1}/{n_layers} layers resident")
-    return layers, norms, host_f32
+    return SyntheticStack(be, n_layers, seed, recipe, log=lambda m: log("bench: " + m))
 
 
 def verify_inputs(seed: int):
@@ -84,7 +76,7 @@ def host_cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(be, layers, host_f32, inputs, budget_s: float):
+def cpu_baseline(model, inputs, budget_s: float):
     """The reference's portable scalar path (C restatement, -O3
     -ffp-contract=off) on this host: MoE layers at M = 4 plus the acceptance
     at V = 151936, timed on a bounded sample of layers and scaled to 40."""
@@ -93,16 +85,13 @@ def cpu_baseline(be, layers, host_f32, inputs, budget_s: float):
 
     target, draft, dtok, u, ur, h0 = inputs
     threads = int(os.environ.get("OMP_NUM_THREADS") or len(os.sched_getaffinity(0)))
-    n_sample = min(4, len(layers))
+    n_sample = min(4, model.n_layers)
     hosts, norm_host = [], []
-    for L, (router, gate, norm) in zip(layers[:n_sample], host_f32[:n_sample]):
-        mats = L.owned[2:]
-        sg, su, sd = mats[0:3]
-        rg, ru, rd = mats[3:3 + E], mats[3 + E:3 + 2 * E], mats[3 + 2 * E:3 + 3 * E]
-        hosts.append(orc.MoeLayerHost(
-            router, gate, *(be.download_q4_0(w) for w in (sg, su, sd)),
-            [be.download_q4_0(w) for w in rg], [be.download_q4_0(w) for w in ru],
-            [be.download_q4_0(w) for w in rd]))
+    for l in range(n_sample):
+        router, gate, norm = model.host_f32[l]
+        ex = [model.expert_q4_0(l, e) for e in range(E + 1)]
+        hosts.append(orc.MoeLayerHost(router, gate, *ex[E], [x[0] for x in ex[:E]],
+                                      [x[1] for x in ex[:E]], [x[2] for x in ex[:E]]))
         norm_host.append(norm)
 
     def run_layers(nthreads):
@@ -125,7 +114,7 @@ def cpu_baseline(be, layers, host_f32, inputs, budget_s: float):
     t_acc = timed(lambda: orc.accept(target, draft, dtok, TEMPERATURE, False, u, ur), 0.5)
     for nt in sorted({1, threads}):
         per_sample = timed(lambda: run_layers(nt), budget_s / 2)
-        per_step = per_sample / n_sample * len(layers) + t_acc
+        per_step = per_sample / n_sample * model.n_layers + t_acc
         res[nt] = 1.0 / per_step
         log(f"bench: cpu {nt} thread(s): {per_sample / n_sample * 1e3:.1f} ms/layer, "
             f"{per_step * 1e3:.1f} ms/step")
@@ -336,6 +325,194 @@ def lm_head_bench(be, seed: int, iters: int = 20):
     return out
 
 
+def verify_bench(be, model, inputs, steps: int, warmup: int, greedy: bool, distribution=True):
+    """Config 4 on a resident model: verify steps/s (stream-ordered), the
+    per-step distribution, HIP-event kernel times of eager launches, and the
+    algorithmic bytes of the dominant kernel from the routes of the same input."""
+    from turboqwenfare_amd import _lib, mtp
+
+    target, draft, dtok, u, ur, h0 = inputs
+    d = {k: be.to_device(v) for k, v in dict(t=target, d=draft, dt=dtok, u=u, ur=ur, h0=h0,
+                                              h=h0).items()}
+    d_acc, d_tok = be.alloc(4), be.alloc(4 * M)
+    d_st = be.to_device(np.zeros(1, np.int32))
+    st = model.stack
+
+    def step():
+        be.verify_step_device(st, d["h0"], d["h"], M, d["t"], None if greedy else d["d"],
+                              d["dt"], V, TEMPERATURE, greedy, d["u"], d["ur"], d_acc, d_tok, d_st)
+
+    for _ in range(warmup):
+        step()
+    be.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    be.synchronize()
+    elapsed = time.perf_counter() - t0
+    status = int(be.read(d_st, np.int32, (1,))[0])
+    if status != 0:
+        raise RuntimeError(f"verify step reported device status {status}")
+    out = dict(steps_per_s=steps / elapsed, ms_per_step=elapsed / steps * 1e3)
+    if distribution:
+        # each step synchronised on its own (so each sample also holds one
+        # launch + synchronise round trip)
+        per_step = []
+        for _ in range(steps):
+            t1 = time.perf_counter()
+            step()
+            be.synchronize()
+            per_step.append((time.perf_counter() - t1) * 1e3)
+        q10, q50, q90 = (float(v) for v in np.percentile(per_step, [10, 50, 90]))
+        out["synchronised_step_ms"] = {"p10": q10, "median": q50, "p90": q90}
+    # kernel timing with HIP events on the library stream (eager launches)
+    be.profile_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    be.synchronize()
+    out["eager_profiled_ms_per_step"] = (time.perf_counter() - t0) / steps * 1e3
+    prof = {}
+    for kind, nm in ((_lib.KERNEL_STACK, "stack"), (_lib.KERNEL_ROUTE, "route"),
+                     (_lib.KERNEL_GATE_UP, "gate_up"), (_lib.KERNEL_DOWN, "down"),
+                     (_lib.KERNEL_ACCEPT, "accept")):
+        n, ms, by = be.profile_read(kind)
+        if n:
+            prof[nm] = dict(launches=n, avg_us=ms / n * 1e3, bytes_per_launch=by / n,
+                            gbs=by / (ms * 1e-3) / 1e9 if ms > 0 else 0.0)
+    be.profile_enable(False)
+    # algorithmic HBM bytes of one stack pass: every layer's router (f32
+    # [E+1 x H] incl. the shared input gate), RMSNorm weight and the Q4_0
+    # bytes of its (union + shared) experts, from the routes of the same input
+    n_layers = model.n_layers
+    d_ids = be.alloc(n_layers * M * 8 * 2)
+    d_tmp = be.alloc(M * H * 4)
+    be.stack_forward_device(st, d_tmp, M, d_ids, d_h_in=d["h0"])
+    ids = be.read(d_ids, np.uint16, (n_layers, M, 8))
+    unions = [len(mtp.routes_union(ids[l])) for l in range(n_layers)]
+    stack_bytes = sum((un + 1) * mtp.expert_bytes_q4_0() + (E + 1) * H * 4 + H * 4
+                      for un in unions) + 2 * M * H * 4
+    accept_bytes = (2 * K + 1) * V * 4 if not greedy else (K + 1) * V * 4
+    if "stack" in prof:
+        prof["stack"]["bytes_per_launch"] = stack_bytes
+        prof["stack"]["gbs"] = stack_bytes / (prof["stack"]["avg_us"] * 1e-6) / 1e9
+    if "accept" in prof:
+        prof["accept"]["bytes_per_launch"] = accept_bytes
+        prof["accept"]["gbs"] = accept_bytes / (prof["accept"]["avg_us"] * 1e-6) / 1e9
+    out["kernels"] = prof
+    out["expert_union"] = {"mean": float(np.mean(unions)), "min": int(min(unions)),
+                           "max": int(max(unions))}
+    out["stack_algorithmic_bytes"] = stack_bytes
+    for b in list(d.values()) + [d_acc, d_tok, d_st, d_ids, d_tmp]:
+        be.free(b)
+    return out
+
+
+def stack_m1_bench(be, model, seed: int, iters: int = 20):
+    """The 40-layer stack at M = 1 (decode): HIP-event time of the stack
+    kernel per launch and per layer, with its algorithmic bytes."""
+    from turboqwenfare_amd import _lib, mtp, synth
+
+    h0 = synth.normal((1, H), seed=seed + 1)
+    dh0, dh = be.to_device(h0), be.alloc(H * 4)
+    be.stack_forward_device(model.stack, dh, 1, d_h_in=dh0)
+    be.profile_enable(True)
+    for _ in range(iters):
+        be.stack_forward_device(model.stack, dh, 1, d_h_in=dh0)
+    n, ms, _ = be.profile_read(_lib.KERNEL_STACK)
+    if not n:  # a device without the persistent path: the per-layer kernels
+        n, ms = iters, sum(be.profile_read(k)[1] for k in (_lib.KERNEL_ROUTE, _lib.KERNEL_GATE_UP,
+                                                           _lib.KERNEL_DOWN))
+    be.profile_enable(False)
+    nb = model.n_layers * (9 * mtp.expert_bytes_q4_0() + (E + 1) * H * 4 + H * 4) + 2 * H * 4
+    us = ms / n * 1e3
+    be.free(dh0)
+    be.free(dh)
+    return dict(m=1, layers=model.n_layers, avg_us=us, per_layer_us=us / model.n_layers,
+                algorithmic_bytes=nb, gbs=nb / (us * 1e-6) / 1e9,
+                frac=nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS)
+
+
+def layer_bench(be, model, inputs, m: int, with_accept: bool, seed: int, iters: int = 50):
+    """Configs 2 and 3: one MoE layer (layer 0 of the resident model) through
+    tqf_hip_moe_layer_device at M = m with x ~ N(0, 1), plus (config 3) the
+    stochastic acceptance over the [4, V] logits; HIP-event kernel times and
+    the algorithmic bytes of the layer's own routes."""
+    from turboqwenfare_amd import _lib, mtp, synth
+
+    target, draft, dtok, u, ur, _ = inputs
+    x = synth.normal((m, H), seed=seed + 200 + m)
+    dx, dy = be.to_device(x), be.alloc(m * H * 4)
+    dids, dw = be.alloc(m * 8 * 2), be.alloc(m * 8 * 4)
+    acc = {k: be.to_device(v) for k, v in dict(t=target, d=draft, dt=dtok, u=u, ur=ur).items()}
+    d_acc, d_tok = be.alloc(4), be.alloc(4 * M)
+    layer = model.layers[0]
+
+    def call():
+        be.moe_layer_device(layer, dx, m, dy, dids, dw)
+        if with_accept:
+            be.accept_device(acc["t"], acc["d"], acc["dt"], K, V, TEMPERATURE, False, acc["u"],
+                             acc["ur"], d_acc, d_tok)
+
+    for _ in range(3):
+        call()
+    be.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        call()
+    be.synchronize()
+    wall_us = (time.perf_counter() - t0) / iters * 1e6
+    be.profile_enable(True)
+    for _ in range(iters):
+        call()
+    per = {}
+    for kind, nm in ((_lib.KERNEL_ROUTE, "route"), (_lib.KERNEL_GATE_UP, "gate_up"),
+                     (_lib.KERNEL_DOWN, "down"), (_lib.KERNEL_Q4K_MATVEC, "q4k_matvec"),
+                     (_lib.KERNEL_ACCEPT, "accept")):
+        n, ms, _ = be.profile_read(kind)
+        if n:
+            per[nm] = ms / iters * 1e3
+    be.profile_enable(False)
+    ids = be.read(dids, np.uint16, (m, 8))
+    union = len(mtp.routes_union(ids))
+    layer_bytes = (union + 1) * mtp.expert_bytes_q4_0() + (E + 1) * H * 4 + 2 * m * H * 4
+    accept_bytes = (2 * K + 1) * V * 4 if with_accept else 0
+    kernel_us = sum(per.values())
+    total = layer_bytes + accept_bytes
+    out = dict(m=m, expert_union=union, kernel_us=per, total_kernel_us=kernel_us,
+               wall_us_per_call=wall_us, layer_algorithmic_bytes=layer_bytes,
+               accept_algorithmic_bytes=accept_bytes, gbs=total / (kernel_us * 1e-6) / 1e9,
+               frac=total / (kernel_us * 1e-6) / 1e9 / HBM_PEAK_GBS)
+    for b in [dx, dy, dids, dw, d_acc, d_tok] + list(acc.values()):
+        be.free(b)
+    return out
+
+
+def kernel_source_digest() -> str:
+    """sha256 of the dominant kernel's sources: a committed traffic profile
+    counts for this build only when it was taken on the same sources."""
+    import hashlib
+
+    hsh = hashlib.sha256()
+    for f in ("tqf_stack.hip", "tqf_device.h", "tqf_internal.h"):
+        hsh.update((ROOT / "turboqwenfare_amd" / "csrc" / f).read_bytes())
+    return hsh.hexdigest()[:16]
+
+
+def committed_traffic(recipe: str):
+    """HBM bytes per stack launch from the committed rocprofv3 FETCH/WRITE
+    profile, if it was taken on these kernel sources and this workload."""
+    tfile = ROOT / "profiles" / "stack_verify_traffic.json"
+    if not tfile.exists():
+        return None, "no committed traffic profile"
+    t = json.loads(tfile.read_text())
+    if t.get("source_digest") != kernel_source_digest():
+        return None, "committed traffic profile was taken on other kernel sources"
+    if t.get("recipe") != recipe:
+        return None, f"committed traffic profile is for recipe {t.get('recipe')}"
+    return t.get("hbm_bytes_per_launch"), t.get("source", "")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -343,9 +520,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--layers", type=int, default=40)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--recipe", choices=("zero_mean", "uniform"), default="zero_mean",
+                    help="nibble recipe of the headline model's experts (zero_mean: q - 8 "
+                         "symmetric on [-7, 7]; uniform: the literal nibbles 0..15)")
     ap.add_argument("--greedy", action="store_true", help="greedy instead of stochastic acceptance")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--verify-only", action="store_true",
+                    help="only the headline verify step (the command its rocprofv3 profiles are "
+                         "taken with); prints the bench line without the other sections")
     ap.add_argument("--gemv-pool", type=int, default=2048,
                     help="distinct 512x2048 matrices in the config-1 GEMV bandwidth pool")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -355,6 +538,9 @@ def main():
                     help="only run the config-5 grouped expert GEMM on one resident layer "
                          "(the command its rocprofv3 profiles are taken with) and exit")
     ap.add_argument("--grouped-iters", type=int, default=20)
+    ap.add_argument("--layer-only", action="store_true",
+                    help="only configs 2 and 3 (one MoE layer at M = 1, and at M = 4 plus the "
+                         "acceptance) on a one-layer model, and exit")
     ap.add_argument("--lm-head-only", action="store_true",
                     help="only run the Q6_K LM head (the command its rocprofv3 profiles are "
                          "taken with) and exit")
@@ -364,40 +550,6 @@ def main():
                     help="only run the Q4_K config-1 GEMV pools (the command their rocprofv3 "
                          "profiles are taken with) and exit")
     args = ap.parse_args()
-    if args.q4k_verify_only:
-        from turboqwenfare_amd.backend import HipBackend
-
-        be = HipBackend(0)
-        r = q4k_verify_bench(be, args.layers, args.seed, verify_inputs(args.seed),
-                             steps=min(args.steps, 100))
-        log("bench: Q4_K verify step " + json.dumps(r))
-        be.close()
-        return
-    if args.lm_head_only:
-        from turboqwenfare_amd.backend import HipBackend
-
-        be = HipBackend(0)
-        log("bench: LM head " + json.dumps(lm_head_bench(be, args.seed)))
-        be.close()
-        return
-    if args.q4k_only:
-        from turboqwenfare_amd.backend import HipBackend
-
-        be = HipBackend(0)
-        log("bench: Q4_K config-1 pools " + json.dumps(q4k_pool_bench(be, args.gemv_pool,
-                                                                      args.seed)))
-        be.close()
-        return
-    if args.grouped_only:
-        from turboqwenfare_amd.backend import HipBackend
-
-        be = HipBackend(0)
-        layers, _, _ = build_model(be, 1, args.seed)
-        cases = ("zipf", "dense8") if args.grouped_only == "both" else (args.grouped_only,)
-        grouped = grouped_gemm_bench(be, layers[0], args.seed, args.grouped_iters, cases)
-        log("bench: config-5 grouped GEMM " + json.dumps(grouped))
-        be.close()
-        return
     if args.copy_calibration:
         import torch
 
@@ -416,117 +568,103 @@ def main():
               f"WORLD_SIZE {world}); multi-GPU sharding is design-only.", file=sys.stderr)
         sys.exit(2)
 
-    from turboqwenfare_amd import _lib, mtp
+    from turboqwenfare_amd import mtp
     from turboqwenfare_amd.backend import HipBackend
 
     be = HipBackend(0)
+    if args.q4k_verify_only:
+        r = q4k_verify_bench(be, args.layers, args.seed, verify_inputs(args.seed),
+                             steps=min(args.steps, 100))
+        log("bench: Q4_K verify step " + json.dumps(r))
+        be.close()
+        return
+    if args.lm_head_only:
+        log("bench: LM head " + json.dumps(lm_head_bench(be, args.seed)))
+        be.close()
+        return
+    if args.q4k_only:
+        log("bench: Q4_K config-1 pools " + json.dumps(q4k_pool_bench(be, args.gemv_pool,
+                                                                      args.seed)))
+        be.close()
+        return
+    if args.grouped_only or args.layer_only:
+        model = build_model(be, 1, args.seed, args.recipe)
+        if args.layer_only:
+            inputs = verify_inputs(args.seed)
+            for name, m, acc in (("config2_layer_m1", 1, False), ("config3_layer_m4_accept", M, True)):
+                log(f"bench: {name} " + json.dumps(layer_bench(be, model, inputs, m, acc, args.seed)))
+        else:
+            cases = ("zipf", "dense8") if args.grouped_only == "both" else (args.grouped_only,)
+            grouped = grouped_gemm_bench(be, model.layers[0], args.seed, args.grouped_iters, cases)
+            log("bench: config-5 grouped GEMM " + json.dumps(grouped))
+        be.close()
+        return
+
     name, cus = be.device_info()
     log(f"bench: device {name}, {cus} CUs")
     t0 = time.perf_counter()
-    layers, norms, host_f32 = build_model(be, args.layers, args.seed)
-    log(f"bench: model resident in {time.perf_counter() - t0:.1f} s")
-
+    model = build_model(be, args.layers, args.seed, args.recipe)
+    log(f"bench: {args.recipe} model resident in {time.perf_counter() - t0:.1f} s")
     inputs = verify_inputs(args.seed)
-    target, draft, dtok, u, ur, h0 = inputs
-    d = {k: be.to_device(v) for k, v in dict(t=target, d=draft, dt=dtok, u=u, ur=ur, h0=h0,
-                                              h=h0).items()}
-    d_acc, d_tok = be.alloc(4), be.alloc(4 * M)
-    st = be.prepare_stack(layers, norms)
+    head = verify_bench(be, model, inputs, args.steps, args.warmup, args.greedy)
+    steps_per_s = head["steps_per_s"]
+    log(f"bench: verify step {head['ms_per_step']:.3f} ms; mean expert union "
+        f"{head['expert_union']['mean']:.2f}")
+    log("bench: kernel profile " + json.dumps(head["kernels"]))
 
-    def step():
-        be.verify_step_device(st, d["h0"], d["h"], M, d["t"], None if args.greedy else d["d"],
-                              d["dt"], V, TEMPERATURE, args.greedy, d["u"], d["ur"], d_acc, d_tok)
+    extras = {}
+    if not args.verify_only:
+        inputs_layer = inputs
+        extras["config2_layer_m1"] = layer_bench(be, model, inputs_layer, 1, False, args.seed)
+        log("bench: config 2 " + json.dumps(extras["config2_layer_m1"]))
+        extras["config3_layer_m4_accept"] = layer_bench(be, model, inputs_layer, M, True, args.seed)
+        log("bench: config 3 " + json.dumps(extras["config3_layer_m4_accept"]))
+        extras["stack_m1"] = stack_m1_bench(be, model, args.seed)
+        log("bench: 40-layer stack at M=1 " + json.dumps(extras["stack_m1"]))
+        other = "uniform" if args.recipe == "zero_mean" else "zero_mean"
+        side = build_model(be, args.layers, args.seed, other)
+        r = verify_bench(be, side, inputs, min(args.steps, 50), 3, args.greedy, distribution=False)
+        side.free()
+        extras[f"{other}_recipe"] = {k: r[k] for k in ("steps_per_s", "ms_per_step", "expert_union",
+                                                       "stack_algorithmic_bytes")}
+        extras[f"{other}_recipe"]["stack_us"] = r["kernels"].get("stack", {}).get("avg_us")
+        log(f"bench: {other} recipe " + json.dumps(extras[f"{other}_recipe"]))
 
-    for _ in range(args.warmup):
-        step()
-    be.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    be.synchronize()
-    elapsed = time.perf_counter() - t0
-    steps_per_s = args.steps / elapsed
-    log(f"bench: verify step {elapsed / args.steps * 1e3:.3f} ms")
+        # Config-1 GEMV bandwidth: a rotating pool of distinct 512x2048
+        # matrices (far beyond the 256 MB Infinity Cache), one launch.
+        from turboqwenfare_amd import _lib, synth
 
-    # Step-time distribution: each step synchronised on its own (so each
-    # sample also holds one launch + synchronise round trip).
-    per_step = []
-    for _ in range(args.steps):
-        t0 = time.perf_counter()
-        step()
-        be.synchronize()
-        per_step.append((time.perf_counter() - t0) * 1e3)
-    q10, q50, q90 = (float(v) for v in np.percentile(per_step, [10, 50, 90]))
-    log(f"bench: synchronised step p10 {q10:.3f} / median {q50:.3f} / p90 {q90:.3f} ms")
-
-    # Kernel timing with HIP events on the library stream (eager launches).
-    be.profile_enable(True)
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    be.synchronize()
-    eager_ms = (time.perf_counter() - t0) / args.steps * 1e3
-    prof = {}
-    for kind, nm in ((_lib.KERNEL_STACK, "stack"), (_lib.KERNEL_ROUTE, "route"),
-                     (_lib.KERNEL_GATE_UP, "gate_up"), (_lib.KERNEL_DOWN, "down"),
-                     (_lib.KERNEL_ACCEPT, "accept")):
-        n, ms, by = be.profile_read(kind)
-        if n:
-            prof[nm] = dict(launches=n, avg_us=ms / n * 1e3, bytes_per_launch=by / n,
-                            gbs=by / (ms * 1e-3) / 1e9 if ms > 0 else 0.0)
-    be.profile_enable(False)
-
-    # Algorithmic HBM bytes of one stack pass: every layer's router (f32
-    # [E+1 x H] incl. the shared input gate), RMSNorm weight and the Q4_0
-    # bytes of its (union + shared) experts, from the routes of the same input.
-    d_ids = be.alloc(args.layers * M * 8 * 2)
-    d_tmp = be.alloc(M * H * 4)
-    be.stack_forward_device(st, d_tmp, M, d_ids, d_h_in=d["h0"])
-    ids = be.read(d_ids, np.uint16, (args.layers, M, 8))
-    unions = [len(mtp.routes_union(ids[l])) for l in range(args.layers)]
-    stack_bytes = sum((u + 1) * mtp.expert_bytes_q4_0() + (E + 1) * H * 4 + H * 4
-                      for u in unions) + 2 * M * H * 4
-    accept_bytes = (2 * K + 1) * V * 4
-    if "stack" in prof:
-        prof["stack"]["bytes_per_launch"] = stack_bytes
-        prof["stack"]["gbs"] = stack_bytes / (prof["stack"]["avg_us"] * 1e-6) / 1e9
-    if "accept" in prof:
-        prof["accept"]["bytes_per_launch"] = accept_bytes
-        prof["accept"]["gbs"] = accept_bytes / (prof["accept"]["avg_us"] * 1e-6) / 1e9
-    log(f"bench: mean expert union {np.mean(unions):.2f} (min {min(unions)}, max {max(unions)})")
-    log("bench: kernel profile " + json.dumps(prof))
-
-    # Config-1 GEMV bandwidth: a rotating pool of distinct 512x2048 matrices
-    # (far beyond the 256 MB Infinity Cache) against one x, one launch.
-    from turboqwenfare_amd import synth
-
-    pool = [be.synth_q4_0(512, 2048, 900_000 + i, args.seed) for i in range(args.gemv_pool)]
-    dx = be.to_device(synth.normal((2048,), seed=args.seed))
-    dy = be.alloc(args.gemv_pool * 512 * 4)
-    be.q4_gemv_batched_device(pool, dx, dy)
-    be.profile_enable(True)
-    for _ in range(10):
+        pool = [be.synth_q4_0(512, 2048, 900_000 + i, args.seed) for i in range(args.gemv_pool)]
+        dx = be.to_device(synth.normal((2048,), seed=args.seed))
+        dy = be.alloc(args.gemv_pool * 512 * 4)
         be.q4_gemv_batched_device(pool, dx, dy)
-    n, ms, by = be.profile_read(_lib.KERNEL_GEMV)
-    be.profile_enable(False)
-    gemv = dict(matrices=args.gemv_pool, bytes_per_launch=by / n, avg_us=ms / n * 1e3,
-                gbs=by / (ms * 1e-3) / 1e9)
-    gemv["frac"] = gemv["gbs"] / HBM_PEAK_GBS
-    for w in pool:
-        be.free_weights(w)
-    log("bench: config-1 GEMV pool " + json.dumps(gemv))
-    q4k = q4k_pool_bench(be, args.gemv_pool, args.seed)
-    log("bench: Q4_K config-1 pools " + json.dumps(q4k))
-    lm = lm_head_bench(be, args.seed)
-    log("bench: LM head " + json.dumps(lm))
-    grouped = grouped_gemm_bench(be, layers[0], args.seed)
-    log("bench: config-5 grouped GEMM " + json.dumps(grouped))
-    q4k_verify = q4k_verify_bench(be, args.layers, args.seed, inputs, steps=min(args.steps, 100))
-    log("bench: Q4_K verify step " + json.dumps(q4k_verify))
+        be.profile_enable(True)
+        for _ in range(10):
+            be.q4_gemv_batched_device(pool, dx, dy)
+        n, ms, by = be.profile_read(_lib.KERNEL_GEMV)
+        be.profile_enable(False)
+        gemv = dict(matrices=args.gemv_pool, bytes_per_launch=by / n, avg_us=ms / n * 1e3,
+                    gbs=by / (ms * 1e-3) / 1e9)
+        gemv["frac"] = gemv["gbs"] / HBM_PEAK_GBS
+        for w in pool:
+            be.free_weights(w)
+        be.free(dx)
+        be.free(dy)
+        extras["gemv_config1"] = gemv
+        log("bench: config-1 GEMV pool " + json.dumps(gemv))
+        extras["q4k_config1"] = q4k_pool_bench(be, args.gemv_pool, args.seed)
+        log("bench: Q4_K config-1 pools " + json.dumps(extras["q4k_config1"]))
+        extras["lm_head_q6k"] = lm_head_bench(be, args.seed)
+        log("bench: LM head " + json.dumps(extras["lm_head_q6k"]))
+        extras["grouped_gemm_config5"] = grouped_gemm_bench(be, model.layers[0], args.seed)
+        log("bench: config-5 grouped GEMM " + json.dumps(extras["grouped_gemm_config5"]))
+        extras["q4k_verify"] = q4k_verify_bench(be, args.layers, args.seed, inputs,
+                                                steps=min(args.steps, 100))
+        log("bench: Q4_K verify step " + json.dumps(extras["q4k_verify"]))
 
     cpu = None
-    if not args.no_cpu_baseline:
-        res, threads, n_sample = cpu_baseline(be, layers, host_f32, inputs, args.cpu_budget)
+    if not args.no_cpu_baseline and not args.verify_only:
+        res, threads, n_sample = cpu_baseline(model, inputs, args.cpu_budget)
         cpu = dict(value=res[threads], unit="verify steps/s", cores=threads, kind="port",
                    host_cpu=host_cpu_model(), host_nproc=os.cpu_count(),
                    sample=f"{n_sample} of {args.layers} MoE layers at M=4 plus one acceptance at "
@@ -534,12 +672,10 @@ def main():
                           f"-ffp-contract=off, OpenMP over output rows",
                    single_thread_value=res[1])
 
-    traffic = None
-    tfile = ROOT / "profiles" / "stack_verify_traffic.json"
-    if tfile.exists():
-        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
-
+    traffic, traffic_src = committed_traffic(args.recipe)
+    prof = head["kernels"]
     dom = prof.get("stack") or prof.get("gate_up")
+    acc_word = "greedy" if args.greedy else "stochastic"
     line = {
         "metric": "MTP k=3 verify steps/sec + Q4 expert GEMV HBM GB/s (% of peak), 1 GPU",
         "value": steps_per_s,
@@ -547,16 +683,16 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": elapsed / args.steps * 1e3,
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "q4_0 weights, fp32 activations, int8 dot4 + fp32 accumulate",
-        "data": "synthetic (seeded Philox Q4_0 experts, N(0,1) activations, N(0,9) logits)",
-        "config": {"workload": "config 4: full-depth MTP verify step, 40 MoE layers at M=4 "
-                               "(k=3) + stochastic acceptance" if not args.greedy else
-                               "config 4: full-depth MTP verify step, 40 MoE layers at M=4 "
-                               "(k=3) + greedy acceptance",
+        "data": f"synthetic (seeded Philox Q4_0 experts, nibble recipe {args.recipe}, N(0,1) "
+                f"activations, N(0,9) logits)",
+        "config": {"workload": f"config 4: full-depth MTP verify step, 40 MoE layers at M=4 (k=3) "
+                               f"+ {acc_word} acceptance",
+                   "expert_recipe": args.recipe,
                    "layers": args.layers, "hidden": H, "experts": E, "top_k": 8,
                    "expert_width": F, "vocab": V, "temperature": TEMPERATURE,
                    "resident_weight_gb": round(args.layers * (E + 1) * 3 * 589824 / 1e9, 2)},
@@ -564,24 +700,22 @@ def main():
                                    for a in (0.6, 0.8)},
         "roofline": {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": dom["gbs"] / HBM_PEAK_GBS, "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "kernel": "stack_kernel (persistent 40-layer MoE stack: router, union-expert "
                                "gate/up + SwiGLU, down + combine)",
-                     "avg_us": dom["avg_us"], "algorithmic_bytes_per_launch": dom["bytes_per_launch"]},
-        "expert_union": {"mean": float(np.mean(unions)), "min": int(min(unions)),
-                         "max": int(max(unions))},
+                     "avg_us": dom["avg_us"], "algorithmic_bytes_per_launch": dom["bytes_per_launch"],
+                     "source_digest": kernel_source_digest()},
+        "expert_union": head["expert_union"],
         "kernels": prof,
-        "gemv_config1": gemv,
-        "q4k_config1": q4k,
-        "lm_head_q6k": lm,
-        "grouped_gemm_config5": grouped,
-        "q4k_verify": q4k_verify,
-        "eager_profiled_ms_per_step": eager_ms,
-        "synchronised_step_ms": {"p10": q10, "median": q50, "p90": q90},
+        "eager_profiled_ms_per_step": head["eager_profiled_ms_per_step"],
+        "synchronised_step_ms": head.get("synchronised_step_ms"),
+        **extras,
         "cpu_baseline": cpu,
     }
     if cpu:
         line["speedup_vs_cpu"] = steps_per_s / cpu["value"]
     print(json.dumps(line), flush=True)
+    model.free()
     be.close()
 
 

@@ -327,14 +327,38 @@ int32_t tqf_hip_lm_head_logits_device(tqf_hip_ctx *ctx, const tqf_hip_weights *w
 
 /* ---- one MTP verify step: the stack over the k+1 verify rows, then the
  *      acceptance, as one stream-ordered (graph-replayed) unit.  The verify
- *      loop the reference leaves unwired (runtime/mtp.rs:1-20). ------------- */
+ *      loop the reference leaves unwired (runtime/mtp.rs:1-20).
+ *      d_status (device int32, may be null): the stack's device status, as
+ *      tqf_hip_stack_forward_device writes it -- TQF_HIP_ERR_ROUTER for a
+ *      non-finite router logit (RouterResult::from_logits, experts/mod.rs:
+ *      140-145), TQF_HIP_ERR_DEVICE for a timed-out grid barrier; never
+ *      cleared by the library, so the caller zeroes it and checks it after
+ *      the step.  A step that sets it has left d_h undefined; the acceptance,
+ *      which reads only the logits, still runs. ---------------------------- */
 int32_t tqf_hip_verify_step_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack,
                                    const float *d_h_in, float *d_h, uint32_t m,
                                    const float *d_target, const float *d_draft,
                                    const int32_t *d_draft_tokens, uint32_t vocab,
                                    float temperature, int32_t greedy, const float *d_u,
                                    const float *d_u_resample, int32_t *d_accepted,
-                                   int32_t *d_tokens_out);
+                                   int32_t *d_tokens_out, int32_t *d_status);
+
+/* ---- kernel variants: the counterpart of GpuKernelKind::from_env and
+ *      GpuExecutionState::kernel_kind (backend/metal/expert.rs:56-92).  Each
+ *      selector starts from the environment when the context is created
+ *      (TQF_HIP_PERSISTENT, TQF_HIP_Q4K_FOLD, TQF_HIP_GRAPHS: "0" selects 0,
+ *      anything else or unset 1) and is changed per context here; a change
+ *      drops the context's captured graphs, so no replay keeps an old
+ *      choice. ----------------------------------------------------------- */
+#define TQF_HIP_VARIANT_PERSISTENT 0 /* 1: the persistent stack kernel where it applies;
+                                        0: per-layer kernels (graph-replayed)          */
+#define TQF_HIP_VARIANT_Q4K_FOLD 1   /* 1: a Q4_K layer's combine folded into its down
+                                        launch; 0: the separate combine launch          */
+#define TQF_HIP_VARIANT_GRAPHS 2     /* 1: multi-launch paths replay HIP graphs;
+                                        0: eager launches of the same kernels           */
+#define TQF_HIP_VARIANTS 3
+int32_t tqf_hip_set_variant(tqf_hip_ctx *ctx, int32_t variant, int32_t value);
+int32_t tqf_hip_get_variant(tqf_hip_ctx *ctx, int32_t variant, int32_t *value);
 
 /* ---- profiling: the HIP counterpart of backend/metal/timing.rs:23-80 ----- */
 #define TQF_HIP_KERNEL_ROUTE 0    /* rmsnorm + router + top-8 + union plan    */

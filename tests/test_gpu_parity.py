@@ -7,7 +7,7 @@ import pytest
 
 import cpu_oracle as orc
 from conftest import rel_err
-from turboqwenfare_amd import mtp, synth
+from turboqwenfare_amd import _lib, mtp, synth
 from turboqwenfare_amd._lib import ERR_INVALID, ERR_ROUTER, HipError
 
 pytestmark = pytest.mark.gpu
@@ -43,8 +43,13 @@ def test_device_synth_matches_host_generator(backend):
     assert np.array_equal(backend.download_q4_0(w), synth.q4_0_synthetic(512, 2048, 7, 3))
     w2 = backend.synth_q4_0(2048, 512, 123456, 0)
     assert np.array_equal(backend.download_q4_0(w2), synth.q4_0_synthetic(2048, 512, 123456, 0))
-    backend.free_weights(w)
-    backend.free_weights(w2)
+    w3 = backend.synth_q4_0(512, 2048, 7, 3, "zero_mean")
+    assert np.array_equal(backend.download_q4_0(w3), synth.q4_0_synthetic(512, 2048, 7, 3, "zero_mean"))
+    for w_ in (w, w2, w3):
+        backend.free_weights(w_)
+    with pytest.raises(HipError) as e:
+        backend.synth_q4_0(64, 64, 1, 1, 2)
+    assert e.value.status == ERR_INVALID
 
 
 def test_upload_rejects_bad_shapes(backend):
@@ -371,11 +376,7 @@ def test_small_geometry_layer_matches_committed_golden(backend):
 
 # ---- the persistent whole-stack kernel ----------------------------------------
 def _stack_run(backend, st, h0, m, n_layers, persistent, with_w=False):
-    import os
-
-    old = os.environ.get("TQF_HIP_PERSISTENT")
-    os.environ["TQF_HIP_PERSISTENT"] = "1" if persistent else "0"
-    try:
+    with backend.variant(_lib.VARIANT_PERSISTENT, persistent):
         dh = backend.to_device(h0[:m])
         dids = backend.alloc(n_layers * m * 8 * 2)
         dw = backend.alloc(n_layers * m * 8 * 4)
@@ -386,11 +387,6 @@ def _stack_run(backend, st, h0, m, n_layers, persistent, with_w=False):
         for b in (dh, dids, dw, dst):
             backend.free(b)
         return out
-    finally:
-        if old is None:
-            del os.environ["TQF_HIP_PERSISTENT"]
-        else:
-            os.environ["TQF_HIP_PERSISTENT"] = old
 
 
 @pytest.mark.parametrize("m", [1, 2, 3, 4])
@@ -425,3 +421,32 @@ def test_persistent_stack_reports_router_error(backend, stack3):
     h0[2, 100] = np.inf
     _, _, _, status = _stack_run(backend, st, h0, 4, 3, True)
     assert status == ERR_ROUTER
+
+
+@pytest.mark.parametrize("persistent", [True, False], ids=["persistent", "per_layer"])
+def test_verify_step_reports_router_error(backend, stack3, persistent):
+    """A non-finite router logit inside the verify step reaches its d_status
+    (TQF_HIP_ERR_ROUTER); the acceptance, which reads only the logits, still
+    returns the oracle's decision, and a clean step afterwards reports 0."""
+    _, _, st = stack3
+    vocab, k = 4096, 3
+    rng = np.random.default_rng(21)
+    target = (rng.standard_normal((k + 1, vocab)) * 3).astype(np.float32)
+    dtok = np.argmax(target[:k], axis=1).astype(np.int32)
+    want = orc.accept(target, None, dtok, 0.7, True)
+    h_bad = synth.normal((4, 2048), seed=413)
+    h_bad[1, 7] = np.nan
+    with backend.variant(_lib.VARIANT_PERSISTENT, persistent):
+        for h0, expect in ((h_bad, ERR_ROUTER), (synth.normal((4, 2048), seed=414), 0)):
+            dh0, dh = backend.to_device(h0), backend.alloc(4 * 2048 * 4)
+            dt, ddt = backend.to_device(target), backend.to_device(dtok)
+            acc, toks = backend.alloc(4), backend.alloc(4 * (k + 1))
+            dst = backend.to_device(np.zeros(1, np.int32))
+            backend.verify_step_device(st, dh0, dh, 4, dt, None, ddt, vocab, 0.7, True, None, None,
+                                       acc, toks, dst)
+            assert int(backend.read(dst, np.int32, (1,))[0]) == expect
+            a = int(backend.read(acc, np.int32, (1,))[0])
+            tk = backend.read(toks, np.int32, (k + 1,))
+            assert (a, [int(v) for v in tk[: a + 1]]) == want
+            for b in (dh0, dh, dt, ddt, acc, toks, dst):
+                backend.free(b)

@@ -16,7 +16,7 @@ import pytest
 
 import cpu_oracle as orc
 from conftest import rel_err
-from turboqwenfare_amd import synth
+from turboqwenfare_amd import _lib, synth
 from turboqwenfare_amd.synth import centered_q4_k
 from turboqwenfare_amd._lib import ERR_INVALID, ERR_ROUTER, HipError
 
@@ -251,27 +251,20 @@ def test_q4k_verify_step_graph_replays_match_eager(backend, q4k_stack):
 def test_q4k_folded_combine_equals_the_combine_launch(backend, q4k_stack):
     """The down launch's folded combine and q4k_moe_combine_kernel run the same
     arithmetic in the same order: a layer and a 2-layer stack give the same
-    bits with the fold switched off (TQF_HIP_Q4K_FOLD=0, read per call)."""
-    import os
-
+    bits with the fold switched off (variant TQF_HIP_VARIANT_Q4K_FOLD = 0),
+    graph-replayed (a variant change drops the captured graphs)."""
     layers, norms, st = q4k_stack
     x = synth.normal((4, H), seed=808)
     outs = []
-    old = os.environ.get("TQF_HIP_Q4K_FOLD")
-    try:
-        for fold in ("1", "0"):
-            os.environ["TQF_HIP_Q4K_FOLD"] = fold
+    for fold in (True, False, True):
+        with backend.variant(_lib.VARIANT_Q4K_FOLD, fold):
             y, _, _ = backend.moe_forward_batch(layers[0].dev, x)
             dh = backend.to_device(x)
-            backend.profile_enable(True)  # eager launches: a graph keeps its first capture
-            backend.stack_forward_device(st, dh, 4)
-            backend.profile_enable(False)
+            for _ in range(2):  # capture, then replay
+                backend.write(dh, x)
+                backend.stack_forward_device(st, dh, 4)
             outs.append((y, backend.read(dh, np.float32, (4, H))))
             backend.free(dh)
-    finally:
-        if old is None:
-            del os.environ["TQF_HIP_Q4K_FOLD"]
-        else:
-            os.environ["TQF_HIP_Q4K_FOLD"] = old
-    for a, b in zip(outs[0], outs[1]):
-        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    for other in outs[1:]:
+        for a, b in zip(outs[0], other):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

@@ -153,3 +153,39 @@ def test_bf16_round_nearest_even_kats():
     r = synth.bf16_to_f32(synth.bf16_round(x))
     assert np.all(np.abs(r - x) <= np.abs(x) * 2.0 ** -8)  # half an ulp of 8 significant bits
     assert np.array_equal(synth.bf16_to_f32(synth.bf16_round(r)), r)
+
+
+def test_zero_mean_recipe_maps_only_nibble_zero():
+    """Every nibble value at every position of a word: 0 -> 8, 1..15 kept,
+    the other nibbles of the word untouched."""
+    from turboqwenfare_amd import synth
+
+    words = []
+    for pos in range(8):
+        for v in range(16):
+            for fill in (0x0, 0xF, 0x5):
+                w = 0
+                for j in range(8):
+                    w |= (v if j == pos else fill) << (4 * j)
+                words.append(w)
+    words = np.array(words, dtype=np.uint32)
+    out = synth.zero_mean_nibbles(words)
+    for w, o in zip(words.tolist(), out.tolist()):
+        for j in range(8):
+            n, m = (w >> (4 * j)) & 15, (o >> (4 * j)) & 15
+            assert m == (8 if n == 0 else n)
+
+
+def test_zero_mean_recipe_is_symmetric_and_keeps_scales():
+    from turboqwenfare_amd import synth
+
+    a = synth.q4_0_synthetic(64, 2048, 5, 1).reshape(-1, 18)
+    b = synth.q4_0_synthetic(64, 2048, 5, 1, "zero_mean").reshape(-1, 18)
+    assert np.array_equal(a[:, :2], b[:, :2])  # the same binary16 scales
+    q = np.concatenate([b[:, 2:] & 15, b[:, 2:] >> 4]).astype(np.int64) - 8
+    assert q.min() == -7 and q.max() == 7
+    assert abs(q.mean()) < 0.01
+    q0 = np.concatenate([a[:, 2:] & 15, a[:, 2:] >> 4]).astype(np.int64) - 8
+    assert abs(q0.mean() + 0.5) < 0.01
+    with pytest.raises(ValueError):
+        synth.q4_0_synthetic(1, 32, 1, 1, 7)

@@ -32,6 +32,9 @@ KERNEL_Q4K_GEMV = 9
 KERNEL_Q4K_MATVEC = 10
 KERNEL_Q6K_MATVEC = 11
 KERNEL_KINDS = 12
+VARIANT_PERSISTENT = 0
+VARIANT_Q4K_FOLD = 1
+VARIANT_GRAPHS = 2
 FORMAT_Q4_0 = 0
 FORMAT_Q4_K = 1
 FORMAT_Q6_K = 2
@@ -122,11 +125,15 @@ SIGNATURES = {
     "tqf_hip_grouped_gemm": (_i32, [_vp, _vp, _vp, _u32, _vp, _vp, _vp]),
     "tqf_hip_grouped_gemm_device": (_i32, [_vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp]),
     "tqf_hip_verify_step_device": (
-        _i32, [_vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _u32, _f32, _i32, _vp, _vp, _vp, _vp]),
+        _i32, [_vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _u32, _f32, _i32, _vp, _vp, _vp, _vp,
+               _vp]),
+    "tqf_hip_set_variant": (_i32, [_vp, _i32, _i32]),
+    "tqf_hip_get_variant": (_i32, [_vp, _i32, C.POINTER(_i32)]),
     "tqf_hip_profile_enable": (_i32, [_vp, _i32]),
     "tqf_hip_profile_read": (_i32, [_vp, _i32, C.POINTER(_u64), C.POINTER(C.c_double),
                                     C.POINTER(C.c_double)]),
     "tqf_hip_weights_synth": (_i32, [_vp, _u32, _u32, _u32, _u32, _pp]),
+    "tqf_hip_weights_synth_recipe": (_i32, [_vp, _u32, _u32, _u32, _u32, _u32, _pp]),
 }
 
 _LIB = None

@@ -18,6 +18,7 @@ GPU through the library; there is no CPU path here.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes as C
 from dataclasses import dataclass
 from typing import Sequence
@@ -162,10 +163,16 @@ class HipBackend:
                                                     C.byref(h)))
         return Q4Weights(h.value, rows, cols)
 
-    def synth_q4_0(self, rows: int, cols: int, tensor_id: int, seed: int) -> Q4Weights:
+    def synth_q4_0(self, rows: int, cols: int, tensor_id: int, seed: int,
+                   recipe: int | str = 0) -> Q4Weights:
+        """Seeded synthetic Q4_0 matrix generated in HBM; ``recipe`` "uniform"
+        (0) or "zero_mean" (1), as ``synth.q4_0_synthetic``."""
+        from . import synth
+
+        r = synth.RECIPES.get(recipe, recipe) if isinstance(recipe, str) else int(recipe)
         h = C.c_void_p()
-        self._check(self.lib.tqf_hip_weights_synth(self.ctx, rows, cols, tensor_id, seed,
-                                                   C.byref(h)))
+        self._check(self.lib.tqf_hip_weights_synth_recipe(self.ctx, rows, cols, tensor_id, seed,
+                                                          r, C.byref(h)))
         return Q4Weights(h.value, rows, cols)
 
     def download_q4_0(self, w: Q4Weights) -> np.ndarray:
@@ -465,12 +472,16 @@ class HipBackend:
                            m: int, d_target: DeviceBuffer, d_draft: DeviceBuffer | None,
                            d_dtok: DeviceBuffer, vocab: int, temperature: float, greedy: bool,
                            d_u: DeviceBuffer | None, d_ures: DeviceBuffer | None,
-                           d_accepted: DeviceBuffer, d_tokens: DeviceBuffer) -> None:
+                           d_accepted: DeviceBuffer, d_tokens: DeviceBuffer,
+                           d_status: DeviceBuffer | None = None) -> None:
+        """One verify step: h <- stack(h_in), then the acceptance.  d_status
+        (device int32, caller-zeroed) receives the stack's device status."""
         self._check(self.lib.tqf_hip_verify_step_device(
             self.ctx, st.handle, d_h_in.ptr if d_h_in else None, d_h.ptr, m, d_target.ptr,
             d_draft.ptr if d_draft else None,
             d_dtok.ptr, vocab, temperature, 1 if greedy else 0, d_u.ptr if d_u else None,
-            d_ures.ptr if d_ures else None, d_accepted.ptr, d_tokens.ptr))
+            d_ures.ptr if d_ures else None, d_accepted.ptr, d_tokens.ptr,
+            d_status.ptr if d_status else None))
 
     # ---- acceptance ------------------------------------------------------------------
     def accept(self, target: np.ndarray, draft: np.ndarray | None, draft_tokens: Sequence[int],
@@ -516,6 +527,25 @@ class HipBackend:
         self._check(self.lib.tqf_hip_top_logit_candidates(self.ctx, _ptr(lg2), rows, vocab,
                                                           _ptr(toks), _ptr(vals)))
         return (toks[0], vals[0]) if squeeze else (toks, vals)
+
+    # ---- kernel variants (GpuKernelKind) ------------------------------------------------
+    def set_variant(self, variant: int, value: bool) -> None:
+        self._check(self.lib.tqf_hip_set_variant(self.ctx, variant, 1 if value else 0))
+
+    def get_variant(self, variant: int) -> bool:
+        v = C.c_int32()
+        self._check(self.lib.tqf_hip_get_variant(self.ctx, variant, C.byref(v)))
+        return bool(v.value)
+
+    @contextlib.contextmanager
+    def variant(self, variant: int, value: bool):
+        """Selects a kernel variant for the duration of a with-block."""
+        old = self.get_variant(variant)
+        self.set_variant(variant, value)
+        try:
+            yield
+        finally:
+            self.set_variant(variant, old)
 
     # ---- profiling ---------------------------------------------------------------------
     def profile_enable(self, enable: bool = True) -> None:

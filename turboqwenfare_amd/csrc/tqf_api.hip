@@ -379,8 +379,7 @@ int32_t enqueue_layer_q4k(tqf_hip_ctx *ctx, const LayerDev &L, const float *h, c
     }
     // the combine folded into the down launch; TQF_HIP_Q4K_FOLD=0 in the
     // environment keeps the separate combine launch (the same arithmetic)
-    const char *fold_env = std::getenv("TQF_HIP_Q4K_FOLD");
-    const bool fold = !(fold_env && fold_env[0] == '0') && q4k_fold_ok(dd);
+    const bool fold = ctx->variant[TQF_HIP_VARIANT_Q4K_FOLD] != 0 && q4k_fold_ok(dd);
     {
         Prof p(ctx);
         e = fold ? launch_q4k_q8k_slots(ctx->stream, sc.plan, S, true, dd, nullptr, b.dn, b.gu, out, resid,
@@ -426,8 +425,7 @@ int32_t enqueue_stack(tqf_hip_ctx *ctx, const tqf_hip_stack *st, const float *d_
 // The persistent path: model geometry, m <= kStackMT, a device that can
 // co-schedule one workgroup per CU.
 bool stack_persistent_ok(tqf_hip_ctx *ctx, const tqf_hip_stack *st, uint32_t m) {
-    if (std::getenv("TQF_HIP_PERSISTENT") && std::string(std::getenv("TQF_HIP_PERSISTENT")) == "0")
-        return false;
+    if (!ctx->variant[TQF_HIP_VARIANT_PERSISTENT]) return false;
     if (st->format != TQF_HIP_FORMAT_Q4_0) return false;  // the persistent kernel reads Q4_0
     if (!st->d_layers || m > (uint32_t)kStackMT || st->hidden != (uint32_t)kStackHidden ||
         st->experts == 0 || st->experts > 256 || st->width % 256 || st->width > 2048)
@@ -484,23 +482,17 @@ int32_t enqueue_accept(tqf_hip_ctx *ctx, const float *t, const float *d, const i
 }
 
 // Runs `enqueue` eagerly, or captures it once per key into a HIP graph and
-// replays it.  Profiling forces eager execution so events bracket kernels.
-// TQF_HIP_GRAPHS=0 in the environment disables capture (eager launches of
-// the same kernels), e.g. under tracing tools that do not follow graphs.
-bool graphs_enabled() {
-    static const bool on = [] {
-        const char *v = std::getenv("TQF_HIP_GRAPHS");
-        return !(v && v[0] == '0');
-    }();
-    return on;
-}
-
+// replays it.  Profiling forces eager execution so events bracket kernels;
+// variant TQF_HIP_VARIANT_GRAPHS = 0 disables capture (eager launches of the
+// same kernels), e.g. under tracing tools that do not follow graphs.
 template <typename F>
 int32_t run_graphed(tqf_hip_ctx *ctx, const std::vector<uint64_t> &key, F enqueue) {
-    if (ctx->profiling || !graphs_enabled()) return enqueue();
+    if (ctx->profiling || !ctx->variant[TQF_HIP_VARIANT_GRAPHS]) return enqueue();
     GraphEntry *g = find_graph(ctx, key);
     if (!g) {
         if (ctx->graphs.size() >= kMaxGraphs) {
+            // the evicted graph may still be executing on the stream
+            TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
             GraphEntry *old = ctx->graphs.front();
             (void)hipGraphExecDestroy(old->exec);
             (void)hipGraphDestroy(old->graph);
@@ -567,7 +559,32 @@ extern "C" int32_t tqf_hip_create(int32_t device, tqf_hip_ctx **out) {
     }
     ctx->d_adhoc_mats = reinterpret_cast<const uint8_t **>(p);
     ctx->d_adhoc_plan = reinterpret_cast<Plan *>(p + align_up(3 * sizeof(void *), kAlign));
+    static const char *const kVariantEnv[TQF_HIP_VARIANTS] = {"TQF_HIP_PERSISTENT", "TQF_HIP_Q4K_FOLD",
+                                                              "TQF_HIP_GRAPHS"};
+    for (int i = 0; i < TQF_HIP_VARIANTS; ++i) {
+        const char *v = std::getenv(kVariantEnv[i]);
+        ctx->variant[i] = (v && v[0] == '0') ? 0 : 1;
+    }
     *out = ctx;
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_set_variant(tqf_hip_ctx *ctx, int32_t variant, int32_t value) {
+    TQF_ENTER(ctx);
+    if (variant < 0 || variant >= TQF_HIP_VARIANTS || (value != 0 && value != 1))
+        return fail(ctx, TQF_HIP_ERR_INVALID, "unknown variant or value");
+    if (ctx->variant[variant] == value) return TQF_HIP_OK;
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    drop_graphs(ctx);
+    ctx->variant[variant] = value;
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_get_variant(tqf_hip_ctx *ctx, int32_t variant, int32_t *value) {
+    TQF_ENTER(ctx);
+    if (variant < 0 || variant >= TQF_HIP_VARIANTS || !value)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "unknown variant or null pointer");
+    *value = ctx->variant[variant];
     return TQF_HIP_OK;
 }
 
@@ -763,16 +780,19 @@ extern "C" int32_t tqf_hip_weights_upload_device(tqf_hip_ctx *ctx, const void *d
     return TQF_HIP_OK;
 }
 
-extern "C" int32_t tqf_hip_weights_synth(tqf_hip_ctx *ctx, uint32_t rows, uint32_t cols,
-                                         uint32_t tensor_id, uint32_t seed, tqf_hip_weights **out) {
+extern "C" int32_t tqf_hip_weights_synth_recipe(tqf_hip_ctx *ctx, uint32_t rows, uint32_t cols,
+                                                uint32_t tensor_id, uint32_t seed, uint32_t recipe,
+                                                tqf_hip_weights **out) {
     TQF_ENTER(ctx);
     if (!out) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
     *out = nullptr;
     if (rows == 0 || cols == 0 || cols % 32)
         return fail(ctx, TQF_HIP_ERR_INVALID, "Q4_0 matrix needs cols a positive multiple of 32");
+    if (recipe != TQF_HIP_SYNTH_UNIFORM && recipe != TQF_HIP_SYNTH_ZERO_MEAN)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "unknown synthetic recipe");
     tqf_hip_weights *w = nullptr;
     if (int32_t rc = weights_alloc(ctx, rows, cols, &w)) return rc;
-    hipError_t e = launch_synth_q4_0(ctx->stream, w->dims, tensor_id, seed, w->tiles);
+    hipError_t e = launch_synth_q4_0(ctx->stream, w->dims, tensor_id, seed, recipe, w->tiles);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) {
         weights_release(ctx, w);
@@ -780,6 +800,11 @@ extern "C" int32_t tqf_hip_weights_synth(tqf_hip_ctx *ctx, uint32_t rows, uint32
     }
     *out = w;
     return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_weights_synth(tqf_hip_ctx *ctx, uint32_t rows, uint32_t cols,
+                                         uint32_t tensor_id, uint32_t seed, tqf_hip_weights **out) {
+    return tqf_hip_weights_synth_recipe(ctx, rows, cols, tensor_id, seed, TQF_HIP_SYNTH_UNIFORM, out);
 }
 
 extern "C" int32_t tqf_hip_weights_download(tqf_hip_ctx *ctx, const tqf_hip_weights *w,
@@ -1842,7 +1867,8 @@ extern "C" int32_t tqf_hip_verify_step_device(tqf_hip_ctx *ctx, const tqf_hip_st
                                               const float *d_draft, const int32_t *d_dtok,
                                               uint32_t vocab, float temperature, int32_t greedy,
                                               const float *d_u, const float *d_ures,
-                                              int32_t *d_accepted, int32_t *d_tokens) {
+                                              int32_t *d_accepted, int32_t *d_tokens,
+                                              int32_t *d_status) {
     TQF_ENTER(ctx);
     if (!stack || !d_h || !d_target || !d_accepted || !d_tokens)
         return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
@@ -1854,7 +1880,7 @@ extern "C" int32_t tqf_hip_verify_step_device(tqf_hip_ctx *ctx, const tqf_hip_st
         return rc;
     if (int32_t rc = ensure_accept_scratch(ctx, accept_scratch_bytes(k, vocab))) return rc;
     if (stack_persistent_ok(ctx, stack, m)) {
-        if (int32_t rc = enqueue_stack_persistent(ctx, stack, d_h_in, d_h, m, nullptr, nullptr, nullptr))
+        if (int32_t rc = enqueue_stack_persistent(ctx, stack, d_h_in, d_h, m, nullptr, nullptr, d_status))
             return rc;
         return enqueue_accept(ctx, d_target, d_draft, d_dtok, k, vocab, temperature, greedy, d_u,
                               d_ures, d_accepted, d_tokens);
@@ -1864,9 +1890,10 @@ extern "C" int32_t tqf_hip_verify_step_device(tqf_hip_ctx *ctx, const tqf_hip_st
     std::memcpy(&tbits, &temperature, 4);
     std::vector<uint64_t> key = {2,          k64(stack), k64(d_h_in), k64(d_h), m, k64(d_target),
                                  k64(d_draft), k64(d_dtok), vocab,     tbits,       (uint64_t)greedy,
-                                 k64(d_u),   k64(d_ures), k64(d_accepted), k64(d_tokens)};
+                                 k64(d_u),   k64(d_ures), k64(d_accepted), k64(d_tokens),
+                                 k64(d_status)};
     return run_graphed(ctx, key, [&]() {
-        if (int32_t rc = enqueue_stack(ctx, stack, d_h_in, d_h, m, nullptr, nullptr, nullptr)) return rc;
+        if (int32_t rc = enqueue_stack(ctx, stack, d_h_in, d_h, m, nullptr, nullptr, d_status)) return rc;
         return enqueue_accept(ctx, d_target, d_draft, d_dtok, k, vocab, temperature, greedy, d_u,
                               d_ures, d_accepted, d_tokens);
     });

@@ -378,6 +378,9 @@ struct tqf_hip_ctx {
     // grouped expert GEMM scratch
     void *d_grouped = nullptr;
     size_t grouped_bytes = 0;
+    // kernel variant selectors (TQF_HIP_VARIANT_*), from the environment at
+    // creation, changed by tqf_hip_set_variant
+    int32_t variant[TQF_HIP_VARIANTS] = {1, 1, 1};
 };
 
 namespace tqf {
@@ -398,7 +401,7 @@ inline size_t counter_count(uint32_t hidden) {
 hipError_t launch_repack(hipStream_t s, const uint8_t *d_aos, const MatrixDims &d,
                          uint8_t *tiles);
 hipError_t launch_synth_q4_0(hipStream_t s, const MatrixDims &d, uint32_t tensor_id,
-                             uint32_t seed, uint8_t *tiles);
+                             uint32_t seed, uint32_t recipe, uint8_t *tiles);
 hipError_t launch_prep(hipStream_t s, const float *x, uint32_t m, uint32_t cols,
                        uint32_t blocks_padded, uint32_t *xprep);
 hipError_t launch_gemv(hipStream_t s, const uint8_t *const *d_tiles, uint32_t count,

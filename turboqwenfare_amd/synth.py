@@ -35,14 +35,40 @@ def philox4x32_10(ctr: np.ndarray, key: tuple[int, int]) -> np.ndarray:
     return np.stack([c0, c1, c2, c3], axis=1).astype(np.uint32)
 
 
-def q4_0_synthetic(rows: int, cols: int, tensor_id: int, seed: int) -> np.ndarray:
+RECIPE_UNIFORM = 0
+RECIPE_ZERO_MEAN = 1
+RECIPES = {"uniform": RECIPE_UNIFORM, "zero_mean": RECIPE_ZERO_MEAN}
+
+
+def zero_mean_nibbles(words: np.ndarray) -> np.ndarray:
+    """Every nibble 0 of the uint32 ``words`` becomes 8, so that q - 8 is
+    symmetric on [-7, 7] (mean 0) instead of uniform on [-8, 7] (mean -0.5).
+    Bit 4j of t is the OR of nibble j's four bits; no bit of another nibble
+    reaches it."""
+    w = np.asarray(words, dtype=np.uint32)
+    t = w | (w >> np.uint32(1))
+    t = t | (t >> np.uint32(2))
+    z = ~t & np.uint32(0x11111111)
+    return w | (z << np.uint32(3))
+
+
+def q4_0_synthetic(rows: int, cols: int, tensor_id: int, seed: int,
+                   recipe: int | str = RECIPE_UNIFORM) -> np.ndarray:
     """GGML Q4_0 bytes [rows * cols/32 * 18] of (tensor_id, seed).
 
     Block b (row-major): Philox(ctr=(b_lo, b_hi, 0, 0)) gives the 16 nibble
     bytes (little-endian words); Philox(ctr=(b_lo, b_hi, 1, 0)) word 0 gives
     u = (w >> 8) 2^-24 and the scale d = 0.005 + 0.015 u (binary32, no fused
     multiply-add), stored as binary16 rounded to nearest even.
+
+    ``recipe`` "uniform" (0) keeps the nibbles uniform on 0..15, the literal
+    configuration text, whose weights carry E[q - 8] = -0.5 and so a common
+    rank-one component in every matrix; "zero_mean" (1) maps nibble 0 to 8
+    (``zero_mean_nibbles``), still packed Q4_0 with zero-point 8.
     """
+    recipe = RECIPES.get(recipe, recipe) if isinstance(recipe, str) else int(recipe)
+    if recipe not in (RECIPE_UNIFORM, RECIPE_ZERO_MEAN):
+        raise ValueError(f"unknown recipe {recipe}")
     if cols % 32:
         raise ValueError("cols must be a multiple of 32")
     n = rows * (cols // 32)
@@ -51,6 +77,8 @@ def q4_0_synthetic(rows: int, cols: int, tensor_id: int, seed: int) -> np.ndarra
     hi = (idx >> np.uint64(32)).astype(np.uint32)
     zeros = np.zeros(n, dtype=np.uint32)
     q = philox4x32_10(np.stack([lo, hi, zeros, zeros], axis=1), (tensor_id, seed))
+    if recipe == RECIPE_ZERO_MEAN:
+        q = zero_mean_nibbles(q)
     s = philox4x32_10(np.stack([lo, hi, np.ones(n, dtype=np.uint32), zeros], axis=1),
                       (tensor_id, seed))
     u = (s[:, 0] >> np.uint32(8)).astype(np.float32) * np.float32(2.0 ** -24)
