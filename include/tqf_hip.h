@@ -207,6 +207,23 @@ int32_t tqf_hip_accept_device(tqf_hip_ctx *ctx, const float *d_target, const flo
                               float temperature, int32_t greedy, const float *d_u,
                               const float *d_u_resample, int32_t *d_accepted,
                               int32_t *d_tokens_out);
+/* tqf_hip_accept_device without any allocation: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * same kernels and results as tqf_hip_accept_device, with their scratch in a
+ * fixed per-GPU array of 256 KiB (held until the process ends) instead of a
+ * context allocation: k and vocab whose scratch exceeds it (vocab above about
+ * 3.4 million at k = 7) are TQF_HIP_ERR_INVALID.  Every call on one GPU
+ * shares that array, so calls that overlap on one GPU (from two contexts or
+ * two streams) race; calls ordered on one stream do not.  The entry point
+ * calls no hipMalloc, hipFree or other allocating routine, and records no
+ * profiling events. */
+int32_t tqf_hip_accept_device_noalloc(tqf_hip_ctx *ctx, const float *d_target,
+                                      const float *d_draft, const int32_t *d_draft_tokens,
+                                      uint32_t k, uint32_t vocab, float temperature,
+                                      int32_t greedy, const float *d_u,
+                                      const float *d_u_resample, int32_t *d_accepted,
+                                      int32_t *d_tokens_out);
 /* top_logit_candidates (runtime/decode.rs:48-64) over `rows` rows of vocab
  * logits: tokens4/logits4 are [rows x 4]. */
 int32_t tqf_hip_top_logit_candidates(tqf_hip_ctx *ctx, const float *logits, uint32_t rows,

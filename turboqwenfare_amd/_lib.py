@@ -121,6 +121,8 @@ SIGNATURES = {
     "tqf_hip_stack_forward_device": (_i32, [_vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp]),
     "tqf_hip_accept": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _f32, _i32, _vp, _vp, _vp, _vp]),
     "tqf_hip_accept_device": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _f32, _i32, _vp, _vp, _vp, _vp]),
+    "tqf_hip_accept_device_noalloc": (
+        _i32, [_vp, _vp, _vp, _vp, _u32, _u32, _f32, _i32, _vp, _vp, _vp, _vp]),
     "tqf_hip_top_logit_candidates": (_i32, [_vp, _vp, _u32, _u32, _vp, _vp]),
     "tqf_hip_grouped_gemm": (_i32, [_vp, _vp, _vp, _u32, _vp, _vp, _vp]),
     "tqf_hip_grouped_gemm_device": (_i32, [_vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp]),

@@ -516,6 +516,17 @@ class HipBackend:
             float(temperature), 1 if greedy else 0, d_u.ptr if d_u else None,
             d_ures.ptr if d_ures else None, d_accepted.ptr, d_tokens.ptr))
 
+    def accept_device_noalloc(self, d_target: DeviceBuffer, d_draft: DeviceBuffer | None,
+                              d_dtok: DeviceBuffer | None, k: int, vocab: int, temperature: float,
+                              greedy: bool, d_u: DeviceBuffer | None, d_ures: DeviceBuffer | None,
+                              d_accepted: DeviceBuffer, d_tokens: DeviceBuffer) -> None:
+        """accept_device on the library's fixed per-GPU scratch (no allocation)."""
+        self._check(self.lib.tqf_hip_accept_device_noalloc(
+            self.ctx, d_target.ptr, d_draft.ptr if d_draft else None,
+            d_dtok.ptr if d_dtok else None, k, vocab, float(temperature), 1 if greedy else 0,
+            d_u.ptr if d_u else None, d_ures.ptr if d_ures else None, d_accepted.ptr,
+            d_tokens.ptr))
+
     def top_logit_candidates(self, logits: np.ndarray):
         """[V] or [rows, V] logits -> (tokens [rows, 4] u32, logits [rows, 4])."""
         lg = np.ascontiguousarray(logits, dtype=np.float32)

@@ -6,6 +6,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -22,6 +23,37 @@ struct GraphEntry {
     hipGraphExec_t exec = nullptr;
 };
 }  // namespace tqf
+
+// ---- allocation-free acceptance scratch -----------------------------------
+// tqf_hip_accept_device_noalloc runs the acceptance kernels on this array
+// instead of a context-allocated buffer: one copy per GPU, held until the
+// process ends, shared by every call on that GPU (calls that overlap on one
+// GPU race).  The kernels' hand-off counters live in its first 64 bytes and
+// start at zero (the array is zero-initialised when the code object loads);
+// every launch returns them to zero before it ends.  The partials after them
+// are rewritten by each launch before they are read.  In host code `scratch`
+// names a host-side stand-in; kernels get the per-device address that
+// hipGetSymbolAddress returns (tqf_hip_create resolves it once per device).
+namespace {
+constexpr size_t kNoAllocScratchBytes = size_t(256) << 10;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device `device` (resolved
+// once per device); nullptr on failure.
+void *noalloc_scratch_for(int device) {
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void *ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+        g_scratch_ptr[device] = ptr;
+    }
+    return g_scratch_ptr[device];
+}
+}  // namespace
 
 namespace {
 
@@ -559,6 +591,16 @@ extern "C" int32_t tqf_hip_create(int32_t device, tqf_hip_ctx **out) {
     }
     ctx->d_adhoc_mats = reinterpret_cast<const uint8_t **>(p);
     ctx->d_adhoc_plan = reinterpret_cast<Plan *>(p + align_up(3 * sizeof(void *), kAlign));
+    // set-up of the allocation-free entry point: this device's copy of
+    // `scratch` (the device is current here)
+    ctx->noalloc_scratch = noalloc_scratch_for(device);
+    if (!ctx->noalloc_scratch) {
+        (void)hipFree(p);
+        (void)hipHostFree(ctx->prof_ring);
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return TQF_HIP_ERR_DEVICE;
+    }
     static const char *const kVariantEnv[TQF_HIP_VARIANTS] = {"TQF_HIP_PERSISTENT", "TQF_HIP_Q4K_FOLD",
                                                               "TQF_HIP_GRAPHS"};
     for (int i = 0; i < TQF_HIP_VARIANTS; ++i) {
@@ -1684,6 +1726,31 @@ extern "C" int32_t tqf_hip_accept_device(tqf_hip_ctx *ctx, const float *d_target
     if (int32_t rc = ensure_accept_scratch(ctx, accept_scratch_bytes(k, vocab))) return rc;
     return enqueue_accept(ctx, d_target, d_draft, d_draft_tokens, k, vocab, temperature, greedy,
                           d_u, d_ures, d_accepted, d_tokens);
+}
+
+extern "C" int32_t tqf_hip_accept_device_noalloc(tqf_hip_ctx *ctx, const float *d_target,
+                                                 const float *d_draft, const int32_t *d_draft_tokens,
+                                                 uint32_t k, uint32_t vocab, float temperature,
+                                                 int32_t greedy, const float *d_u, const float *d_ures,
+                                                 int32_t *d_accepted, int32_t *d_tokens) {
+    TQF_ENTER(ctx);
+    if (!d_target || !d_accepted || !d_tokens || (k > 0 && !d_draft_tokens))
+        return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (int32_t rc = check_accept(ctx, k, vocab, temperature, greedy, d_draft != nullptr,
+                                  d_u != nullptr && d_ures != nullptr))
+        return rc;
+    if (accept_scratch_bytes(k, vocab) > kNoAllocScratchBytes)
+        return fail(ctx, TQF_HIP_ERR_INVALID,
+                    "k and vocab need " + std::to_string(accept_scratch_bytes(k, vocab)) +
+                        " scratch bytes; the allocation-free scratch holds " +
+                        std::to_string(kNoAllocScratchBytes));
+    if (!ctx->noalloc_scratch) return fail(ctx, TQF_HIP_ERR_DEVICE, "allocation-free scratch not resolved");
+    // no profiling events here: an empty event pool would create events
+    hipError_t e = launch_accept(ctx->stream, d_target, d_draft, d_draft_tokens, k, vocab, temperature,
+                                 greedy, d_u, d_ures, d_accepted, d_tokens, ctx->noalloc_scratch,
+                                 nullptr, nullptr);
+    if (e != hipSuccess) return hip_fail(ctx, "acceptance kernel launch", e);
+    return TQF_HIP_OK;
 }
 
 extern "C" int32_t tqf_hip_accept(tqf_hip_ctx *ctx, const float *target, const float *draft,

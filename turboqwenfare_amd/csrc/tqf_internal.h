@@ -378,6 +378,8 @@ struct tqf_hip_ctx {
     // grouped expert GEMM scratch
     void *d_grouped = nullptr;
     size_t grouped_bytes = 0;
+    // this device's copy of the allocation-free acceptance scratch
+    void *noalloc_scratch = nullptr;
     // kernel variant selectors (TQF_HIP_VARIANT_*), from the environment at
     // creation, changed by tqf_hip_set_variant
     int32_t variant[TQF_HIP_VARIANTS] = {1, 1, 1};
