@@ -223,6 +223,7 @@ int32_t ensure_stack_scratch(tqf_hip_ctx *ctx, uint32_t experts, uint32_t bp_dow
     (void)hipFree(sc.logits);
     (void)hipFree(sc.xprep);
     (void)hipFree(sc.hprep);
+    (void)hipFree(sc.hshared);
     (void)hipFree(sc.partial);
     (void)hipFree(sc.ssq);
     sc = StackScratch();
@@ -231,6 +232,7 @@ int32_t ensure_stack_scratch(tqf_hip_ctx *ctx, uint32_t experts, uint32_t bp_dow
     TQF_HIP(ctx, hipMalloc(&sc.logits, (size_t)kStackMT * (experts + 1) * 4));
     TQF_HIP(ctx, hipMalloc(&sc.xprep, (size_t)kStackMT * (kStackHidden / 32) * kXprepDwords * 4));
     TQF_HIP(ctx, hipMalloc(&sc.hprep, (size_t)kStackMT * (kTopK + 1) * bp_down * kXprepDwords * 4));
+    TQF_HIP(ctx, hipMalloc(&sc.hshared, (size_t)kStackMT * bp_down * 32 * 4));
     TQF_HIP(ctx, hipMalloc(&sc.partial, (size_t)kStackTeams * members * kStackMT * 64 * 4));
     TQF_HIP(ctx, hipMalloc(&sc.ssq, (size_t)kStackTeams * kStackMT * 4));
     TQF_HIP(ctx, hipMemset(sc.ssq, 0, (size_t)kStackTeams * kStackMT * 4));
@@ -490,6 +492,7 @@ int32_t enqueue_stack_persistent(tqf_hip_ctx *ctx, const tqf_hip_stack *st, cons
     a.logits = sc.logits;
     a.xprep = sc.xprep;
     a.hprep = sc.hprep;
+    a.hshared = sc.hshared;
     a.partial = sc.partial;
     a.ssq = sc.ssq;
     a.sync = sc.sync;
@@ -652,6 +655,7 @@ extern "C" int32_t tqf_hip_destroy(tqf_hip_ctx *ctx) {
     (void)hipFree(ctx->stack.logits);
     (void)hipFree(ctx->stack.xprep);
     (void)hipFree(ctx->stack.hprep);
+    (void)hipFree(ctx->stack.hshared);
     (void)hipFree(ctx->stack.partial);
     (void)hipFree(ctx->stack.ssq);
     (void)hipFree(ctx->d_stage);

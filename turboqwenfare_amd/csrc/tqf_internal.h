@@ -304,6 +304,7 @@ struct StackArgs {
     float *logits;      // [kStackMT x (E + 1)]
     uint32_t *xprep;    // [kStackMT rows of 28 x 64 dwords]
     uint32_t *hprep;    // [9 kStackMT pair rows of 28 x bp_down dwords]
+    float *hshared;     // [kStackMT x F] the shared expert's silu(g) * u rows
     float *partial;     // [teams x members x kStackMT x 64]
     float *ssq;         // [teams x kStackMT]
     StackSync *sync;
@@ -314,6 +315,7 @@ struct StackScratch {
     float *logits = nullptr;
     uint32_t *xprep = nullptr;
     uint32_t *hprep = nullptr;
+    float *hshared = nullptr;
     float *partial = nullptr;
     float *ssq = nullptr;
     uint32_t experts = 0, bp_down = 0, members = 0;

@@ -6,17 +6,25 @@
 // the router's top-8 (experts/mod.rs:1540-1634).  Per layer three phases are
 // separated by grid barriers (every workgroup is resident, one per CU):
 //
-//   A  the first ~33 workgroups: RMSNorm of the M rows (the sum of squares
-//      comes from per-team partials written by the previous phase C), one
-//      router row (or the shared-expert input gate) per wavefront, and the
-//      activation records of the M x 64 blocks of x.
+//   A  every workgroup: stages the M rows of h in LDS and derives their
+//      RMSNorm scale (the sum of squares comes from per-team partials written
+//      by the previous phase C); router row(s) (or the shared-expert input
+//      gate) with the columns split over its wavefronts; the first M x 32
+//      workgroups also write the activation records of the M x 64 blocks of
+//      x.
 //   B  every workgroup: the routes (softmax, stable top-8, renormalise;
-//      experts/mod.rs:134-197) from the logits -- computed identically in
-//      every workgroup, so the plan needs no further exchange -- then
-//      gate/up units of (expert, 32 rows) for ALL tokens routed to that
-//      expert: its weights are read once, its activation records staged
-//      through LDS; h = silu(g) * u is written as records per (expert, token)
-//      pair.
+//      experts/mod.rs:134-197) from the logits on wavefronts 0..M-1 --
+//      computed identically in every workgroup, so the plan needs no further
+//      exchange -- then
+//      gate/up units of 64 rows (one row octet per wavefront) of one routed
+//      (expert, token) pair, with the activation records of every row in
+//      LDS; h = silu(g) * u is written as records per pair.  M = 4 tokens
+//      have 32 routed pairs: 256 units of equal work, one per workgroup (an
+//      expert two tokens chose is read twice, the second time mostly from
+//      the Infinity Cache).  The shared
+//      expert (all M tokens) is spread thinner: every workgroup takes two of
+//      its rows, one (row, token) per wavefront, and writes raw h values; the
+//      phase C member that owns the shared pairs turns them into records.
 //   C  teams of workgroups own 64 output rows each; a team member takes a
 //      contiguous share of the expert-sorted pair list (8 rows per
 //      wavefront, every weight load issued up front), and the last member to
@@ -38,6 +46,24 @@
 namespace tqf {
 
 namespace {
+
+// The thread index through an opaque register move, so that the compiler
+// rederives each phase's lane arithmetic inside the layer loop instead of
+// hoisting all of it out of the loop, where the hoisted values of every phase
+// would stay live across every other phase (and spill).
+__device__ __forceinline__ uint32_t tid() {
+    uint32_t t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
+// Marks loaded registers as used here: on a path that never uses the data,
+// the loads then complete at this point, instead of leaving the compiler to
+// wait for them (with every later load) wherever the paths join.
+__device__ __forceinline__ void consume(uint32_t v) { asm volatile("" ::"v"(v)); }
+__device__ __forceinline__ void consume(const uint4 &v) {
+    asm volatile("" ::"v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w));
+}
 
 constexpr int kThreads = 512;  // 8 wavefronts
 constexpr int kWaves = kThreads / kWave;
@@ -66,28 +92,43 @@ struct RoutePlan {
     float inv_rms[MT];
     int32_t last;
     int32_t ok;
+    int32_t arrived_last;  // this workgroup released the current grid barrier
 };
 
 // Workgroup-shared state (file scope, so that every access is a ds_* access).
 __shared__ RoutePlan P;
-__shared__ float s_h[MT][32];
+__shared__ float s_h[MT][64];
 __shared__ const uint8_t *s_mats[(256 + 1) * 3];  // the layer's expert matrix table
 extern __shared__ uint4 s_dyn[];
 
 // Phase C's down weights are prefetched into LDS during phase B with direct
 // global -> LDS loads, where they fit: a wavefront's share of one pair is the
 // contiguous octet chunk of its 8 rows (nibbles of 8 rows x LPRD blocks, then
-// their scales: 9 LPRD 16 B), copied byte for byte.  The images sit above
-// every phase's own LDS region.
+// their scales: 9 LPRD 16 B), copied byte for byte.
 template <int LPRD, int MAXP>
 struct DownPrefetch {
     static constexpr uint32_t kWaveBytes = 9 * LPRD * 16;
     static constexpr bool kOn = LPRD == 16 && MAXP <= 5;
     static constexpr uint32_t kBytes = kOn ? MAXP * kWaves * kWaveBytes : 0;
 };
-constexpr uint32_t kPrefOffset = MT * H * 4;  // phase A's h rows, the largest region
-static_assert(MT * 7 * kBpGate * 16 <= kPrefOffset, "phase B region");
-static_assert(5 * 7 * 16 * 16 <= kPrefOffset, "phase C region of the prefetching variant");
+// Dynamic LDS, in phase order:
+//   [0, kHxBytes)            phase A: the M staged rows of h (read by the
+//                            phase B record builders too);
+//   [0, PF::kBytes)          from the arrival at the barrier before phase C
+//                            on: the prefetched down weights (the h rows are
+//                            dead by then);
+//   [xr, xr + kXrBytes)      phase B: the activation records of the M rows
+//                            (7 planes x 64 blocks x 16 B per row);
+//   [xr, ...)                phase C: the h records of the member's pairs.
+constexpr uint32_t kHxBytes = MT * H * 4;
+constexpr uint32_t kXrBytes = MT * 7 * kBpGate * 16;
+template <int LPRD, int MAXP>
+struct LdsLayout {
+    static constexpr uint32_t kPf = DownPrefetch<LPRD, MAXP>::kBytes;
+    static constexpr uint32_t kXr = (kPf > kHxBytes ? kPf : kHxBytes);
+    static constexpr uint32_t kCStage = MAXP * 7 * LPRD * 16;
+    static constexpr uint32_t kTotal = kXr + (kXrBytes > kCStage ? kXrBytes : kCStage);
+};
 
 // Workgroup barrier for LDS data only: this wavefront's LDS accesses
 // complete (lgkmcnt(0)), then s_barrier.  __syncthreads() would also wait for
@@ -125,34 +166,64 @@ __device__ __forceinline__ void stage_coherent(uint64_t *dst, const uint64_t *sr
     uint64_t v[PER_THREAD];
 #pragma unroll
     for (int i = 0; i < PER_THREAD; ++i) {
-        const uint32_t k = threadIdx.x + (uint32_t)i * kThreads;
+        const uint32_t k = tid() + (uint32_t)i * kThreads;
         v[i] = k < n ? load_coherent_u64(src + k) : 0;
     }
 #pragma unroll
     for (int i = 0; i < PER_THREAD; ++i) {
-        const uint32_t k = threadIdx.x + (uint32_t)i * kThreads;
+        const uint32_t k = tid() + (uint32_t)i * kThreads;
         if (k < n) dst[k] = v[i];
     }
 }
 
 // ---- grid barrier ------------------------------------------------------------
-__device__ bool grid_sync(StackSync *sync, uint32_t &epoch, int32_t *status) {
-    wait_own_stores();
-    __syncthreads();
+// Split phase: barrier_arrive counts this workgroup in once every thread's
+// stores are complete (the caller waits for them) and the last arrival
+// releases everyone; grid_wait polls for the release.  Work placed between
+// the two overlaps the barrier, and grid_wait uses only an LDS barrier, so
+// loads issued in between (the down weight prefetch) are not waited for.
+// One thread arrives and polls: lane 0 of the last wavefront, which issues
+// none of the prefetch's copies (its poll loads would wait for them).
+constexpr int kPoller = (kWaves - 1) * kWave;
+constexpr int kDmaWaves = 6;  // wavefronts 0..5 issue the down prefetch
+
+__device__ void barrier_arrive(StackSync *sync, uint32_t &epoch) {
+    lds_barrier();
     ++epoch;
-    if (threadIdx.x == 0) {
+    if (tid() == kPoller) {
         const uint32_t target = epoch * gridDim.x;
+        const bool last = counter_arrive(&sync->barrier) + 1 == target;
+        // last arrival: release everyone (the poll line sees no atomics)
+        if (last) __hip_atomic_store(&sync->release, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        P.arrived_last = last ? 1 : 0;
+    }
+}
+
+__device__ void grid_arrive(StackSync *sync, uint32_t &epoch) {
+    wait_own_stores();
+    barrier_arrive(sync, epoch);
+}
+
+__device__ __forceinline__ uint64_t poll_load(const uint64_t *word) {
+    return __hip_atomic_load(const_cast<uint64_t *>(word), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The poller keeps three loads of the release word in flight, so a release
+// is seen about one round trip after it lands rather than up to two.
+__device__ bool grid_wait(StackSync *sync, uint32_t epoch, int32_t *status) {
+    if (tid() == kPoller) {
         int ok = 1;
-        if (counter_arrive(&sync->barrier) + 1 == target) {
-            // last arrival: release everyone (the poll line sees no atomics)
-            __hip_atomic_store(&sync->release, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-            uint64_t *word = reinterpret_cast<uint64_t *>(&sync->release);
+        if (!P.arrived_last) {
+            const uint64_t *word = reinterpret_cast<const uint64_t *>(&sync->release);
+            uint64_t v0 = poll_load(word);
+            __builtin_amdgcn_s_sleep(1);
+            uint64_t v1 = poll_load(word);
             int64_t t0 = 0;
             for (uint32_t spin = 1;; ++spin) {
-                const uint64_t v = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if ((uint32_t)v >= epoch) break;
-                if (v >> 32) {  // another workgroup timed out
+                __builtin_amdgcn_s_sleep(1);
+                const uint64_t v2 = poll_load(word);
+                if ((uint32_t)v0 >= epoch) break;
+                if (v0 >> 32) {  // another workgroup timed out
                     ok = 0;
                     break;
                 }
@@ -169,13 +240,22 @@ __device__ bool grid_sync(StackSync *sync, uint32_t &epoch, int32_t *status) {
                         break;
                     }
                 }
-                __builtin_amdgcn_s_sleep(2);
+                v0 = v1;
+                v1 = v2;
             }
+            // the loads still in flight complete here, in this wavefront,
+            // rather than at a later reuse of their registers by every one
+            asm volatile("s_waitcnt vmcnt(0)" ::"v"(v0), "v"(v1) : "memory");
         }
         P.ok = ok;
     }
-    __syncthreads();
+    lds_barrier();
     return P.ok != 0;
+}
+
+__device__ bool grid_sync(StackSync *sync, uint32_t &epoch, int32_t *status) {
+    grid_arrive(sync, epoch);
+    return grid_wait(sync, epoch, status);
 }
 
 // Last workgroup out resets the barrier state (every workgroup reaches this,
@@ -183,7 +263,7 @@ __device__ bool grid_sync(StackSync *sync, uint32_t &epoch, int32_t *status) {
 __device__ void stack_exit(StackSync *sync) {
     wait_own_stores();
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid() == 0) {
         if (counter_arrive(&sync->exit) == gridDim.x - 1) {
             counter_reset(&sync->barrier);
             counter_reset(&sync->release);
@@ -201,8 +281,8 @@ __device__ void stack_exit(StackSync *sync) {
 // staged in LDS.
 __device__ void phase_a(const StackArgs &a, const StackLayer &L, const float *hin) {
     float *s_hx = reinterpret_cast<float *>(s_dyn);
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int lane = threadIdx.x % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
+    const int lane = tid() % kWave;
     const uint32_t m = a.m, E = a.E;
     const uint32_t col = 256 * wave + 4 * lane;
     const float4 nw = load_global_f4(L.norm + col);
@@ -266,75 +346,190 @@ __device__ void phase_a(const StackArgs &a, const StackLayer &L, const float *hi
     }
 }
 
-// ---- phase B: the loads of one gate/up unit ----------------------------------------
-// Wavefront w's rows 4w..4w+3 of the unit in gate and up (one block per lane,
-// raw nibbles) and their scales, held in registers between issue and use.
+// ---- phase B: gate/up units ------------------------------------------------------
+// Unit u < 8 M (F / 64) is rows [64 (u % (F / 64)), +64) of routed pair
+// M + u / (F / 64) in the plan's pair order (wavefront w: the octet of rows
+// 8w..8w+7).
+struct UnitDesc {
+    int pair, row0, rw;  // pair, first row, rows per wavefront
+};
+__device__ __forceinline__ UnitDesc unit_desc(int u, int F, int m) {
+    UnitDesc d;
+    d.pair = m + u / (F / 64);
+    d.row0 = (u % (F / 64)) * 64;
+    d.rw = 8;
+    return d;
+}
+
+// Wavefront w's rows of the unit in gate and up (one block per lane, raw
+// nibbles) and their scale octets, held in registers between issue and use.
 constexpr int kRecRow = 7 * kBpGate * 2;  // 64-bit words of one token's records
 constexpr int kRecPer = (MT * kRecRow + kThreads - 1) / kThreads;
 struct UnitLoads {
-    uint4 ng[4], nu[4], sg, su;
+    uint64_t xv[kRecPer];  // this thread's share of the M rows' activation records
+    uint4 ng[8], nu[8], sg, su;
 };
 
-__device__ __forceinline__ void unit_loads(const StackArgs &a, int expert, int blk32, UnitLoads &U) {
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int lane = threadIdx.x % kWave;
-    const RowLane Wg = row_lane(s_mats[expert * 3 + 0], kBpGate), Wu = row_lane(s_mats[expert * 3 + 1], kBpGate);
-    const uint32_t r = (uint32_t)blk32 * 32 + 4 * wave;
+// The records of the M rows (written by phase A), this thread's share of the
+// LDS image; issued when the layer's phase B starts, stored by store_records.
+__device__ __forceinline__ void record_loads(const StackArgs &a, UnitLoads &U) {
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
+    for (int i = 0; i < kRecPer; ++i) {
+        const int k = (int)tid() + i * kThreads;
+        U.xv[i] = k < (int)a.m * kRecRow ? load_coherent_u64(reinterpret_cast<const uint64_t *>(a.xprep) + k) : 0;
+    }
+}
+template <int LPRD, int MAXP>
+__device__ __forceinline__ void store_records(const StackArgs &a, const UnitLoads &U) {
+    uint64_t *dst = reinterpret_cast<uint64_t *>(reinterpret_cast<uint8_t *>(s_dyn) + LdsLayout<LPRD, MAXP>::kXr);
+#pragma unroll
+    for (int i = 0; i < kRecPer; ++i) {
+        const int k = (int)tid() + i * kThreads;
+        if (k < (int)a.m * kRecRow) dst[k] = U.xv[i];
+    }
+}
+
+// ---- phase B: the shared expert's rows ------------------------------------------
+// Wavefront w of workgroup b: row 2 b + (w & 1) (then + 2 G, ...) of the
+// shared expert's gate and up for token w >> 1; the raw value silu(g) * u goes
+// to hshared[token][row].
+struct SharedLoads {
+    uint4 ng, nu;
+    uint32_t sg, su;  // the lane's block scale of the row (binary16 bits)
+};
+__device__ __forceinline__ void consume_shared(const SharedLoads &S) {
+    consume(S.ng);
+    consume(S.nu);
+    consume(S.sg);
+    consume(S.su);
+}
+__device__ __forceinline__ uint32_t load_scale_row(const RowLane &m, uint32_t row, uint32_t block) {
+    return *(const __attribute__((address_space(1))) uint16_t *)(m.base + (((size_t)(row >> 3) * 9 + 8) * m.bp + block) * 16 +
+                                                                 (row & 7) * 2);
+}
+__device__ __forceinline__ void shared_row_loads(const StackArgs &a, uint32_t row, SharedLoads &S) {
+    const int lane = tid() % kWave;
+    const RowLane Wg = row_lane(s_mats[a.E * 3 + 0], kBpGate), Wu = row_lane(s_mats[a.E * 3 + 1], kBpGate);
+    S.ng = load_nibbles(Wg, row, lane);
+    S.nu = load_nibbles(Wu, row, lane);
+    S.sg = load_scale_row(Wg, row, lane);
+    S.su = load_scale_row(Wu, row, lane);
+}
+template <int LPRD, int MAXP>
+__device__ void shared_rows(const StackArgs &a, const SharedLoads &S0) {
+    const uint4 *xr = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint8_t *>(s_dyn) +
+                                                      LdsLayout<LPRD, MAXP>::kXr);
+    const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
+    const int lane = tid() % kWave;
+    const uint32_t t = (uint32_t)wave >> 1;
+    if (t >= a.m || 2 * blockIdx.x + (wave & 1) >= a.F) {
+        consume_shared(S0);
+        return;
+    }
+    SharedLoads S = S0;
+    for (uint32_t row = 2 * blockIdx.x + (wave & 1), i = 0; row < a.F; row += 2 * gridDim.x, ++i) {
+        if (i > 0) shared_row_loads(a, row, S);
+        uint32_t x[28];
+#pragma unroll
+        for (int qd = 0; qd < 7; ++qd) {
+            const uint4 v = xr[((size_t)t * 7 + qd) * kBpGate + lane];
+            x[4 * qd] = v.x;
+            x[4 * qd + 1] = v.y;
+            x[4 * qd + 2] = v.z;
+            x[4 * qd + 3] = v.w;
+        }
+        float v[2] = {f16_to_f32(S.sg) * q4_block_dot(q4_signed(S.ng), x),
+                      f16_to_f32(S.su) * q4_block_dot(q4_signed(S.nu), x)};
+        const float gate = transpose_reduce<64, 2>(v);  // lanes 0..31: gate, 32..63: up
+        const float up = __shfl_xor(gate, 32);
+        if (lane == 0) store_coherent(&a.hshared[(size_t)t * a.F + row], (gate / (1.0f + expf(-gate))) * up);
+    }
+}
+
+template <int RW>
+__device__ __forceinline__ void unit_loads_rw(int expert, int row0, UnitLoads &U) {
+    const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
+    const int lane = tid() % kWave;
+    const RowLane Wg = row_lane(s_mats[expert * 3 + 0], kBpGate), Wu = row_lane(s_mats[expert * 3 + 1], kBpGate);
+    const uint32_t r = (uint32_t)row0 + RW * wave;
+#pragma unroll
+    for (int n = 0; n < RW; ++n) {
         U.ng[n] = load_nibbles(Wg, r + n, lane);
         U.nu[n] = load_nibbles(Wu, r + n, lane);
     }
     U.sg = load_scales(Wg, r / 8, lane);
     U.su = load_scales(Wu, r / 8, lane);
 }
+__device__ __forceinline__ void unit_loads(int expert, const UnitDesc &d, UnitLoads &U) {
+    if (d.rw == 8) unit_loads_rw<8>(expert, d.row0, U);
+    else unit_loads_rw<4>(expert, d.row0, U);
+}
 
 // This workgroup's first unit (blockIdx.x) from the routes alone, before the
-// pair plan exists: its group is the shared expert or the g-th distinct routed
-// expert in first-demand order (the plan's group order).  Every wavefront
-// issues its weight loads, which then fly while wavefront 0 builds the plan.
-// False: the workgroup has no unit.
+// pair plan exists: the expert of its pair, found with the plan's own pair
+// order (groups in first-demand order, a group's tokens ascending).  Every
+// wavefront issues its weight loads, which then fly while wavefront 0 builds
+// the plan.  False: the workgroup has no unit.
 __device__ __forceinline__ bool early_unit_loads(const StackArgs &a, UnitLoads &U) {
-    const int lane = threadIdx.x % kWave;
-    const int nb32 = (int)a.F / 32;
-    const int g = (int)blockIdx.x / nb32, blk32 = (int)blockIdx.x % nb32;
+    const int lane = tid() % kWave;
     const int m = (int)a.m, n = m * kTopK;
-    int expert;
-    if (g == 0) {
-        expert = (int)a.E;
-    } else {
-        // route entry i = (t, k) on lane i; other lanes carry distinct dummy keys
-        const int e_i = lane < n ? P.ids[lane / kTopK][lane % kTopK] : 256 + lane;
-        const uint64_t peers = match_peers((uint32_t)e_i);
-        const uint64_t below = (1ull << lane) - 1ull;
-        const uint64_t firsts = __ballot(lane < n && (peers & below) == 0);
-        if (g > __builtin_popcountll(firsts)) return false;
-        uint64_t mk = firsts;
-        for (int r = 1; r < g; ++r) mk &= mk - 1ull;
-        expert = __builtin_amdgcn_readlane(e_i, (int)__builtin_ctzll(mk));
+    const int u = (int)blockIdx.x;
+    if (u >= n * ((int)a.F / 64)) return false;
+    const UnitDesc d = unit_desc(u, (int)a.F, m);
+    // route entry i = (t, k) on lane i; other lanes carry distinct dummy keys
+    const int e_i = lane < n ? P.ids[lane / kTopK][lane % kTopK] : 256 + lane;
+    const uint64_t peers = match_peers((uint32_t)e_i);
+    const uint64_t below = (1ull << lane) - 1ull;
+    const int first = (int)__builtin_ctzll(peers);  // the group's first entry
+    const int rank = __builtin_popcountll(peers & below);
+    // entries of groups that start before this entry's group: an exclusive
+    // prefix sum, in lane order, of each group's size at its first entry
+    const int size_at_first = (lane < n && first == lane) ? __builtin_popcountll(peers) : 0;
+    int incl = size_at_first;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int o = __shfl_up(incl, off);
+        if (lane >= off) incl += o;
     }
-    unit_loads(a, expert, blk32, U);
+    const int before = __shfl(incl - size_at_first, first);
+    const uint64_t hit = __ballot(lane < n && m + before + rank == d.pair);
+    const int expert = __builtin_amdgcn_readlane(e_i, (int)__builtin_ctzll(hit));
+    unit_loads(expert, d, U);
     return true;
 }
 
 // ---- phase B: routes ------------------------------------------------------------
 // `pre`: whether this workgroup's first unit's loads were issued (in `U`).
-__device__ void compute_routes(const StackArgs &a, UnitLoads &U, bool &pre) {
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int lane = threadIdx.x % kWave;
+// After the loads are issued only LDS barriers are used: __syncthreads()
+// would wait for them.
+template <int LPRD, int MAXP>
+__device__ void compute_routes(const StackArgs &a, const StackLayer &L, UnitLoads &U, SharedLoads &S,
+                               bool &pre) {
+    const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
+    const int lane = tid() % kWave;
     const uint32_t m = a.m, E = a.E;
-    if (threadIdx.x == 0) P.bad = 0;
-    __syncthreads();
+    if (tid() == 0) P.bad = 0;
+    lds_barrier();
+    // the routing wavefronts' logits first, then the loads that need no
+    // routes (the M rows' records, this wavefront's shared-expert row), so
+    // that the logits are not queued behind them
+    const int t = wave;
+    const float *lt = a.logits + (size_t)(t < (int)m ? t : 0) * (E + 1);
+    float lv[4], glog = 0.0f;
     if (wave < (int)m) {
-        const int t = wave;
-        const float *lt = a.logits + (size_t)t * (E + 1);
-        float lv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {  // unconditional loads: one round trip
             const uint32_t e = (uint32_t)lane + 64u * i;
             lv[i] = load_coherent(lt + (e < E ? e : E - 1));
         }
-        const float glog = load_coherent(lt + E);
+        glog = load_coherent(lt + E);
+    }
+    record_loads(a, U);
+    {
+        const uint32_t row = 2 * blockIdx.x + (wave & 1);
+        if (row < a.F && (uint32_t)(wave >> 1) < m) shared_row_loads(a, row, S);
+    }
+    if (wave < (int)m) {
         bool fin = true;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -400,19 +595,27 @@ __device__ void compute_routes(const StackArgs &a, UnitLoads &U, bool &pre) {
             if (lane == 0 && !(fabsf(wsum - 1.0f) <= 1e-4f)) P.bad = 1;
         }
     }
-    __syncthreads();
+    store_records<LPRD, MAXP>(a, U);  // waits for the record loads only
+    lds_barrier();
     pre = false;
     if (P.bad) {
-        if (threadIdx.x == 0) {
+        if (tid() == 0) {
             P.n_groups = 0;
             P.n_pairs = 0;
         }
-        __syncthreads();
+        // no unit uses the shared-expert row: its loads complete here
+        consume_shared(S);
+        lds_barrier();
         return;
     }
-    pre = early_unit_loads(a, U);
+    // the shared expert's rows (records and row loads are in by now), before
+    // any unit load is issued, so that they wait for nothing else
+    shared_rows<LPRD, MAXP>(a, S);
     // the pair plan, one route entry i = (t, k) per lane of wavefront 0: the
-    // entries of the same expert as bits of one mask (broadcast LDS reads)
+    // entries of the same expert as bits of one mask (broadcast LDS reads).
+    // Wavefront 0 builds it before issuing its own unit loads: the others'
+    // loads already stream meanwhile, and issuing stalls once the CU's memory
+    // pipeline is full.
     if (wave == 0) {
         const int n = (int)m * kTopK;
         const int *flat = &P.ids[0][0];
@@ -462,121 +665,151 @@ __device__ void compute_routes(const StackArgs &a, UnitLoads &U, bool &pre) {
             P.n_pairs = (int)m * (kTopK + 1);
         }
     }
-    __syncthreads();
+    pre = early_unit_loads(a, U);
+    lds_barrier();
+}
+
+// ---- phase C's pair shares -----------------------------------------------------------
+// Member k (of K) of a team: the shared pairs s = k, k + K, ... < M (at most
+// one when K >= M, so that the shared records, which the member builds from
+// raw rows, are spread over the members), then an equal contiguous share of
+// the routed pairs [M, n_pairs).
+struct MemberShare {
+    int k, K, ns, r0, r1;
+    __device__ int cnt() const { return ns + r1 - r0; }
+    __device__ int pair(int q) const { return q < ns ? k + K * q : r0 + q - ns; }
+};
+__device__ __forceinline__ MemberShare member_share(int k, int K, int m, int n_pairs) {
+    MemberShare s;
+    s.k = k;
+    s.K = K;
+    if (n_pairs == 0) {  // routing failed: no pairs
+        s.ns = s.r0 = s.r1 = 0;
+        return s;
+    }
+    s.ns = k < m ? (m - 1 - k) / K + 1 : 0;
+    const int R = n_pairs - m;
+    s.r0 = m + k * R / K;
+    s.r1 = m + (k + 1) * R / K;
+    return s;
 }
 
 // ---- phase B: prefetch of phase C's down weights ------------------------------------
 // This workgroup's phase C share (the same member / pair split as phase_c):
 // per pair, wavefront w's octet chunk of the pair's down matrix into its LDS
-// image.  Issued inside the workgroup's first gate/up unit once its own loads
-// are consumed, so the copies overlap the unit's compute (whose barriers are
-// LDS-only); the grid barrier before phase C drains them.
+// image.  Issued after the workgroup has arrived at the barrier before phase
+// C (its gate/up loads and h record stores are complete by then), so the
+// copies stream while the barrier completes; phase C's first wait drains
+// them before the images are read.
 template <int LPRD, int MAXP>
-__device__ void prefetch_down(const StackArgs &a) {
+struct PrefetchOps {
+    static constexpr int kParts = LPRD / 8 + LPRD / 16;  // copies per image: nibble KiBs, scale rows
+    static constexpr int kOps = MAXP * kWaves * kParts;
+    static constexpr int kPerWave = kOps / kDmaWaves;
+    static_assert(kOps % kDmaWaves == 0, "prefetch copies split evenly");
+};
+
+// Every image slot gets a copy (slots past the member's pairs repeat its last
+// pair, or the shared expert's down matrix when it has none), so each of
+// wavefronts 0..5 issues exactly PrefetchOps::kPerWave copies.  The poller's
+// wavefront issues none.  Returns whether this wavefront issued copies.
+template <int LPRD, int MAXP>
+__device__ bool prefetch_down(const StackArgs &a) {
     using PF = DownPrefetch<LPRD, MAXP>;
+    using OPS = PrefetchOps<LPRD, MAXP>;
     if constexpr (PF::kOn) {
         const uint32_t K = a.members;
         const uint32_t tau = blockIdx.x % kStackTeams, k = blockIdx.x / kStackTeams;
-        if (k >= K) return;
-        const int n_pairs = P.n_pairs;
-        const int p0 = (int)(k * n_pairs / K), p1 = (int)((k + 1) * n_pairs / K);
-        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-        const int lane = threadIdx.x % kWave;
-        const uint32_t octet = tau * 8 + (uint32_t)wave;  // rows tau * 64 + 8 wave ..
-        const uint32_t img = kPrefOffset + (uint32_t)wave * MAXP * PF::kWaveBytes;
+        const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
+        if (k >= K || wave >= kDmaWaves) return false;
+        const MemberShare sh = member_share((int)k, (int)K, (int)a.m, P.n_pairs);
+        const int cnt = sh.cnt();
+        const int lane = tid() % kWave;
 #pragma unroll
-        for (int q = 0; q < MAXP; ++q) {
-            if (p0 + q < p1) {
-                const uint8_t *chunk = s_mats[P.pair_expert[p0 + q] * 3 + 2] + (size_t)octet * PF::kWaveBytes;
-                const uint32_t dst = img + (uint32_t)q * PF::kWaveBytes;
-#pragma unroll
-                for (int i = 0; i < LPRD / 8; ++i)  // nibbles: 1 KiB per instruction
-                    copy_to_lds_16(chunk + i * 1024 + lane * 16, lds_addr(dst + i * 1024));
-#pragma unroll
-                for (int i = 0; i < LPRD / 16; ++i)  // scales: 256 B per instruction
-                    copy_to_lds_4(chunk + 8 * LPRD * 16 + i * 256 + lane * 4, lds_addr(dst + 8 * LPRD * 16 + i * 256));
-            }
+        for (int i = 0; i < OPS::kPerWave; ++i) {
+            const int o = wave * OPS::kPerWave + i;
+            const int img = o / OPS::kParts, part = o % OPS::kParts;
+            const int q = img / kWaves, w = img % kWaves;  // pair slot, octet wavefront
+            const int e = cnt > 0 ? P.pair_expert[sh.pair(q < cnt ? q : cnt - 1)] : (int)a.E;
+            const uint8_t *chunk = s_mats[e * 3 + 2] + (size_t)(tau * 8 + w) * PF::kWaveBytes;
+            const uint32_t dst = ((uint32_t)w * MAXP + q) * PF::kWaveBytes;
+            if (part < LPRD / 8)  // nibbles: 1 KiB per instruction
+                copy_to_lds_16(chunk + part * 1024 + lane * 16, lds_addr(dst + part * 1024));
+            else  // scales: 256 B per instruction
+                copy_to_lds_4(chunk + 8 * LPRD * 16 + (part - LPRD / 8) * 256 + lane * 4,
+                              lds_addr(dst + 8 * LPRD * 16 + (part - LPRD / 8) * 256));
         }
+        return true;
     }
+    return false;
 }
 
-// ---- phase B: gate/up units ---------------------------------------------------
-// Unit = (group g, rows [32 blk32, +32)) for all of g's tokens.  Wavefront w
-// owns rows 4w..4w+3 of the unit in both matrices.
+// ---- phase B: one gate/up unit -------------------------------------------------
 // `preloaded`: U already holds this unit's loads (early_unit_loads).
-template <int LPRD, int MAXP>
-__device__ void gate_up_unit(const StackArgs &a, const StackLayer &L, int unit, bool prefetch,
-                             UnitLoads &U, bool preloaded) {
-    uint4 *s_x = s_dyn;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int lane = threadIdx.x % kWave;
-    const int nb32 = (int)a.F / 32;
-    const int g = unit / nb32, blk32 = unit % nb32;
-    const int cnt = P.grp_cnt[g];
-    // weights (HBM) and the activation records of the group's tokens: one
-    // round trip for both, issued here unless they are already in flight
-    if (!preloaded) unit_loads(a, P.grp_expert[g], blk32, U);
-    const uint32_t r = (uint32_t)blk32 * 32 + 4 * wave;
-    const int pos = (int)(r & 7);  // 0 or 4
-    {
-        uint64_t v[kRecPer];
+template <int RW, int LPRD, int MAXP>
+__device__ void gate_up_compute(const StackArgs &a, const UnitDesc &d, UnitLoads &U) {
+    // one token: the pair's
+    const uint4 *xr = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint8_t *>(s_dyn) +
+                                                      LdsLayout<LPRD, MAXP>::kXr);
+    const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
+    const int lane = tid() % kWave;
+    const int pos = (int)(((uint32_t)d.row0 + RW * wave) & 7);  // 0, or 4 in a 32-row unit
+    uint4 ng[RW], nu[RW];
 #pragma unroll
-        for (int i = 0; i < kRecPer; ++i) {
-            const int k = (int)threadIdx.x + i * kThreads;
-            const int ti = k / kRecRow, off = k % kRecRow;
-            const uint64_t *src = reinterpret_cast<const uint64_t *>(
-                a.xprep + (size_t)P.grp_tok[g][ti < cnt ? ti : 0] * kBpGate * kXprepDwords);
-            v[i] = ti < cnt ? load_coherent_u64(src + off) : 0;
-        }
-        uint64_t *dst = reinterpret_cast<uint64_t *>(s_x);  // 7 planes x 64 blocks per token
-#pragma unroll
-        for (int i = 0; i < kRecPer; ++i) {
-            const int k = (int)threadIdx.x + i * kThreads;
-            if (k < cnt * kRecRow) dst[k] = v[i];
-        }
-    }
-    lds_barrier();
-    // every load of this unit is consumed here (waited for explicitly, on
-    // every path), so no later wait of the unit covers the prefetch's copies
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt / lgkmcnt at their maxima
-    if (prefetch) prefetch_down<LPRD, MAXP>(a);
-    uint4 ng[4], nu[4];
-#pragma unroll
-    for (int n = 0; n < 4; ++n) {
+    for (int n = 0; n < RW; ++n) {
         ng[n] = q4_signed(U.ng[n]);
         nu[n] = q4_signed(U.nu[n]);
     }
     const uint4 sg = U.sg, su = U.su;
-    for (int i = 0; i < cnt; ++i) {
+    {
+        const int i = 0, t = P.pair_tok[d.pair];
         uint32_t x[28];
 #pragma unroll
         for (int qd = 0; qd < 7; ++qd) {
-            const uint4 v = s_x[((size_t)i * 7 + qd) * kBpGate + lane];
+            const uint4 v = xr[((size_t)t * 7 + qd) * kBpGate + lane];
             x[4 * qd] = v.x;
             x[4 * qd + 1] = v.y;
             x[4 * qd + 2] = v.z;
             x[4 * qd + 3] = v.w;
         }
-        float v[8];
+        float v[2 * RW];
 #pragma unroll
-        for (int n = 0; n < 4; ++n) {
+        for (int n = 0; n < RW; ++n) {
             v[2 * n] = octet_scale(sg, pos + n) * q4_block_dot(ng[n], x);
             v[2 * n + 1] = octet_scale(su, pos + n) * q4_block_dot(nu[n], x);
         }
-        const float gate = transpose_reduce<64, 8>(v);  // lanes 16n..: gate n, 16n+8..: up n
-        const float up = dpp_f<0x108>(gate);            // row_shl:8
-        if ((lane & 15) == 0) s_h[i][4 * wave + (lane >> 4)] = (gate / (1.0f + expf(-gate))) * up;
+        // value 2n (gate row n) lands on lanes (64 / RW) n .., value 2n + 1 (up
+        // row n) on the lanes 32 / RW above them
+        const float gate = transpose_reduce<64, 2 * RW>(v);
+        const float up = RW == 8 ? dpp_f<0x104>(gate) : dpp_f<0x108>(gate);  // row_shl:4 / :8
+        if ((lane & (64 / RW - 1)) == 0)
+            s_h[i][RW * wave + lane / (64 / RW)] = (gate / (1.0f + expf(-gate))) * up;
     }
+}
+
+template <int LPRD, int MAXP>
+__device__ void gate_up_unit(const StackArgs &a, const UnitDesc &d, UnitLoads &U, bool preloaded) {
+    const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
+    const int lane = tid() % kWave;
+    const int cnt = 1;
+    // the weights (HBM), unless early_unit_loads already issued them; the
+    // activation records are in LDS
+    if (!preloaded) unit_loads(P.pair_expert[d.pair], d, U);
+    gate_up_compute<8, LPRD, MAXP>(a, d, U);
     lds_barrier();
-    // h records: two tokens per wavefront
-    if (2 * wave < cnt) {
-        const int i = 2 * wave + (lane >> 5);
-        const bool active = i < cnt;
-        const int ii = active ? i : 2 * wave;
-        const int pair = P.grp_base[g] + ii;
-        prep_block32(s_h[ii][lane & 31], lane & 31, active,
-                     a.hprep + (size_t)pair * LPRD * kXprepDwords, LPRD, (uint32_t)blk32,
-                     CoherentStore());
+    // h records: one (token, 32-row block) per half-wavefront, from the last
+    // wavefront down (the wavefronts that issue no prefetch copies)
+    const int nblk = d.rw / 4;  // 32-row blocks in the unit
+    const int rwave = kWaves - 1 - wave;
+    if (2 * rwave < cnt * nblk) {
+        const int q = 2 * rwave + (lane >> 5);
+        const bool active = q < cnt * nblk;
+        const int qq = active ? q : 2 * rwave;
+        const int i = qq / nblk, kb = qq % nblk;
+        const int pair = d.pair;
+        prep_block32(s_h[i][32 * kb + (lane & 31)], lane & 31, active,
+                     a.hprep + (size_t)pair * LPRD * kXprepDwords, LPRD,
+                     (uint32_t)(d.row0 / 32 + kb), CoherentStore());
     }
     lds_barrier();
 }
@@ -584,9 +817,9 @@ __device__ void gate_up_unit(const StackArgs &a, const StackLayer &L, int unit, 
 // ---- phase C -------------------------------------------------------------------
 template <int LPRD, int MAXP>
 __device__ void phase_c(const StackArgs &a, const StackLayer &L, const float *hin) {
-    uint4 *s_x = s_dyn;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int lane = threadIdx.x % kWave;
+    uint4 *s_x = reinterpret_cast<uint4 *>(reinterpret_cast<uint8_t *>(s_dyn) + LdsLayout<LPRD, MAXP>::kXr);
+    const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
+    const int lane = tid() % kWave;
     constexpr int G = kWave / LPRD;   // lane groups per wavefront
     constexpr int RG = 8 / G;         // rows per lane group (a wavefront owns one octet)
     constexpr int NL = MT * RG;       // values per lane before the transpose
@@ -594,9 +827,8 @@ __device__ void phase_c(const StackArgs &a, const StackLayer &L, const float *hi
     const uint32_t K = a.members;
     const uint32_t tau = blockIdx.x % kStackTeams, k = blockIdx.x / kStackTeams;
     if (k >= K) return;
-    const int n_pairs = P.n_pairs;
-    const int p0 = (int)(k * n_pairs / K), p1 = (int)((k + 1) * n_pairs / K);
-    const int cnt = p1 - p0;
+    const MemberShare share = member_share((int)k, (int)K, (int)a.m, P.n_pairs);
+    const int cnt = share.cnt();
     const uint32_t j = (uint32_t)lane / LPRD, b = (uint32_t)lane % LPRD;
     const uint32_t r0 = tau * 64 + 8 * wave;  // this wavefront's octet
     // every weight load of the member up front (pair index clamped into the
@@ -607,17 +839,47 @@ __device__ void phase_c(const StackArgs &a, const StackLayer &L, const float *hi
     if (!PF::kOn && cnt > 0) {
 #pragma unroll
         for (int q = 0; q < MAXP; ++q) {
-            const int pq = p0 + (q < cnt ? q : cnt - 1);
+            const int pq = share.pair(q < cnt ? q : cnt - 1);
             const RowLane W = row_lane(s_mats[P.pair_expert[pq] * 3 + 2], LPRD);
 #pragma unroll
             for (int rr = 0; rr < RG; ++rr) nib[q][rr] = q4_signed(load_nibbles(W, r0 + j * RG + rr, b));
             sc[q] = load_scales(W, r0 / 8, b);
         }
     }
+    // routed pairs (staging slots ns..): their records from phase B; shared
+    // pairs (slots 0..ns-1): records of the raw rows, one (pair, block) per
+    // half-wavefront and round
     stage_coherent<(MAXP * 7 * LPRD * 2 + kThreads - 1) / kThreads>(
-        reinterpret_cast<uint64_t *>(s_x),
-        reinterpret_cast<const uint64_t *>(a.hprep + (size_t)p0 * LPRD * kXprepDwords),
-        (uint32_t)cnt * 7 * LPRD * 2);
+        reinterpret_cast<uint64_t *>(s_x) + (size_t)share.ns * 7 * LPRD * 2,
+        reinterpret_cast<const uint64_t *>(a.hprep + (size_t)share.r0 * LPRD * kXprepDwords),
+        (uint32_t)(share.r1 - share.r0) * 7 * LPRD * 2);
+    {
+        // kIt rounds (the most a member can own: ceil(M / K) shared pairs of
+        // LPRD blocks over 16 half-wavefronts); every round's loads go out
+        // before the first build
+        constexpr int kIt = MT * LPRD / (2 * kWaves);
+        const int nb = (int)a.F / 32, n_sh = share.ns * nb;
+        const int hw = (int)(tid() >> 5), jj = lane & 31;
+        float vv[kIt];
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+            const int q = it * 2 * kWaves + hw;  // uniform per half-wavefront
+            const int qq = q < n_sh ? q : 0;
+            const int pair = share.pair(qq / nb), blk = qq % nb;
+            vv[it] = q < n_sh ? load_coherent(&a.hshared[(size_t)P.pair_tok[pair] * a.F + blk * 32 + jj]) : 0.0f;
+        }
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+            const int q = it * 2 * kWaves + hw;
+            if (it * 2 * kWaves < n_sh) {  // uniform over the workgroup
+                const bool active = q < n_sh;
+                const int qq = active ? q : 0;
+                prep_block32(vv[it], jj, active,
+                             reinterpret_cast<uint32_t *>(s_x) + (size_t)(qq / nb) * 7 * LPRD * 4, LPRD,
+                             (uint32_t)(qq % nb), PlainStore());
+            }
+        }
+    }
     __syncthreads();
     float acc[NL];
 #pragma unroll
@@ -626,7 +888,7 @@ __device__ void phase_c(const StackArgs &a, const StackLayer &L, const float *hi
 #pragma unroll
     for (int q = 0; q < MAXP; ++q) {
         if (q < cnt) {
-            const int pq = p0 + q;
+            const int pq = share.pair(q);
             const int tok = P.pair_tok[pq];
             const float coef = P.pair_coef[pq];
             uint32_t x[28];
@@ -640,7 +902,7 @@ __device__ void phase_c(const StackArgs &a, const StackLayer &L, const float *hi
             }
             if (pad) x[24] = 0;
             if constexpr (PF::kOn) {  // this wavefront's image of the pair (prefetch_down)
-                const uint8_t *img = reinterpret_cast<const uint8_t *>(s_dyn) + kPrefOffset +
+                const uint8_t *img = reinterpret_cast<const uint8_t *>(s_dyn) +
                                      ((size_t)wave * MAXP + q) * PF::kWaveBytes;
 #pragma unroll
                 for (int rr = 0; rr < RG; ++rr)
@@ -664,12 +926,12 @@ __device__ void phase_c(const StackArgs &a, const StackLayer &L, const float *hi
     // team combine: the last member sums the members' partials in order
     wait_own_stores();
     __syncthreads();
-    if (threadIdx.x == 0) P.last = counter_arrive(&a.sync->team[tau]) == K - 1 ? 1 : 0;
+    if (tid() == 0) P.last = counter_arrive(&a.sync->team[tau]) == K - 1 ? 1 : 0;
     __syncthreads();
     if (!P.last) return;
     float *s_red = reinterpret_cast<float *>(s_x);  // [MT][64] squares
     const uint32_t m = a.m;
-    for (uint32_t i = threadIdx.x; i < MT * 64; i += kThreads) {
+    for (uint32_t i = tid(); i < MT * 64; i += kThreads) {
         const uint32_t tt = i / 64, row = i % 64;
         float sq = 0.0f;
         if (tt < m) {
@@ -696,16 +958,16 @@ __device__ void phase_c(const StackArgs &a, const StackLayer &L, const float *hi
         const float v = group_reduce<64>(s_red[wave * 64 + lane], AddOp());
         if (lane == 0 && wave < (int)m) store_coherent(&a.ssq[tau * MT + wave], v);
     }
-    if (threadIdx.x == 0) counter_reset(&a.sync->team[tau]);
+    if (tid() == 0) counter_reset(&a.sync->team[tau]);
 }
 
 // sum of squares of h rows of the team (prologue for the first layer)
 __device__ void team_ssq(const StackArgs &a) {
     float *s_red = reinterpret_cast<float *>(s_dyn);
     const uint32_t tau = blockIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int lane = threadIdx.x % kWave;
-    for (uint32_t i = threadIdx.x; i < MT * 64; i += kThreads) {
+    const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
+    const int lane = tid() % kWave;
+    for (uint32_t i = tid(); i < MT * 64; i += kThreads) {
         const uint32_t tt = i / 64, row = i % 64;
         float v = 0.0f;
         if (tt < a.m) v = load_coherent(&a.h_in[(size_t)tt * H + tau * 64 + row]);
@@ -734,51 +996,76 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
         const uint8_t *mp[kPtrPer];
 #pragma unroll
         for (int i = 0; i < kPtrPer; ++i) {
-            const uint32_t k = threadIdx.x + (uint32_t)i * kThreads;
+            const uint32_t k = tid() + (uint32_t)i * kThreads;
             mp[i] = load_global_ptr(L.mats + (k < (a.E + 1) * 3 ? k : 0));
         }
         phase_a(a, L, hin);
 #pragma unroll
         for (int i = 0; i < kPtrPer; ++i) {
-            const uint32_t k = threadIdx.x + (uint32_t)i * kThreads;
+            const uint32_t k = tid() + (uint32_t)i * kThreads;
             if (k < (a.E + 1) * 3) s_mats[k] = mp[i];
         }
         if (!(ok = grid_sync(a.sync, epoch, a.status))) break;
         UnitLoads U;
+        SharedLoads S;
         bool pre;
-        compute_routes(a, U, pre);
-        if (blockIdx.x == 0 && threadIdx.x < a.m * kTopK) {
-            const uint32_t t = threadIdx.x / kTopK, kk = threadIdx.x % kTopK;
+        compute_routes<LPRD, MAXP>(a, L, U, S, pre);
+        if (blockIdx.x == 0 && tid() < a.m * kTopK) {
+            const uint32_t t = tid() / kTopK, kk = tid() % kTopK;
             if (a.ids_out) a.ids_out[((size_t)l * a.m + t) * kTopK + kk] = P.bad ? 0 : (uint16_t)P.ids[t][kk];
             if (a.w_out) a.w_out[((size_t)l * a.m + t) * kTopK + kk] = P.bad ? 0.0f : P.w[t][kk];
         }
-        if (blockIdx.x == 0 && threadIdx.x == 0 && P.bad && a.status)
+        if (blockIdx.x == 0 && tid() == 0 && P.bad && a.status)
             __hip_atomic_store(a.status, (int32_t)TQF_HIP_ERR_ROUTER, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
-        const int n_units = P.n_groups * (int)(a.F / 32);
-        bool prefetch = true;  // with the first unit's loads, or alone
-        for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
-            gate_up_unit<LPRD, MAXP>(a, L, u, prefetch, U, pre && u == (int)blockIdx.x);
-            prefetch = false;
+        const int n_units = P.n_groups > 0 ? (int)a.m * kTopK * (int)(a.F / 64) : 0;
+        // the preloaded first unit (pre holds exactly when blockIdx.x <
+        // n_units); both branches use U, so no path leaves its loads pending
+        if (pre) {
+            gate_up_unit<LPRD, MAXP>(a, unit_desc(blockIdx.x, (int)a.F, (int)a.m), U, true);
+        } else {
+#pragma unroll
+            for (int n = 0; n < 8; ++n) {
+                consume(U.ng[n]);
+                consume(U.nu[n]);
+            }
+            consume(U.sg);
+            consume(U.su);
         }
-        if (prefetch) prefetch_down<LPRD, MAXP>(a);
-        if (!(ok = grid_sync(a.sync, epoch, a.status))) break;
+        for (int u = blockIdx.x + gridDim.x; u < n_units; u += gridDim.x)
+            gate_up_unit<LPRD, MAXP>(a, unit_desc(u, (int)a.F, (int)a.m), U, false);
+        // arrive once every load of phase B is consumed and this thread's
+        // record and row stores are complete (a compiler-visible wait, which
+        // also settles the compiler's own bookkeeping of those loads); then
+        // phase C's down weights stream while the barrier completes (issuing
+        // them stalls until the memory pipeline takes them, so they go out
+        // after the arrival)
+        grid_arrive(a.sync, epoch);
+        prefetch_down<LPRD, MAXP>(a);
+        if (!(ok = grid_wait(a.sync, epoch, a.status))) break;
         phase_c<LPRD, MAXP>(a, L, hin);
         if (l + 1 < a.n_layers && !(ok = grid_sync(a.sync, epoch, a.status))) break;
     }
     stack_exit(a.sync);
 }
 
+namespace {
+template <int LPRD>
+size_t lds_bytes_for(uint32_t maxp) {
+    return maxp <= 5 ? LdsLayout<LPRD, 5>::kTotal : LdsLayout<LPRD, 9>::kTotal;
+}
+}  // namespace
+
+// The most pairs a phase C member owns (member_share).
+uint32_t member_max_pairs(uint32_t members) {
+    return (MT + members - 1) / members + (MT * kTopK + members - 1) / members;
+}
+
 size_t stack_lds_bytes(uint32_t bp_down, uint32_t members) {
-    const size_t a = (size_t)MT * H * 4;                        // phase A: h rows
-    const size_t b = (size_t)MT * 7 * kBpGate * 16;             // phase B: x records
-    const uint32_t maxp = (MT * (kTopK + 1) + members - 1) / members;
-    const size_t c = (size_t)maxp * 7 * bp_down * 16;           // phase C: h records
-    size_t m = a > b ? a : b;
-    m = m > c ? m : c;
-    // the prefetching variant (pick: bp_down 16, maxp <= 5) adds its images
-    if (bp_down == 16 && maxp <= 5) m = (m > kPrefOffset ? m : kPrefOffset) + DownPrefetch<16, 5>::kBytes;
-    return m;
+    const uint32_t maxp = member_max_pairs(members);
+    if (bp_down == 16) return lds_bytes_for<16>(maxp);
+    if (bp_down == 32) return lds_bytes_for<32>(maxp);
+    return lds_bytes_for<64>(maxp);
 }
 
 namespace {
@@ -790,7 +1077,7 @@ const void *pick(uint32_t maxp, int &chosen) {
     return nullptr;
 }
 const void *kernel_for(uint32_t bp_down, uint32_t members) {
-    const uint32_t maxp = (MT * (kTopK + 1) + members - 1) / members;
+    const uint32_t maxp = member_max_pairs(members);
     int chosen = 0;
     if (bp_down == 16) return pick<16>(maxp, chosen);
     if (bp_down == 32) return pick<32>(maxp, chosen);
