@@ -212,8 +212,9 @@ int32_t tqf_hip_accept_device(tqf_hip_ctx *ctx, const float *d_target, const flo
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
  * same kernels and results as tqf_hip_accept_device, with their scratch in a
  * fixed per-GPU array of 256 KiB (held until the process ends) instead of a
- * context allocation: k and vocab whose scratch exceeds it (vocab above about
- * 3.4 million at k = 7) are TQF_HIP_ERR_INVALID.  Every call on one GPU
+ * context allocation.  It holds the one-launch acceptance kernel's scratch
+ * (vocab up to 1,048,576 at k <= 3 and 524,288 at k >= 4 on MI355X); larger
+ * vocabularies, whose kernels need more, are TQF_HIP_ERR_INVALID.  Every call on one GPU
  * shares that array, so calls that overlap on one GPU (from two contexts or
  * two streams) race; calls ordered on one stream do not.  The entry point
  * calls no hipMalloc, hipFree or other allocating routine, and records no

@@ -193,3 +193,55 @@ def test_matches_committed_golden(backend):
             a, toks = backend.accept(target, draft, dtok, 0.7, greedy, u, ur)
             assert a == g["accept_len"][gi, seed], (greedy, seed)
             assert toks == list(g["accept_tokens"][gi, seed, : a + 1]), (greedy, seed)
+
+
+def test_launch_paths_alternate_on_one_context(backend):
+    """Calls that take the one-launch kernel (every chunk's workgroup resident
+    at once) and calls whose vocab is beyond its grid (the three-kernel path)
+    interleave on one context and its scratch, each equal to the oracle."""
+    for k, vocab, seed in ((3, V, 21), (1, 1_100_000, 22), (3, V, 23), (7, 600_000, 24),
+                           (7, 20_000, 25), (0, 1_100_000, 26), (3, 600_000, 27), (3, V, 21)):
+        target, draft, dtok, u, ur = case(seed, k=k, vocab=vocab, noise=0.5)
+        for greedy in (False, True):
+            got = backend.accept(target, draft, dtok, 0.7, greedy, u, ur)
+            assert got == orc.accept(target, draft, dtok, 0.7, greedy, u, ur), (k, vocab, greedy)
+
+
+@pytest.mark.parametrize("vocab", [3000, 150_000])
+def test_rejection_without_residual_mass(backend, vocab):
+    """A rejected pair whose residual max(0, p - q) is zero everywhere (target
+    row = draft row, the draft token impossible under both): the replacement
+    is drawn from the target row itself; with no mass in that row either
+    (every logit NaN), it is the row's arg-max (token 0 without candidates)."""
+    rng = np.random.default_rng(31)
+    k = 2
+    draft = (rng.standard_normal((k, vocab)) * 3).astype(np.float32)
+    target = np.concatenate([draft, (rng.standard_normal((1, vocab)) * 3).astype(np.float32)])
+    bad = vocab // 2 + 7
+    target[0, bad] = draft[0, bad] = -np.inf
+    u = np.array([0.3, 0.3], np.float32)
+    for ur0 in (0.0, 0.37, 0.999):
+        ur = np.array([ur0, 0.5, 0.5], np.float32)
+        got = backend.accept(target, draft, [bad, 1], 0.7, False, u, ur)
+        assert got[0] == 0
+        assert got == orc.accept(target, draft, [bad, 1], 0.7, False, u, ur), ur0
+    target[0, :] = np.nan
+    draft[0, :] = np.nan
+    ur = np.array([0.6, 0.5, 0.5], np.float32)
+    got = backend.accept(target, draft, [bad, 1], 0.7, False, u, ur)
+    assert got == (0, [0]) == orc.accept(target, draft, [bad, 1], 0.7, False, u, ur)
+
+
+@pytest.mark.parametrize("T", [2.0 ** -31, 2.0 ** -29, 0.01, 0.1, 0.37, 0.7, 1.0, 1.7, 3.3, 100.0,
+                               2.0 ** 29, 2.0 ** 31])
+def test_temperatures_across_the_division_paths(backend, T):
+    """Temperatures inside [2^-30, 2^30] take the launch-wide reciprocal form
+    of (l - M) / T, the others the per-element division; every one must match
+    the oracle's IEEE division bit for bit."""
+    for seed in range(3):
+        target, draft, dtok, u, ur = case(200 + seed, k=3, vocab=20000, noise=0.5)
+        scale = np.float32(min(max(T, 1e-3), 1e3))  # logit spreads comparable to T
+        target = (target * scale).astype(np.float32)
+        draft = (draft * scale).astype(np.float32)
+        got = backend.accept(target, draft, dtok, T, False, u, ur)
+        assert got == orc.accept(target, draft, dtok, T, False, u, ur), (T, seed)
