@@ -70,6 +70,9 @@ int32_t tqf_hip_buffer_alloc(tqf_hip_ctx *ctx, size_t bytes, void **dptr);
 int32_t tqf_hip_buffer_free(tqf_hip_ctx *ctx, void *dptr);
 int32_t tqf_hip_memcpy_h2d(tqf_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
 int32_t tqf_hip_memcpy_d2h(tqf_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Device-to-device copy ordered on the context's stream (not waited for):
+ * the copies a decode loop makes between stages (the MTP loop's h_prev row). */
+int32_t tqf_hip_memcpy_d2d(tqf_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
 
 /* ---- Q4_0 weights: GpuResidentExpert::upload (backend/metal/expert.rs:
  *      110-147) ------------------------------------------------------------- */
@@ -342,6 +345,23 @@ int32_t tqf_hip_lm_head_logits(tqf_hip_ctx *ctx, const tqf_hip_weights *w, const
 int32_t tqf_hip_lm_head_logits_device(tqf_hip_ctx *ctx, const tqf_hip_weights *w,
                                       const float *d_x, uint32_t m, float *d_logits,
                                       uint32_t *d_tokens4, float *d_logits4);
+
+/* ---- the decode loop's row kernels ------------------------------------------
+ * Embedding rows (Qwen36Runtime::decode_step's embedding.row,
+ * model/qwen36/runtime.rs:403; the row decoded per its dtype as
+ * LoadedQwen36Tensor::row, model/qwen36/weights.rs:346-379): d_out[i] =
+ * dequantize_q4_0(row d_tokens[i] of emb) (+ d_add[i] when d_add is given),
+ * [n x cols] f32.  emb is a Q4_0 handle [V x cols].  A token outside [0, V)
+ * gives a NaN row and, when d_status is given, TQF_HIP_ERR_INVALID there
+ * (the reference's ModelError::Shape, runtime.rs:392-399). */
+int32_t tqf_hip_embed_rows_device(tqf_hip_ctx *ctx, const tqf_hip_weights *emb, const int32_t *d_tokens,
+                                  uint32_t n, const float *d_add, float *d_out, int32_t *d_status);
+/* RMSNorm rows: the final norm ahead of the LM head (runtime.rs:430-431,
+ * Qwen36Activation::qwen_rmsnorm): d_out[i] = d_x[i] * (1 / sqrt(mean(d_x[i]^2)
+ * + 1e-6)) * w, [n x cols] f32, w a tensor of cols floats.  The sum of squares
+ * is a block reduction (its order is not the scalar loop's). */
+int32_t tqf_hip_rmsnorm_rows_device(tqf_hip_ctx *ctx, const float *d_x, uint32_t n, uint32_t cols,
+                                    const tqf_hip_tensor *w, float *d_out);
 
 /* ---- one MTP verify step: the stack over the k+1 verify rows, then the
  *      acceptance, as one stream-ordered (graph-replayed) unit.  The verify

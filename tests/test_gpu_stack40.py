@@ -13,42 +13,18 @@ from the oracle's own f32 router and from_logits first), downloaded from the
 device.  Tolerances as everywhere: routes bit-equal, route weights within
 1e-5, h within 1e-3 of |g - c| / max(|c|, 1) (backend/metal/expert.rs:309);
 acceptance decisions and tokens bit-exact."""
-import os
-
 import numpy as np
 import pytest
 
 import cpu_oracle as orc
 from conftest import rel_err
+from stack_oracle import oracle_replay
 from turboqwenfare_amd import _lib, mtp, synth
-from turboqwenfare_amd.workloads import E, F, H, SyntheticStack
+from turboqwenfare_amd.workloads import H, SyntheticStack
 
 pytestmark = pytest.mark.gpu
 
 LAYERS = 40
-THREADS = max(1, min(16, len(os.sched_getaffinity(0))))
-
-
-def oracle_replay(model: SyntheticStack, h0: np.ndarray):
-    """Host oracle of the stack over h0 [m, H]: (h, ids [L, m, 8], w [L, m, 8])."""
-    h = np.array(h0, dtype=np.float32, copy=True)
-    m = h.shape[0]
-    blank = np.zeros(F * (H // 32) * 18, np.uint8)  # gate/up and down have the same byte size
-    routes, weights = [], []
-    for l in range(model.n_layers):
-        router, gate, norm = model.host_f32[l]
-        xn = np.stack([orc.qwen_rmsnorm(h[t], norm) for t in range(m)])
-        ids = np.stack([orc.router_from_logits(orc.f32_matvec(router, xn[t]))[0] for t in range(m)])
-        g, u, d = [blank] * E, [blank] * E, [blank] * E
-        for e in sorted(set(int(v) for v in ids.reshape(-1))):
-            g[e], u[e], d[e] = model.expert_q4_0(l, e)
-        host = orc.MoeLayerHost(router, gate, *model.expert_q4_0(l, E), g, u, d)
-        y, ids2, w = host.forward_batch(xn, nthreads=THREADS)
-        assert np.array_equal(ids, ids2)
-        h = (h + y).astype(np.float32)
-        routes.append(ids2)
-        weights.append(w)
-    return h, np.stack(routes), np.stack(weights)
 
 
 @pytest.fixture(scope="module", params=["zero_mean", "uniform"])

@@ -79,6 +79,7 @@ SIGNATURES = {
     "tqf_hip_buffer_free": (_i32, [_vp, _vp]),
     "tqf_hip_memcpy_h2d": (_i32, [_vp, _vp, _vp, _sz]),
     "tqf_hip_memcpy_d2h": (_i32, [_vp, _vp, _vp, _sz]),
+    "tqf_hip_memcpy_d2d": (_i32, [_vp, _vp, _vp, _sz]),
     "tqf_hip_weights_bytes_for": (_u64, [_u32, _u32]),
     "tqf_hip_weights_upload": (_i32, [_vp, _vp, _sz, _u32, _u32, _pp]),
     "tqf_hip_weights_upload_device": (_i32, [_vp, _vp, _sz, _u32, _u32, _pp]),
@@ -126,6 +127,8 @@ SIGNATURES = {
     "tqf_hip_top_logit_candidates": (_i32, [_vp, _vp, _u32, _u32, _vp, _vp]),
     "tqf_hip_grouped_gemm": (_i32, [_vp, _vp, _vp, _u32, _vp, _vp, _vp]),
     "tqf_hip_grouped_gemm_device": (_i32, [_vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp]),
+    "tqf_hip_embed_rows_device": (_i32, [_vp, _vp, _vp, _u32, _vp, _vp, _vp]),
+    "tqf_hip_rmsnorm_rows_device": (_i32, [_vp, _vp, _u32, _u32, _vp, _vp]),
     "tqf_hip_verify_step_device": (
         _i32, [_vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _u32, _f32, _i32, _vp, _vp, _vp, _vp,
                _vp]),

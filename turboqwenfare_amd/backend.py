@@ -145,6 +145,19 @@ class HipBackend:
             raise ValueError("array larger than the device buffer")
         self._check(self.lib.tqf_hip_memcpy_h2d(self.ctx, buf.ptr, _ptr(a), a.nbytes))
 
+    def copy_device(self, dst: DeviceBuffer, src: DeviceBuffer, nbytes: int) -> None:
+        """Stream-ordered device-to-device copy of nbytes."""
+        if nbytes > dst.nbytes or nbytes > src.nbytes:
+            raise ValueError("copy larger than a buffer")
+        self._check(self.lib.tqf_hip_memcpy_d2d(self.ctx, dst.ptr, src.ptr, nbytes))
+
+    @staticmethod
+    def view(buf: DeviceBuffer, offset: int, nbytes: int) -> DeviceBuffer:
+        """A sub-range of a buffer (not to be freed on its own)."""
+        if offset < 0 or offset + nbytes > buf.nbytes:
+            raise ValueError("view outside the buffer")
+        return DeviceBuffer(buf.ptr + offset, nbytes)
+
     def read(self, buf: DeviceBuffer, dtype, shape) -> np.ndarray:
         out = np.empty(shape, dtype=dtype)
         self._check(self.lib.tqf_hip_memcpy_d2h(self.ctx, _ptr(out), buf.ptr, out.nbytes))
@@ -467,6 +480,20 @@ class HipBackend:
             self.ctx, st.handle, d_h_in.ptr if d_h_in else None, d_h.ptr, m,
             d_ids.ptr if d_ids else None, d_w.ptr if d_w else None,
             d_status.ptr if d_status else None))
+
+    def embed_rows_device(self, emb: Q4Weights, d_tokens: DeviceBuffer, n: int, d_out: DeviceBuffer,
+                          d_add: DeviceBuffer | None = None,
+                          d_status: DeviceBuffer | None = None) -> None:
+        """d_out [n x cols] = Q4_0 rows d_tokens of emb (+ d_add)."""
+        self._check(self.lib.tqf_hip_embed_rows_device(
+            self.ctx, emb.handle, d_tokens.ptr, n, d_add.ptr if d_add else None, d_out.ptr,
+            d_status.ptr if d_status else None))
+
+    def rmsnorm_rows_device(self, d_x: DeviceBuffer, n: int, cols: int, w: F32Tensor,
+                            d_out: DeviceBuffer) -> None:
+        """d_out [n x cols] = qwen_rmsnorm of each row of d_x with weight w."""
+        self._check(self.lib.tqf_hip_rmsnorm_rows_device(self.ctx, d_x.ptr, n, cols, w.handle,
+                                                         d_out.ptr))
 
     def verify_step_device(self, st: Stack, d_h_in: DeviceBuffer | None, d_h: DeviceBuffer,
                            m: int, d_target: DeviceBuffer, d_draft: DeviceBuffer | None,

@@ -730,6 +730,14 @@ extern "C" int32_t tqf_hip_memcpy_d2h(tqf_hip_ctx *ctx, void *dst, const void *s
     return TQF_HIP_OK;
 }
 
+extern "C" int32_t tqf_hip_memcpy_d2d(tqf_hip_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    TQF_ENTER(ctx);
+    if (bytes == 0) return TQF_HIP_OK;
+    if (!dst || !src) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    TQF_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    return TQF_HIP_OK;
+}
+
 // ===========================================================================
 // weights
 // ===========================================================================
@@ -1730,6 +1738,30 @@ extern "C" int32_t tqf_hip_accept_device(tqf_hip_ctx *ctx, const float *d_target
     if (int32_t rc = ensure_accept_scratch(ctx, accept_scratch_bytes(k, vocab))) return rc;
     return enqueue_accept(ctx, d_target, d_draft, d_draft_tokens, k, vocab, temperature, greedy,
                           d_u, d_ures, d_accepted, d_tokens);
+}
+
+extern "C" int32_t tqf_hip_embed_rows_device(tqf_hip_ctx *ctx, const tqf_hip_weights *emb,
+                                             const int32_t *d_tokens, uint32_t n, const float *d_add,
+                                             float *d_out, int32_t *d_status) {
+    TQF_ENTER(ctx);
+    if (!valid_weights(emb) || !d_tokens || !d_out) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (emb->format != TQF_HIP_FORMAT_Q4_0)
+        return fail(ctx, TQF_HIP_ERR_INVALID, "the embedding rows need a Q4_0 matrix");
+    if (n == 0) return TQF_HIP_OK;
+    hipError_t e = tqf::launch_embed_rows(ctx->stream, emb->tiles, emb->dims, d_tokens, n, d_add, d_out, d_status);
+    if (e != hipSuccess) return hip_fail(ctx, "embedding rows launch", e);
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_rmsnorm_rows_device(tqf_hip_ctx *ctx, const float *d_x, uint32_t n, uint32_t cols,
+                                               const tqf_hip_tensor *w, float *d_out) {
+    TQF_ENTER(ctx);
+    if (!d_x || !w || !w->data || !d_out) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (w->count != cols || cols == 0) return fail(ctx, TQF_HIP_ERR_INVALID, "norm weight length != cols");
+    if (n == 0) return TQF_HIP_OK;
+    hipError_t e = tqf::launch_rmsnorm_rows(ctx->stream, d_x, n, cols, w->data, d_out);
+    if (e != hipSuccess) return hip_fail(ctx, "rmsnorm rows launch", e);
+    return TQF_HIP_OK;
 }
 
 extern "C" int32_t tqf_hip_accept_device_noalloc(tqf_hip_ctx *ctx, const float *d_target,

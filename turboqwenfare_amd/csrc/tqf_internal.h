@@ -430,6 +430,10 @@ hipError_t launch_gate_up(hipStream_t s, const LayerDev &L, uint32_t slots, cons
 hipError_t launch_down(hipStream_t s, const LayerDev &L, uint32_t m, uint32_t slots, Scratch &sc,
                        const Plan *plan, const uint32_t *hprep, const float *resid, float *out);
 size_t accept_scratch_bytes(uint32_t k, uint32_t vocab);
+hipError_t launch_embed_rows(hipStream_t s, const uint8_t *tiles, const MatrixDims &d, const int32_t *tokens,
+                             uint32_t n, const float *add, float *out, int32_t *status);
+hipError_t launch_rmsnorm_rows(hipStream_t s, const float *x, uint32_t n, uint32_t cols, const float *w,
+                               float *out);
 hipError_t launch_accept(hipStream_t s, const float *target, const float *draft,
                          const int32_t *dtok, uint32_t k, uint32_t vocab, float temperature,
                          int32_t greedy, const float *u, const float *ures, int32_t *accepted,

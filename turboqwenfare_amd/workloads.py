@@ -43,10 +43,10 @@ class SyntheticStack:
     every expert matrix ("uniform" or "zero_mean", ``synth.q4_0_synthetic``)."""
 
     def __init__(self, be, n_layers: int, seed: int = 0, recipe: str = "zero_mean",
-                 log=None):
+                 log=None, first_layer: int = 0):
         self.be, self.n_layers, self.seed, self.recipe = be, n_layers, seed, recipe
         self.layers, self.norms, self.mats, self.host_f32 = [], [], [], []
-        for l in range(n_layers):
+        for l in range(first_layer, first_layer + n_layers):
             mats = []
             for e in range(E + 1):
                 tg, tu, td = expert_tensor_ids(l, e)
@@ -60,10 +60,11 @@ class SyntheticStack:
             self.norms.append(be.upload_f32(norm))
             self.mats.append(mats)
             self.host_f32.append((router, gate, norm))
-            if log and (l + 1) % 10 == 0:
-                log(f"{l + 1}/{n_layers} layers resident")
+            if log and (l - first_layer + 1) % 10 == 0:
+                log(f"{l - first_layer + 1}/{n_layers} layers resident")
         self.stack = be.prepare_stack(self.layers, self.norms)
 
+    # layer indices below are positions in this stack (0 .. n_layers - 1)
     def expert_q4_0(self, layer: int, expert: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
         """GGML Q4_0 bytes of one expert's gate, up and down (device download)."""
         return tuple(self.be.download_q4_0(w) for w in self.mats[layer][expert])
