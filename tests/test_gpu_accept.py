@@ -245,3 +245,50 @@ def test_temperatures_across_the_division_paths(backend, T):
         draft = (draft * scale).astype(np.float32)
         got = backend.accept(target, draft, dtok, T, False, u, ur)
         assert got == orc.accept(target, draft, dtok, T, False, u, ur), (T, seed)
+
+
+def _softmax64(row, T):
+    z = np.exp((row.astype(np.float64) - row.max()) / T)
+    return z / z.sum()
+
+
+def test_draw_frequencies_follow_p(backend):
+    """The acceptance's own draw (k = 0: the bonus token, and the MTP loop's
+    stochastic selection), whose definition departs from Sampler::select's
+    sorted running-sum draw (sampling/mod.rs:166-190, 227-248): its
+    frequencies over 20,000 uniforms follow p = softmax(l / T) (chi-square,
+    5 degrees of freedom)."""
+    V, T, n = 6, 0.7, 20_000
+    target = np.array([[2.0, 1.0, 0.5, 0.0, -1.0, 1.5]], np.float32)
+    p = _softmax64(target[0], T)
+    ur = synth.philox_uniforms(77, 1, n)
+    counts = np.zeros(V)
+    empty = np.zeros((0, V), np.float32)
+    for i in range(n):
+        a, toks = backend.accept(target, empty, [], T, False, np.zeros(0, np.float32),
+                                 ur[i:i + 1])
+        counts[toks[0]] += 1
+    chi2 = float(np.sum((counts - n * p) ** 2 / (n * p)))
+    print(f"draw chi2 {chi2:.2f}, counts {counts.astype(int).tolist()}")
+    assert chi2 < 25.0  # P(chi2 > 25) ~ 1e-4 at 5 degrees of freedom
+
+
+def test_speculative_emission_follows_p(backend):
+    """With d ~ q, the first emitted token is distributed as p: the
+    speculative-sampling identity, on the device path."""
+    V, T, n = 6, 0.7, 20_000
+    target = np.array([[2.0, 1.0, 0.5, 0.0, -1.0, 1.5], [0, 0, 0, 0, 0, 0]], np.float32)
+    draft = np.array([[0.0, 2.0, 1.0, 0.5, 0.0, -2.0]], np.float32)
+    p, q = _softmax64(target[0], T), _softmax64(draft[0], T)
+    uq = synth.philox_uniforms(78, 2, n)
+    u = synth.philox_uniforms(78, 0, n)
+    ur = synth.philox_uniforms(78, 1, 2 * n)
+    cq = np.cumsum(q)
+    counts = np.zeros(V)
+    for i in range(n):
+        d = int(min(np.searchsorted(cq, float(uq[i]), side="right"), V - 1))
+        _, toks = backend.accept(target, draft, [d], T, False, u[i:i + 1], ur[2 * i:2 * i + 2])
+        counts[toks[0]] += 1
+    chi2 = float(np.sum((counts - n * p) ** 2 / (n * p)))
+    print(f"speculative chi2 {chi2:.2f}, counts {counts.astype(int).tolist()}")
+    assert chi2 < 25.0

@@ -1279,6 +1279,15 @@ bool fuse_fits(uint32_t k, uint32_t vocab) {
     }
 }
 
+// The device queries behind the launch choice, made once per process outside
+// any stream capture (at context creation).
+void accept_warm() {
+    (void)fuse_ept(0);
+    (void)fuse_max_grid<3>();
+    (void)fuse_max_grid<7>();
+    (void)fuse_max_grid<15>();
+}
+
 size_t accept_scratch_bytes(uint32_t k, uint32_t vocab) {
     return fuse_fits(k, vocab) ? fuse_layout(k, vocab, fuse_ept(vocab)).total : acc_layout(k, vocab).total;
 }

@@ -604,6 +604,7 @@ extern "C" int32_t tqf_hip_create(int32_t device, tqf_hip_ctx **out) {
         delete ctx;
         return TQF_HIP_ERR_DEVICE;
     }
+    tqf::accept_warm();  // device queries of the acceptance launch, outside any capture
     static const char *const kVariantEnv[TQF_HIP_VARIANTS] = {"TQF_HIP_PERSISTENT", "TQF_HIP_Q4K_FOLD",
                                                               "TQF_HIP_GRAPHS"};
     for (int i = 0; i < TQF_HIP_VARIANTS; ++i) {

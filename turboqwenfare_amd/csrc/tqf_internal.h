@@ -430,6 +430,7 @@ hipError_t launch_gate_up(hipStream_t s, const LayerDev &L, uint32_t slots, cons
 hipError_t launch_down(hipStream_t s, const LayerDev &L, uint32_t m, uint32_t slots, Scratch &sc,
                        const Plan *plan, const uint32_t *hprep, const float *resid, float *out);
 size_t accept_scratch_bytes(uint32_t k, uint32_t vocab);
+void accept_warm();
 hipError_t launch_embed_rows(hipStream_t s, const uint8_t *tiles, const MatrixDims &d, const int32_t *tokens,
                              uint32_t n, const float *add, float *out, int32_t *status);
 hipError_t launch_rmsnorm_rows(hipStream_t s, const float *x, uint32_t n, uint32_t cols, const float *w,
