@@ -12,13 +12,16 @@ from turboqwenfare_amd.workloads import E, F, H
 THREADS = max(1, min(16, len(os.sched_getaffinity(0))))
 
 
-def oracle_replay(model, h0: np.ndarray):
-    """(h [m, H], route ids [L, m, 8], route weights [L, m, 8]) of the stack over h0 [m, H]."""
+def oracle_replay(model, h0: np.ndarray, inputs: list | None = None):
+    """(h [m, H], route ids [L, m, 8], route weights [L, m, 8]) of the stack over h0 [m, H];
+    `inputs`, when given, receives each layer's input h."""
     h = np.array(h0, dtype=np.float32, copy=True)
     m = h.shape[0]
     blank = np.zeros(F * (H // 32) * 18, np.uint8)  # gate/up and down have the same byte size
     routes, weights = [], []
     for l in range(model.n_layers):
+        if inputs is not None:
+            inputs.append(h.copy())
         router, gate, norm = model.host_f32[l]
         xn = np.stack([orc.qwen_rmsnorm(h[t], norm) for t in range(m)])
         ids = np.stack([orc.router_from_logits(orc.f32_matvec(router, xn[t]))[0] for t in range(m)])

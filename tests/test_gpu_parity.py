@@ -398,7 +398,10 @@ def test_persistent_stack_matches_oracle_and_layer_kernels(backend, stack3, m):
     assert s_p == 0 and s_k == 0
     assert np.array_equal(ids_p, ids_k)
     assert rel_err(w_p, w_k) < 1e-5
-    assert rel_err(h_p, h_k) < 1e-4
+    # the persistent kernel scales the dot products of y = h * w_norm by
+    # 1/rms, the layer kernels normalise x first: the two round differently
+    # (this stack's rows reach |h| ~ 1e3), each within the oracle's bound
+    assert rel_err(h_p, h_k) < FFN_TOL
     hc, routes = oracle_stack(layers, norms, h0[:m])
     for l in range(3):
         assert np.array_equal(ids_p[l], routes[l])

@@ -10,9 +10,26 @@ The oracle replays h <- h + MoE_l(rmsnorm_l(h)) (model/qwen36/runtime.rs:
 777-802, experts/mod.rs:1540-1577) layer by layer; each layer's host copy
 holds only that layer's routed experts and the shared one (the routes come
 from the oracle's own f32 router and from_logits first), downloaded from the
-device.  Tolerances as everywhere: routes bit-equal, route weights within
-1e-5, h within 1e-3 of |g - c| / max(|c|, 1) (backend/metal/expert.rs:309);
-acceptance decisions and tokens bit-exact."""
+device.  Routes must be bit-equal at every layer and route weights within
+1e-5; acceptance decisions and tokens bit-exact.
+
+h is checked two ways:
+- layer by layer, teacher-forced: each layer run alone (a one-layer stack
+  over the same resident layer) from the oracle's input to that layer, within
+  1e-3 of |g - c| / max(|c|, 1) (backend/metal/expert.rs:309), the
+  reference's own per-layer tolerance;
+- end to end over 40 layers, within 4x the oracle's own spread at that depth
+  (tests/golden/stack40_spread.json, made by make_stack40_spread.py: the
+  oracle's final h moves by 3.7e-4 to 4.6e-4 on the zero-mean stack when
+  rounding-level noise, 2^-24 relative, enters before every layer; by ~1e-6
+  on the uniform one).  The device rounds differently from the oracle at
+  every layer (its activation records hold 24 bits relative to each 32-value
+  block's maximum, a per-value rounding several times f32's), so its
+  end-to-end distance sits at a small multiple of that spread; a fixed 1e-3
+  is at the zero-mean stack's conditioning floor."""
+import json
+from pathlib import Path
+
 import numpy as np
 import pytest
 
@@ -25,12 +42,18 @@ from turboqwenfare_amd.workloads import H, SyntheticStack
 pytestmark = pytest.mark.gpu
 
 LAYERS = 40
+SPREAD = json.loads((Path(__file__).parent / "golden" / "stack40_spread.json").read_text())
+
+
+def h_bound(recipe: str, m: int) -> float:
+    """4x the oracle's largest 40-layer spread under every-layer rounding noise."""
+    return 4.0 * max(SPREAD[f"{recipe}_m{m}_every_layer"])
 
 
 @pytest.fixture(scope="module", params=["zero_mean", "uniform"])
 def model40(request, backend):
     model = SyntheticStack(backend, LAYERS, seed=0, recipe=request.param)
-    model.oracle = {}
+    model.oracle, model.inputs = {}, {}
     yield model
     model.free()
 
@@ -41,19 +64,23 @@ def h0_rows(m: int) -> np.ndarray:
 
 def oracle_for(model, m):
     if m not in model.oracle:
-        model.oracle[m] = oracle_replay(model, h0_rows(m))
+        inputs = []
+        model.oracle[m] = oracle_replay(model, h0_rows(m), inputs)
+        model.inputs[m] = inputs
     return model.oracle[m]
 
 
-def run_stack(be, model, m, persistent):
+def run_stack(be, model, m, persistent, stack=None, h0=None):
+    stack = stack or model.stack
+    n = len(stack.layers)
     with be.variant(_lib.VARIANT_PERSISTENT, persistent):
-        dh = be.to_device(h0_rows(m))
-        dids = be.alloc(LAYERS * m * 8 * 2)
-        dw = be.alloc(LAYERS * m * 8 * 4)
+        dh = be.to_device(h0_rows(m) if h0 is None else h0)
+        dids = be.alloc(n * m * 8 * 2)
+        dw = be.alloc(n * m * 8 * 4)
         dst = be.to_device(np.zeros(1, np.int32))
-        be.stack_forward_device(model.stack, dh, m, dids, dw, dst)
-        out = (be.read(dh, np.float32, (m, H)), be.read(dids, np.uint16, (LAYERS, m, 8)),
-               be.read(dw, np.float32, (LAYERS, m, 8)), int(be.read(dst, np.int32, (1,))[0]))
+        be.stack_forward_device(stack, dh, m, dids, dw, dst)
+        out = (be.read(dh, np.float32, (m, H)), be.read(dids, np.uint16, (n, m, 8)),
+               be.read(dw, np.float32, (n, m, 8)), int(be.read(dst, np.int32, (1,))[0]))
         for b in (dh, dids, dw, dst):
             be.free(b)
     return out
@@ -73,10 +100,35 @@ def test_stack40_matches_oracle(backend, model40, m, persistent):
     print(f"{model40.recipe} m={m} {'persistent' if persistent else 'per-layer'}: h rel err "
           f"{err:.3e}, |h| rms {np.sqrt(np.mean(hc.astype(np.float64) ** 2)):.2f}, union mean "
           f"{np.mean(unions):.2f} min {min(unions)} max {max(unions)}")
-    assert err < 1e-3
+    assert err < h_bound(model40.recipe, m)
     if model40.recipe == "zero_mean" and m == 4:
         # the headline input stays an M = 4 workload at every depth
         assert np.mean(unions) >= 28 and min(unions) >= 24
+
+
+@pytest.mark.parametrize("m", [4, 1])
+@pytest.mark.parametrize("persistent", [True, False], ids=["persistent", "per_layer"])
+def test_stack40_layers_teacher_forced(backend, model40, m, persistent):
+    """Every layer alone, from the oracle's input to it: routes bit-equal and
+    h within the reference's per-layer 1e-3."""
+    hc, idc, wc = oracle_for(model40, m)
+    inputs = model40.inputs[m]
+    worst = 0.0
+    for l in range(LAYERS):
+        one = backend.prepare_stack([model40.stack.layers[l]], [model40.stack.norms[l]])
+        try:
+            h, ids, w, status = run_stack(backend, model40, m, persistent, one, inputs[l])
+        finally:
+            backend.free_stack(one)
+        want = inputs[l + 1] if l + 1 < LAYERS else hc
+        assert status == 0, f"layer {l}"
+        assert np.array_equal(ids[0], idc[l]), f"layer {l} routes differ"
+        assert rel_err(w[0], wc[l]) < 1e-5, f"layer {l}"
+        err = rel_err(h, want)
+        worst = max(worst, err)
+        assert err < 1e-3, f"layer {l}: {err:.3e}"
+    print(f"{model40.recipe} m={m} {'persistent' if persistent else 'per-layer'}: worst "
+          f"teacher-forced layer {worst:.3e}")
 
 
 def test_stack40_unions_follow_the_recipe(backend, model40):

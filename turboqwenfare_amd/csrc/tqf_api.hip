@@ -220,7 +220,7 @@ int32_t ensure_stack_scratch(tqf_hip_ctx *ctx, uint32_t experts, uint32_t bp_dow
     bp_down = std::max(bp_down, sc.bp_down);
     members = std::max(members, sc.members);
     (void)hipFree(sc.sync);
-    (void)hipFree(sc.logits);
+    (void)hipFree(sc.lacc);
     (void)hipFree(sc.xprep);
     (void)hipFree(sc.hprep);
     (void)hipFree(sc.hshared);
@@ -229,11 +229,15 @@ int32_t ensure_stack_scratch(tqf_hip_ctx *ctx, uint32_t experts, uint32_t bp_dow
     sc = StackScratch();
     TQF_HIP(ctx, hipMalloc(&sc.sync, sizeof(StackSync)));
     TQF_HIP(ctx, hipMemset(sc.sync, 0, sizeof(StackSync)));
-    TQF_HIP(ctx, hipMalloc(&sc.logits, (size_t)kStackMT * (experts + 1) * 4));
+    // the accumulators start (and every launch leaves them) at zero
+    TQF_HIP(ctx, hipMalloc(&sc.lacc, 2 * (size_t)kLaccWords * 8));
+    TQF_HIP(ctx, hipMemset(sc.lacc, 0, 2 * (size_t)kLaccWords * 8));
     TQF_HIP(ctx, hipMalloc(&sc.xprep, (size_t)kStackMT * (kStackHidden / 32) * kXprepDwords * 4));
     TQF_HIP(ctx, hipMalloc(&sc.hprep, (size_t)kStackMT * (kTopK + 1) * bp_down * kXprepDwords * 4));
     TQF_HIP(ctx, hipMalloc(&sc.hshared, (size_t)kStackMT * bp_down * 32 * 4));
-    TQF_HIP(ctx, hipMalloc(&sc.partial, (size_t)kStackTeams * members * kStackMT * 64 * 4));
+    // tagged words: zero holds no launch's tag
+    TQF_HIP(ctx, hipMalloc(&sc.partial, (size_t)kStackTeams * members * kStackMT * 64 * 8));
+    TQF_HIP(ctx, hipMemset(sc.partial, 0, (size_t)kStackTeams * members * kStackMT * 64 * 8));
     TQF_HIP(ctx, hipMalloc(&sc.ssq, (size_t)kStackTeams * kStackMT * 4));
     TQF_HIP(ctx, hipMemset(sc.ssq, 0, (size_t)kStackTeams * kStackMT * 4));
     sc.experts = experts;
@@ -489,7 +493,7 @@ int32_t enqueue_stack_persistent(tqf_hip_ctx *ctx, const tqf_hip_stack *st, cons
     a.ids_out = d_ids;
     a.w_out = d_w;
     a.status = d_status;
-    a.logits = sc.logits;
+    a.lacc = sc.lacc;
     a.xprep = sc.xprep;
     a.hprep = sc.hprep;
     a.hshared = sc.hshared;
@@ -653,7 +657,7 @@ extern "C" int32_t tqf_hip_destroy(tqf_hip_ctx *ctx) {
     (void)hipFree(sc.counters);
     (void)hipFree(sc.accept);
     (void)hipFree(ctx->stack.sync);
-    (void)hipFree(ctx->stack.logits);
+    (void)hipFree(ctx->stack.lacc);
     (void)hipFree(ctx->stack.xprep);
     (void)hipFree(ctx->stack.hprep);
     (void)hipFree(ctx->stack.hshared);

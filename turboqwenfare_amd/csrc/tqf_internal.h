@@ -291,7 +291,7 @@ struct StackSync {
     uint32_t release;  // epoch released by the last arrival, and the abort flag:
     uint32_t abort;    // one 64-bit poll load, on its own cache line
     uint32_t pad1[30];
-    uint32_t team[kStackTeams];
+    uint32_t seq;  // launches completed (every launch advances it once, at its exit)
 };
 struct StackArgs {
     const StackLayer *layers;
@@ -301,22 +301,25 @@ struct StackArgs {
     uint16_t *ids_out;
     float *w_out;
     int32_t *status;
-    float *logits;      // [kStackMT x (E + 1)]
+    uint64_t *lacc;     // [2][kLaccWords] router logits (2^-32 fixed point), by layer parity
     uint32_t *xprep;    // [kStackMT rows of 28 x 64 dwords]
     uint32_t *hprep;    // [9 kStackMT pair rows of 28 x bp_down dwords]
     float *hshared;     // [kStackMT x F] the shared expert's silu(g) * u rows
-    float *partial;     // [teams x members x kStackMT x 64]
+    uint64_t *partial;  // [teams x members x kStackMT x 64] tagged words (tag << 32 | f32 bits)
     float *ssq;         // [teams x kStackMT]
     StackSync *sync;
     uint32_t members;   // workgroups per 64-row team in phase C
 };
+// Words of one parity of the logit accumulator: kStackMT rows of the 256
+// routed experts and the shared-expert gate, then a non-finite flag.
+constexpr uint32_t kLaccWords = kStackMT * (256 + 1) + 1;
 struct StackScratch {
     StackSync *sync = nullptr;
-    float *logits = nullptr;
+    uint64_t *lacc = nullptr;
     uint32_t *xprep = nullptr;
     uint32_t *hprep = nullptr;
     float *hshared = nullptr;
-    float *partial = nullptr;
+    uint64_t *partial = nullptr;
     float *ssq = nullptr;
     uint32_t experts = 0, bp_down = 0, members = 0;
 };

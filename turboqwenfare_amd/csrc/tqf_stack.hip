@@ -3,38 +3,45 @@
 // One cooperative launch runs every layer of a stack over M <= 4 verify rows:
 //   h <- h + MoE_l(rmsnorm_l(h))        (model/qwen36/runtime.rs:777-802)
 // with MoE_l = shared expert * sigmoid(gate . x) + sum_k w_k expert_k(x) over
-// the router's top-8 (experts/mod.rs:1540-1634).  Per layer three phases are
-// separated by grid barriers (every workgroup is resident, one per CU):
+// the router's top-8 (experts/mod.rs:1540-1634).  Per layer two phases are
+// separated by grid barriers (every workgroup is resident, one per CU); the
+// input side of a layer (RMSNorm, router logits, activation records) is
+// produced by the previous layer's phase C (by a prologue for layer 0):
 //
-//   A  every workgroup: stages the M rows of h in LDS and derives their
-//      RMSNorm scale (the sum of squares comes from per-team partials written
-//      by the previous phase C); router row(s) (or the shared-expert input
-//      gate) with the columns split over its wavefronts; the first M x 32
-//      workgroups also write the activation records of the M x 64 blocks of
-//      x.
-//   B  every workgroup: the routes (softmax, stable top-8, renormalise;
-//      experts/mod.rs:134-197) from the logits on wavefronts 0..M-1 --
+//   B  every workgroup: 1/rms of the M rows from the per-team sums of
+//      squares; the router logits = 1/rms x the fixed-point sum of the
+//      teams' partial logits; the routes (softmax, stable top-8,
+//      renormalise; experts/mod.rs:134-197) on wavefronts 0..M-1 --
 //      computed identically in every workgroup, so the plan needs no further
-//      exchange -- then
-//      gate/up units of 64 rows (one row octet per wavefront) of one routed
-//      (expert, token) pair, with the activation records of every row in
-//      LDS; h = silu(g) * u is written as records per pair.  M = 4 tokens
-//      have 32 routed pairs: 256 units of equal work, one per workgroup (an
-//      expert two tokens chose is read twice, the second time mostly from
-//      the Infinity Cache).  The shared
-//      expert (all M tokens) is spread thinner: every workgroup takes two of
-//      its rows, one (row, token) per wavefront, and writes raw h values; the
-//      phase C member that owns the shared pairs turns them into records.
+//      exchange -- then gate/up units of 64 rows (one row octet per
+//      wavefront) of one routed (expert, token) pair, with the activation
+//      records of y = h * w_norm of every row in LDS (1/rms scales the dot
+//      products: rmsnorm(h) . W = (1/rms) (y . W)); h = silu(g) * u is
+//      written as records per pair.  M = 4 tokens have 32 routed pairs: 256
+//      units of equal work, one per workgroup.  The shared expert (all M
+//      tokens) is spread thinner: every workgroup takes two of its rows, one
+//      (row, token) per wavefront, and writes raw h values; the phase C
+//      member that owns the shared pairs turns them into records.
 //   C  teams of workgroups own 64 output rows each; a team member takes a
 //      contiguous share of the expert-sorted pair list (8 rows per
-//      wavefront, every weight load issued up front), and the last member to
-//      finish sums the members' partials in member order, adds the residual
-//      and writes h plus the team's sum of squares for the next layer.
+//      wavefront, every weight load issued up front) and publishes its
+//      partial rows as tagged words; every member polls all the team's
+//      words, sums them in member order and adds the residual (kept in
+//      registers across layers: each member holds the team's rows, the same
+//      bits in all of them), and the members share the next layer's inputs
+//      from the team's 64 rows: the sums of squares, the records of
+//      y = h * w_norm, and the partial router logits sum_c R[e][c] y[c] of
+//      every expert (member k: experts [k E / K, (k + 1) E / K)) and of the
+//      shared-expert gate, added into a 2^-32 fixed-point accumulator with
+//      integer atomics (exact, so the sum over teams does not depend on
+//      their order).  h itself is written once, after the last layer.
 //
 // Everything exchanged between workgroups is written with agent-scope
 // atomic stores and read with agent-scope atomic loads, and every thread
 // drains its stores (s_waitcnt) before the barrier arrival, so no L2
-// write-back / invalidate is needed.  Barrier waits are bounded in time: a
+// write-back / invalidate is needed.  (Workgroup-scope stores and loads do
+// not suffice even between the members of a team: their partial words were
+// not seen within the spin limit.)  Barrier waits are bounded in time: a
 // wait that exceeds kSpinLimit sets `abort`, after which every workgroup
 // leaves at its next barrier and the launch reports TQF_HIP_ERR_DEVICE; the
 // last workgroup to exit resets the barrier state for the next launch.
@@ -68,6 +75,7 @@ __device__ __forceinline__ void consume(const uint4 &v) {
 constexpr int kThreads = 512;  // 8 wavefronts
 constexpr int kWaves = kThreads / kWave;
 constexpr int MT = kStackMT;
+constexpr int kMaxMembers = 16;  // phase C workgroups per team
 constexpr int H = kStackHidden;
 constexpr int kBpGate = H / 32;        // 64 blocks per gate/up row: one per lane
 constexpr int64_t kSpinLimit = 2000000;  // wall-clock ticks (100 MHz): 20 ms
@@ -112,20 +120,16 @@ struct DownPrefetch {
     static constexpr uint32_t kBytes = kOn ? MAXP * kWaves * kWaveBytes : 0;
 };
 // Dynamic LDS, in phase order:
-//   [0, kHxBytes)            phase A: the M staged rows of h (read by the
-//                            phase B record builders too);
 //   [0, PF::kBytes)          from the arrival at the barrier before phase C
-//                            on: the prefetched down weights (the h rows are
-//                            dead by then);
+//                            on: the prefetched down weights;
 //   [xr, xr + kXrBytes)      phase B: the activation records of the M rows
 //                            (7 planes x 64 blocks x 16 B per row);
-//   [xr, ...)                phase C: the h records of the member's pairs.
-constexpr uint32_t kHxBytes = MT * H * 4;
+//   [xr, ...)                phase C: the h records of the member's pairs,
+//                            then the team tail's rows (2 x MT x 64 floats).
 constexpr uint32_t kXrBytes = MT * 7 * kBpGate * 16;
 template <int LPRD, int MAXP>
 struct LdsLayout {
-    static constexpr uint32_t kPf = DownPrefetch<LPRD, MAXP>::kBytes;
-    static constexpr uint32_t kXr = (kPf > kHxBytes ? kPf : kHxBytes);
+    static constexpr uint32_t kXr = DownPrefetch<LPRD, MAXP>::kBytes;
     static constexpr uint32_t kCStage = MAXP * 7 * LPRD * 16;
     static constexpr uint32_t kTotal = kXr + (kXrBytes > kCStage ? kXrBytes : kCStage);
 };
@@ -174,6 +178,29 @@ __device__ __forceinline__ void stage_coherent(uint64_t *dst, const uint64_t *sr
         const uint32_t k = tid() + (uint32_t)i * kThreads;
         if (k < n) dst[k] = v[i];
     }
+}
+
+// Zeroes this workgroup's share (workgroup `part` of `parts`) of one parity of
+// the accumulator.
+__device__ __forceinline__ void zero_lacc(uint64_t *acc, uint32_t part, uint32_t parts) {
+    for (uint32_t k = part * kThreads + tid(); k < kLaccWords; k += parts * kThreads)
+        __hip_atomic_store(acc + k, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Router logits travel between phases as 2^-32 fixed point in 64-bit words:
+// each team adds llrint(partial * 2^32) with an integer atomic, so the sum over
+// the 32 teams is exact and independent of their order; a non-finite (or
+// out-of-range) partial sets the accumulator's flag word instead.
+__device__ __forceinline__ void add_fixed(uint64_t *word, uint64_t *flag, float v) {
+    const double d = (double)v * 4294967296.0;
+    if (fabs(d) < 9.0e18) {
+        __hip_atomic_fetch_add(word, (uint64_t)__double2ll_rn(d), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        __hip_atomic_fetch_or(flag, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+__device__ __forceinline__ float logit_of(uint64_t fixed, float inv_rms) {
+    return (float)((double)(int64_t)fixed * 0x1p-32 * (double)inv_rms);
 }
 
 // ---- grid barrier ------------------------------------------------------------
@@ -259,91 +286,24 @@ __device__ bool grid_sync(StackSync *sync, uint32_t &epoch, int32_t *status) {
 }
 
 // Last workgroup out resets the barrier state (every workgroup reaches this,
-// including after an abort).
-__device__ void stack_exit(StackSync *sync) {
+// including after an abort); after an abort it also zeroes the logit
+// accumulators, which a completed launch leaves at zero.
+__device__ void stack_exit(StackSync *sync, uint64_t *lacc, uint32_t seq) {
     wait_own_stores();
     __syncthreads();
     if (tid() == 0) {
+        P.last = 0;
         if (counter_arrive(&sync->exit) == gridDim.x - 1) {
+            P.last = __hip_atomic_load(&sync->abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ? 2 : 1;
             counter_reset(&sync->barrier);
             counter_reset(&sync->release);
             counter_reset(&sync->abort);
             counter_reset(&sync->exit);
-        }
-    }
-}
-
-// ---- phase A -------------------------------------------------------------------
-// Every workgroup: router row(s) blockIdx.x + k * gridDim.x (row E is the
-// shared-expert input gate), the 2048 columns split over the 8 wavefronts
-// (lane l of wavefront w: columns 256 w + 4 l ..); wavefront 1 of the first
-// m * 32 workgroups also writes two activation records.  h rows [m x H] are
-// staged in LDS.
-__device__ void phase_a(const StackArgs &a, const StackLayer &L, const float *hin) {
-    float *s_hx = reinterpret_cast<float *>(s_dyn);
-    const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
-    const int lane = tid() % kWave;
-    const uint32_t m = a.m, E = a.E;
-    const uint32_t col = 256 * wave + 4 * lane;
-    const float4 nw = load_global_f4(L.norm + col);
-    // this workgroup's first router row (gridDim.x <= E + 1), issued ahead of
-    // the h staging so that the two round trips overlap
-    const uint32_t e0 = blockIdx.x;
-    const float4 r_first = load_global_f4((e0 < E ? L.router + (size_t)e0 * H : L.gate_vec) + col);
-    float sq[MT];
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
-        sq[t] = load_coherent(&a.ssq[(lane % kStackTeams) * MT + ((uint32_t)t < m ? t : 0)]);
-    stage_coherent<MT * H / 2 / kThreads>(reinterpret_cast<uint64_t *>(s_hx),
-                                          reinterpret_cast<const uint64_t *>(hin), m * H / 2);
-    if (wave == 0) {
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            const float v = group_reduce<64>(lane < kStackTeams ? sq[t] : 0.0f, AddOp());
-            if (lane == 0) P.inv_rms[t] = 1.0f / sqrtf(v / (float)H + 1e-6f);
+            __hip_atomic_store(&sync->seq, seq + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     __syncthreads();
-    float4 xn[MT];
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-        const float4 hv = *reinterpret_cast<const float4 *>(s_hx + (size_t)(t < (int)m ? t : 0) * H + col);
-        const float inv = P.inv_rms[t < (int)m ? t : 0];
-        xn[t] = make_float4(hv.x * inv * nw.x, hv.y * inv * nw.y, hv.z * inv * nw.z, hv.w * inv * nw.w);
-    }
-    for (uint32_t e = blockIdx.x; e <= E; e += gridDim.x) {
-        const float4 r = e == e0 ? r_first : load_global_f4((e < E ? L.router + (size_t)e * H : L.gate_vec) + col);
-        float dot[MT];
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            float s0 = xn[t].x * r.x;
-            s0 = fmaf(xn[t].y, r.y, s0);
-            s0 = fmaf(xn[t].z, r.z, s0);
-            s0 = fmaf(xn[t].w, r.w, s0);
-            dot[t] = group_reduce<64>(s0, AddOp());
-        }
-        if (lane == 0)
-#pragma unroll
-            for (int t = 0; t < MT; ++t) s_h[t][wave] = dot[t];
-        __syncthreads();
-        if (wave == 0 && lane < (int)m) {
-            float v = 0.0f;
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w) v += s_h[lane][w];
-            store_coherent(&a.logits[lane * (E + 1) + e], v);
-        }
-        __syncthreads();
-    }
-    // activation records q = 2 blockIdx.x + half, q < m * 64
-    if (wave == 1 && 2 * blockIdx.x < m * kBpGate) {
-        const uint32_t q = 2 * blockIdx.x + (uint32_t)(lane >> 5);
-        const bool active = q < m * kBpGate;
-        const uint32_t t = active ? q / kBpGate : 0, kb = q % kBpGate;
-        const uint32_t c = kb * 32 + (lane & 31);
-        const float x = s_hx[(size_t)t * H + c] * P.inv_rms[t] * load_global_f(L.norm + c);
-        prep_block32(x, lane & 31, active, a.xprep + (size_t)t * kBpGate * kXprepDwords, kBpGate, kb,
-                     CoherentStore());
-    }
+    if (P.last == 2) zero_lacc(lacc, 0, 1), zero_lacc(lacc + kLaccWords, 0, 1);
 }
 
 // ---- phase B: gate/up units ------------------------------------------------------
@@ -440,7 +400,9 @@ __device__ void shared_rows(const StackArgs &a, const SharedLoads &S0) {
         }
         float v[2] = {f16_to_f32(S.sg) * q4_block_dot(q4_signed(S.ng), x),
                       f16_to_f32(S.su) * q4_block_dot(q4_signed(S.nu), x)};
-        const float gate = transpose_reduce<64, 2>(v);  // lanes 0..31: gate, 32..63: up
+        // lanes 0..31: gate, 32..63: up; the records hold y = h * w_norm, so
+        // 1/rms scales the dot products
+        const float gate = transpose_reduce<64, 2>(v) * P.inv_rms[t];
         const float up = __shfl_xor(gate, 32);
         if (lane == 0) store_coherent(&a.hshared[(size_t)t * a.F + row], (gate / (1.0f + expf(-gate))) * up);
     }
@@ -503,33 +465,48 @@ __device__ __forceinline__ bool early_unit_loads(const StackArgs &a, UnitLoads &
 // After the loads are issued only LDS barriers are used: __syncthreads()
 // would wait for them.
 template <int LPRD, int MAXP>
-__device__ void compute_routes(const StackArgs &a, const StackLayer &L, UnitLoads &U, SharedLoads &S,
-                               bool &pre) {
+__device__ void compute_routes(const StackArgs &a, uint32_t l, UnitLoads &U, SharedLoads &S, bool &pre) {
     const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
     const int lane = tid() % kWave;
     const uint32_t m = a.m, E = a.E;
     if (tid() == 0) P.bad = 0;
     lds_barrier();
-    // the routing wavefronts' logits first, then the loads that need no
-    // routes (the M rows' records, this wavefront's shared-expert row), so
-    // that the logits are not queued behind them
+    // the routing wavefronts' logit words and sums of squares first, then the
+    // loads that need no routes (the M rows' records, this wavefront's
+    // shared-expert row), so that the logits are not queued behind them
     const int t = wave;
-    const float *lt = a.logits + (size_t)(t < (int)m ? t : 0) * (E + 1);
-    float lv[4], glog = 0.0f;
+    const uint64_t *acc = a.lacc + (size_t)(l & 1) * kLaccWords;
+    const uint64_t *lt = acc + (size_t)(t < (int)m ? t : 0) * (E + 1);
+    uint64_t fx[4], gfx = 0, flag = 0;
+    float sq = 0.0f;
     if (wave < (int)m) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {  // unconditional loads: one round trip
             const uint32_t e = (uint32_t)lane + 64u * i;
-            lv[i] = load_coherent(lt + (e < E ? e : E - 1));
+            fx[i] = load_coherent_u64(lt + (e < E ? e : E - 1));
         }
-        glog = load_coherent(lt + E);
+        gfx = load_coherent_u64(lt + E);
+        flag = load_coherent_u64(acc + (size_t)MT * (E + 1));
+        sq = load_coherent(&a.ssq[(lane % kStackTeams) * MT + t]);
     }
     record_loads(a, U);
     {
         const uint32_t row = 2 * blockIdx.x + (wave & 1);
         if (row < a.F && (uint32_t)(wave >> 1) < m) shared_row_loads(a, row, S);
     }
+    // the other parity, summed into by this layer's phase C: back to zero
+    if (blockIdx.x * kThreads < kLaccWords)
+        zero_lacc(a.lacc + (size_t)((l + 1) & 1) * kLaccWords, blockIdx.x, gridDim.x);
+    float lv[4], glog = 0.0f;
     if (wave < (int)m) {
+        // 1/rms (RMSNorm, weights.rs:216-239) of row t from the 32 teams' sums
+        const float v = group_reduce<64>(lane < kStackTeams ? sq : 0.0f, AddOp());
+        const float inv = 1.0f / sqrtf(v / (float)H + 1e-6f);
+        if (lane == 0) P.inv_rms[t] = inv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lv[i] = logit_of(fx[i], inv);
+        glog = logit_of(gfx, inv);
+        if (flag != 0 && lane == 0) P.bad = 1;  // a non-finite partial logit
         bool fin = true;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -780,7 +757,8 @@ __device__ void gate_up_compute(const StackArgs &a, const UnitDesc &d, UnitLoads
         }
         // value 2n (gate row n) lands on lanes (64 / RW) n .., value 2n + 1 (up
         // row n) on the lanes 32 / RW above them
-        const float gate = transpose_reduce<64, 2 * RW>(v);
+        // the records hold y = h * w_norm: 1/rms scales the dot products
+        const float gate = transpose_reduce<64, 2 * RW>(v) * P.inv_rms[t];
         const float up = RW == 8 ? dpp_f<0x104>(gate) : dpp_f<0x108>(gate);  // row_shl:4 / :8
         if ((lane & (64 / RW - 1)) == 0)
             s_h[i][RW * wave + lane / (64 / RW)] = (gate / (1.0f + expf(-gate))) * up;
@@ -814,9 +792,151 @@ __device__ void gate_up_unit(const StackArgs &a, const UnitDesc &d, UnitLoads &U
     lds_barrier();
 }
 
+// ---- the team tail: the next layer's inputs from the team's 64 rows -------------
+// Every member of team tau ends a layer holding the team's new rows of h (the
+// same bits in each: the members' partials summed in member order), thread
+// tid < MT * 64 row tid % 64 of token tid / 64, and shares out the next
+// layer's inputs: member t % K writes the records of token t's two y blocks
+// (y = h * w_norm), member 0 the sums of squares, member K - 1 the
+// shared-expert gate, and member k the partial logits of experts
+// [k E / K, (k + 1) E / K) (thread (el, cg) = (tid / 16, tid % 16): expert
+// e0 + 32 i + el over columns 4 cg ..).  A member's loads go out while the
+// barrier before phase C completes and land during phase C.
+static_assert(MT * 64 <= kThreads, "one team row value per thread");
+constexpr int kShareIt = 2;  // expert passes held in registers (E / K <= 64)
+struct ShareLoads {
+    float4 r[kShareIt];
+    float g, wn;
+};
+__device__ __forceinline__ void share_loads(const StackArgs &a, uint32_t ln, ShareLoads &S) {
+    const uint32_t K = a.members, tau = blockIdx.x % kStackTeams, k = blockIdx.x / kStackTeams;
+    if (k >= K) return;
+    const StackLayer Ln = a.layers[ln];
+    const uint32_t epm = (a.E + K - 1) / K, e0 = k * epm;
+    const uint32_t el = tid() >> 4, cg = tid() & 15;
+#pragma unroll
+    for (int i = 0; i < kShareIt; ++i) {
+        const uint32_t e = e0 + 32 * i + el;
+        S.r[i] = load_global_f4(Ln.router + (size_t)(e < a.E ? e : 0) * H + tau * 64 + 4 * cg);
+    }
+    S.g = load_global_f(Ln.gate_vec + tau * 64 + (tid() % 64));
+    S.wn = load_global_f(Ln.norm + tau * 64 + (tid() % 64));
+}
+
+// hv: this thread's row of h (0 past the m tokens); acc: the parity of the
+// logit accumulator layer ln reads; s_y: LDS for the team's [MT][64] y rows.
+__device__ void member_tail(const StackArgs &a, uint32_t tau, uint32_t k, const ShareLoads &S, float hv,
+                            float *s_y, uint64_t *acc, uint32_t ln) {
+    const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
+    const int lane = tid() % kWave;
+    const uint32_t m = a.m, E = a.E, K = a.members;
+    uint64_t *flag = acc + (size_t)MT * (E + 1);
+    const float y = hv * S.wn;  // tid % 64 is this thread's column, the weight it loaded
+    if (tid() < MT * 64) s_y[tid()] = y;
+    if (wave < (int)m) {  // wavefront t holds token t's 64 rows
+        const uint32_t t = (uint32_t)wave;
+        if (k == t % K) {  // records: half-wavefront = block 2 tau + half
+            const uint32_t half = (uint32_t)lane >> 5;
+            prep_block32(y, lane & 31, true, a.xprep + (size_t)t * kBpGate * kXprepDwords, kBpGate,
+                         2 * tau + half, CoherentStore());
+        }
+        if (k == 0) {
+            const float v = group_reduce<64>(hv * hv, AddOp());
+            if (lane == 0) store_coherent(&a.ssq[tau * MT + t], v);
+        }
+        if (k == K - 1) {  // the shared-expert gate, one column per lane
+            const float g = group_reduce<64>(S.g * y, AddOp());
+            if (lane == 0) add_fixed(acc + (size_t)t * (E + 1) + E, flag, g);
+        }
+    }
+    __syncthreads();
+    const uint32_t epm = (E + K - 1) / K, e0 = k * epm, e1 = e0 + epm < E ? e0 + epm : E;
+    const uint32_t el = tid() >> 4, cg = tid() & 15;
+    auto pass = [&](uint32_t i, const float4 &r) {
+        const uint32_t e = e0 + 32 * i + el;
+        const bool valid = e < e1;
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            if (t < (int)m) {
+                const float4 yv = *reinterpret_cast<const float4 *>(s_y + t * 64 + 4 * cg);
+                float v = r.x * yv.x;
+                v = fmaf(r.y, yv.y, v);
+                v = fmaf(r.z, yv.z, v);
+                v = fmaf(r.w, yv.w, v);
+                v = group_reduce<16>(valid ? v : 0.0f, AddOp());
+                if (cg == 0 && valid) add_fixed(acc + (size_t)t * (E + 1) + e, flag, v);
+            }
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < kShareIt; ++i)
+        if (e0 + 32 * i < e1) pass(i, S.r[i]);
+    const StackLayer Ln = a.layers[ln];
+    for (uint32_t i = kShareIt; e0 + 32 * i < e1; ++i) {
+        const uint32_t e = e0 + 32 * i + el;
+        pass(i, load_global_f4(Ln.router + (size_t)(e < e1 ? e : e0) * H + tau * 64 + 4 * cg));
+    }
+}
+
+// Layer 0's inputs: every member takes its team's rows of h_in (kept as the
+// first layer's residual in hres) and does its share of the tail.
+__device__ void team_prologue(const StackArgs &a, float &hres) {
+    const uint32_t tau = blockIdx.x % kStackTeams, k = blockIdx.x / kStackTeams;
+    if (k >= a.members) return;
+    ShareLoads S;
+    share_loads(a, 0, S);
+    const uint32_t tt = tid() / 64, row = tid() % 64;
+    hres = tid() < MT * 64 && tt < a.m ? load_coherent(&a.h_in[(size_t)tt * H + tau * 64 + row]) : 0.0f;
+    member_tail(a, tau, k, S, hres, reinterpret_cast<float *>(s_dyn), a.lacc, 0);
+}
+
+// Phase C's partials travel as tagged 64-bit words: tag << 32 | f32 bits, the
+// tag counting (launch, layer) steps with the high bit set, so a word left by
+// an earlier layer or launch (or the zeroed allocation) never carries the
+// current tag.  Readers poll the words themselves, bounded like grid_wait.
+__device__ __forceinline__ uint32_t part_tag(uint32_t seq, uint32_t n_layers, uint32_t l) {
+    return 0x80000000u | ((seq * n_layers + l) & 0x7FFFFFFFu);
+}
+
+// This thread's K partials (member order) of word `w0` (stride MT * 64 words
+// per member); false after a timeout (which sets abort) or another
+// workgroup's abort.
+__device__ bool poll_partials(const StackArgs &a, const uint64_t *w0, uint32_t K, uint32_t tag,
+                              float (&pv)[kMaxMembers]) {
+    uint32_t need = (1u << K) - 1u;
+    int64_t t0 = 0;
+    for (uint32_t spin = 1;; ++spin) {
+#pragma unroll
+        for (int kk = 0; kk < kMaxMembers; ++kk) {
+            if ((need >> kk) & 1u) {
+                const uint64_t w = poll_load(w0 + (size_t)kk * MT * 64);
+                if ((uint32_t)(w >> 32) == tag) {
+                    pv[kk] = __uint_as_float((uint32_t)w);
+                    need &= ~(1u << kk);
+                }
+            }
+        }
+        if (!need) return true;
+        if ((spin & 15) == 0) {
+            if (__hip_atomic_load(&a.sync->abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+            const int64_t now = wall_clock64();
+            if (t0 == 0) {
+                t0 = now;
+            } else if (now - t0 > kSpinLimit) {
+                __hip_atomic_store(&a.sync->abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (a.status)
+                    __hip_atomic_store(a.status, (int32_t)TQF_HIP_ERR_DEVICE, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                return false;
+            }
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
 // ---- phase C -------------------------------------------------------------------
 template <int LPRD, int MAXP>
-__device__ void phase_c(const StackArgs &a, const StackLayer &L, const float *hin) {
+__device__ void phase_c(const StackArgs &a, uint32_t l, uint32_t seq, float &hres, const ShareLoads &SL) {
     uint4 *s_x = reinterpret_cast<uint4 *>(reinterpret_cast<uint8_t *>(s_dyn) + LdsLayout<LPRD, MAXP>::kXr);
     const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
     const int lane = tid() % kWave;
@@ -921,63 +1041,41 @@ __device__ void phase_c(const StackArgs &a, const StackLayer &L, const float *hi
     const float s = transpose_reduce<LPRD, NL>(acc);
     const int idx = reduced_index<LPRD, NL>(lane);
     const int t = idx / RG, rr = idx % RG;
-    if (reduced_first_copy<LPRD, NL>(lane) && t < (int)a.m)
-        store_coherent(&a.partial[(((size_t)tau * K + k) * MT + t) * 64 + 8 * wave + j * RG + rr], s);
-    // team combine: the last member sums the members' partials in order
-    wait_own_stores();
+    // every token slot, so each word this launch reads was last written by it
+    // or by the previous launch
+    const uint32_t tag = part_tag(seq, a.n_layers, l);
+    if (reduced_first_copy<LPRD, NL>(lane))
+        __hip_atomic_store(&a.partial[(((size_t)tau * K + k) * MT + t) * 64 + 8 * wave + j * RG + rr],
+                           ((uint64_t)tag << 32) | __float_as_uint(s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // team combine: every member polls all K members' words, then sums them
+    // in member order (the same bits in every member) and takes its share of
+    // the next layer's inputs
+    if (tid() == 0) P.ok = 1;
     __syncthreads();
-    if (tid() == 0) P.last = counter_arrive(&a.sync->team[tau]) == K - 1 ? 1 : 0;
-    __syncthreads();
-    if (!P.last) return;
-    float *s_red = reinterpret_cast<float *>(s_x);  // [MT][64] squares
-    const uint32_t m = a.m;
-    for (uint32_t i = tid(); i < MT * 64; i += kThreads) {
-        const uint32_t tt = i / 64, row = i % 64;
-        float sq = 0.0f;
-        if (tt < m) {
-            constexpr int kMaxMembers = 16;
-            float pv[kMaxMembers];
-#pragma unroll
-            for (int kk = 0; kk < kMaxMembers; ++kk)
-                pv[kk] = kk < (int)K ? load_coherent(&a.partial[(((size_t)tau * K + kk) * MT + tt) * 64 + row])
-                                     : 0.0f;
-            const size_t o = (size_t)tt * H + tau * 64 + row;
-            const float res = load_coherent(hin + o);
+    const uint32_t m = a.m, tt = tid() / 64, row = tid() % 64;
+    const bool next = l + 1 < a.n_layers;
+    if (tid() < MT * 64 && tt < m) {
+        float pv[kMaxMembers];
+        if (poll_partials(a, a.partial + ((size_t)tau * K * MT + tt) * 64 + row, K, tag, pv)) {
             float sum = 0.0f;
 #pragma unroll
             for (int kk = 0; kk < kMaxMembers; ++kk)
                 if (kk < (int)K) sum += pv[kk];
-            const float out = res + sum;
-            store_coherent(&a.h[o], out);
-            sq = out * out;
+            hres += sum;
+            if (!next && k == 0) store_coherent(&a.h[(size_t)tt * H + tau * 64 + row], hres);
+        } else {
+            P.ok = 0;
         }
-        s_red[i] = sq;
     }
     __syncthreads();
-    if (wave < MT) {
-        const float v = group_reduce<64>(s_red[wave * 64 + lane], AddOp());
-        if (lane == 0 && wave < (int)m) store_coherent(&a.ssq[tau * MT + wave], v);
+    if (!P.ok) return;
+    if (!next) {
+        // nothing reads this parity any more: leave it at zero
+        zero_lacc(a.lacc + (size_t)(l & 1) * kLaccWords, k * kStackTeams + tau, K * kStackTeams);
+        return;
     }
-    if (tid() == 0) counter_reset(&a.sync->team[tau]);
-}
-
-// sum of squares of h rows of the team (prologue for the first layer)
-__device__ void team_ssq(const StackArgs &a) {
-    float *s_red = reinterpret_cast<float *>(s_dyn);
-    const uint32_t tau = blockIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
-    const int lane = tid() % kWave;
-    for (uint32_t i = tid(); i < MT * 64; i += kThreads) {
-        const uint32_t tt = i / 64, row = i % 64;
-        float v = 0.0f;
-        if (tt < a.m) v = load_coherent(&a.h_in[(size_t)tt * H + tau * 64 + row]);
-        s_red[i] = v * v;
-    }
-    __syncthreads();
-    if (wave < MT) {
-        const float v = group_reduce<64>(s_red[wave * 64 + lane], AddOp());
-        if (lane == 0 && wave < (int)a.m) store_coherent(&a.ssq[tau * MT + wave], v);
-    }
+    member_tail(a, tau, k, SL, hres, reinterpret_cast<float *>(s_x), a.lacc + (size_t)((l + 1) & 1) * kLaccWords,
+                l + 1);
 }
 
 }  // namespace
@@ -985,31 +1083,26 @@ __device__ void team_ssq(const StackArgs &a) {
 template <int LPRD, int MAXP>
 __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
     uint32_t epoch = 0;
-    if (blockIdx.x < (uint32_t)kStackTeams) team_ssq(a);
+    // layer 0's expert-matrix table into LDS (later layers': during the
+    // previous layer's phase C), and layer 0's inputs from h_in
+    constexpr int kPtrPer = ((256 + 1) * 3 + kThreads - 1) / kThreads;
+    {
+        const StackLayer L0 = a.layers[0];
+#pragma unroll
+        for (int i = 0; i < kPtrPer; ++i) {
+            const uint32_t k = tid() + (uint32_t)i * kThreads;
+            if (k < (a.E + 1) * 3) s_mats[k] = load_global_ptr(L0.mats + k);
+        }
+    }
+    const uint32_t seq = __hip_atomic_load(&a.sync->seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float hres = 0.0f;  // the residual: this thread's team row of h (phase C members)
+    team_prologue(a, hres);
     bool ok = grid_sync(a.sync, epoch, a.status);
     for (uint32_t l = 0; ok && l < a.n_layers; ++l) {
-        const StackLayer L = a.layers[l];
-        const float *hin = l == 0 ? a.h_in : a.h;
-        // the layer's expert-matrix pointers: loads issued now, stored to LDS
-        // after phase A (read by phases B and C)
-        constexpr int kPtrPer = ((256 + 1) * 3 + kThreads - 1) / kThreads;
-        const uint8_t *mp[kPtrPer];
-#pragma unroll
-        for (int i = 0; i < kPtrPer; ++i) {
-            const uint32_t k = tid() + (uint32_t)i * kThreads;
-            mp[i] = load_global_ptr(L.mats + (k < (a.E + 1) * 3 ? k : 0));
-        }
-        phase_a(a, L, hin);
-#pragma unroll
-        for (int i = 0; i < kPtrPer; ++i) {
-            const uint32_t k = tid() + (uint32_t)i * kThreads;
-            if (k < (a.E + 1) * 3) s_mats[k] = mp[i];
-        }
-        if (!(ok = grid_sync(a.sync, epoch, a.status))) break;
         UnitLoads U;
         SharedLoads S;
         bool pre;
-        compute_routes<LPRD, MAXP>(a, L, U, S, pre);
+        compute_routes<LPRD, MAXP>(a, l, U, S, pre);
         if (blockIdx.x == 0 && tid() < a.m * kTopK) {
             const uint32_t t = tid() / kTopK, kk = tid() % kTopK;
             if (a.ids_out) a.ids_out[((size_t)l * a.m + t) * kTopK + kk] = P.bad ? 0 : (uint16_t)P.ids[t][kk];
@@ -1042,11 +1135,34 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
         // after the arrival)
         grid_arrive(a.sync, epoch);
         prefetch_down<LPRD, MAXP>(a);
+        // this member's share of the next layer's router rows, gate and norm
+        ShareLoads SL;
+        if (l + 1 < a.n_layers) share_loads(a, l + 1, SL);
         if (!(ok = grid_wait(a.sync, epoch, a.status))) break;
-        phase_c<LPRD, MAXP>(a, L, hin);
-        if (l + 1 < a.n_layers && !(ok = grid_sync(a.sync, epoch, a.status))) break;
+        // the next layer's expert-matrix table: loads now, LDS after phase C
+        // (whose down weights still come from this layer's table)
+        const bool more = l + 1 < a.n_layers;
+        const uint8_t *mp[kPtrPer];
+        if (more) {
+            const StackLayer Ln = a.layers[l + 1];
+#pragma unroll
+            for (int i = 0; i < kPtrPer; ++i) {
+                const uint32_t k = tid() + (uint32_t)i * kThreads;
+                mp[i] = load_global_ptr(Ln.mats + (k < (a.E + 1) * 3 ? k : 0));
+            }
+        }
+        phase_c<LPRD, MAXP>(a, l, seq, hres, SL);
+        if (more) {
+            __syncthreads();  // every wavefront is past phase C's table reads
+#pragma unroll
+            for (int i = 0; i < kPtrPer; ++i) {
+                const uint32_t k = tid() + (uint32_t)i * kThreads;
+                if (k < (a.E + 1) * 3) s_mats[k] = mp[i];
+            }
+        }
+        if (more && !(ok = grid_sync(a.sync, epoch, a.status))) break;
     }
-    stack_exit(a.sync);
+    stack_exit(a.sync, a.lacc, seq);
 }
 
 namespace {
