@@ -176,10 +176,11 @@ class Layer:
     """One synthetic layer resident on the device with host copies for the
     oracle (router ~N(0, 1/2048), shared input gate ~N(0, 1/2048))."""
 
-    def __init__(self, be, layer_id: int, seed: int = 0, router_std=2048 ** -0.5):
+    def __init__(self, be, layer_id: int, seed: int = 0, router_std=2048 ** -0.5, router=None):
         E, H, F = 256, 2048, 512
         base = 10_000 * (layer_id + 1)
-        self.router = synth.normal((E, H), seed=base + 1, std=router_std)
+        self.router = (synth.normal((E, H), seed=base + 1, std=router_std) if router is None
+                       else np.ascontiguousarray(router, np.float32))
         self.gate_vec = synth.normal((H,), seed=base + 2, std=2048 ** -0.5)
         mats = []
         for e in range(E + 1):
@@ -406,6 +407,57 @@ def test_persistent_stack_matches_oracle_and_layer_kernels(backend, stack3, m):
     for l in range(3):
         assert np.array_equal(ids_p[l], routes[l])
     assert rel_err(h_p, hc) < FFN_TOL
+
+
+def test_routes_with_tied_router_rows(backend):
+    """Bit-equal router rows give bit-equal probabilities: the top-8 must
+    take tied experts in ascending id order (from_logits' stable descending
+    sort, experts/mod.rs:134-197).  Token 0: its top expert's row copied to
+    experts 3, 70, 130 and 200 (a five-way tie at rank 1, across all four of
+    a lane's slots); token 1: its 8th expert's row copied to two more, one
+    id below and one above (a three-way tie across the rank-8 boundary).
+    Both stack paths and the single-layer kernel, against the oracle."""
+    E, H = 256, 2048
+    h0 = synth.normal((4, H), seed=4242)
+    norm = (1.0 + 0.05 * synth.normal((H,), seed=4243)).astype(np.float32)
+    router = synth.normal((E, H), seed=4244, std=H ** -0.5)
+
+    def logits(R, t):
+        return orc.f32_matvec(R, orc.qwen_rmsnorm(h0[t], norm))
+
+    def ranking(R, t):
+        lg = logits(R, t)
+        return sorted(range(E), key=lambda e: (-lg[e], e))
+
+    top = ranking(router, 0)[0]
+    copies = [e for e in (3, 70, 130, 200, 5, 75) if e != top][:4]
+    for e in copies:
+        router[e] = router[top]
+    r1 = ranking(router, 1)
+    e8 = r1[7]
+    free = [e for e in range(E) if e not in r1[:8] and e not in copies + [top]]
+    below, above = free[0], free[-1]
+    router[below] = router[e8]
+    router[above] = router[e8]
+    # the construction holds: five equal logits at token 0's top, three
+    # across token 1's rank-8 boundary
+    lg0, lg1 = logits(router, 0), logits(router, 1)
+    assert len({float(lg0[e]) for e in copies + [top]}) == 1
+    assert lg1[below] == lg1[e8] == lg1[above]
+    L = Layer(backend, 9, router=router)
+    st = backend.prepare_stack([L.dev], [backend.upload_f32(norm)])
+    try:
+        hc, routes = oracle_stack([L], [norm], h0)
+        for persistent in (True, False):
+            h, ids, w, status = _stack_run(backend, st, h0, 4, 1, persistent)
+            assert status == 0
+            assert np.array_equal(ids[0], routes[0]), (persistent, ids[0], routes[0])
+            assert rel_err(h, hc) < FFN_TOL
+        xn = np.stack([orc.qwen_rmsnorm(h0[t], norm) for t in range(4)])
+        _, ids1, _ = backend.moe_forward_batch(L.dev, xn)
+        assert np.array_equal(ids1, routes[0])
+    finally:
+        backend.free_stack(st)
 
 
 def test_persistent_stack_repeats_bit_identically(backend, stack3):

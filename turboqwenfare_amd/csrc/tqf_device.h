@@ -62,6 +62,22 @@ __device__ __forceinline__ int readlane_i(int v, int lane) {
     return __builtin_amdgcn_readlane(v, lane);
 }
 
+// The wavefront's maximum, broadcast through a scalar register: the row
+// maximum by the four DPP steps, then row_bcast:15 (lane 15 of rows 0 / 2
+// into rows 1 / 3) and row_bcast:31 (lane 31 into rows 2 and 3) leave the
+// wave's maximum in lane 63.  Every lane must be active.
+__device__ __forceinline__ float wave_max_bcast(float v) {
+    v = fmaxf(v, dpp_f<kDppXor1>(v));
+    v = fmaxf(v, dpp_f<kDppXor2>(v));
+    v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_f<kDppMirror>(v));
+    const int b15 = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x142, 0xA, 0xF, false);
+    v = fmaxf(v, __int_as_float(b15));
+    const int b31 = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x143, 0xC, 0xF, false);
+    v = fmaxf(v, __int_as_float(b31));
+    return readlane_f(v, 63);
+}
+
 // All-reduce over aligned groups of LANES lanes (2..64); every lane of a
 // group receives the group's result.  All lanes of a group must be active.
 template <int LANES, typename Op>

@@ -162,6 +162,10 @@ __device__ __forceinline__ void copy_to_lds_16(const void *gaddr, uint32_t lds) 
 __device__ __forceinline__ void copy_to_lds_4(const void *gaddr, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(gaddr) : "memory", "m0");
 }
+// The same at agent scope (sc1), for data other workgroups wrote.
+__device__ __forceinline__ void copy_to_lds_16_coherent(const void *gaddr, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off sc1" ::"s"(lds), "v"(gaddr) : "memory", "m0");
+}
 
 // Copies n 64-bit words written by other workgroups into LDS: every load of
 // a thread is issued before the first LDS store (one round trip).
@@ -323,30 +327,22 @@ __device__ __forceinline__ UnitDesc unit_desc(int u, int F, int m) {
 
 // Wavefront w's rows of the unit in gate and up (one block per lane, raw
 // nibbles) and their scale octets, held in registers between issue and use.
-constexpr int kRecRow = 7 * kBpGate * 2;  // 64-bit words of one token's records
-constexpr int kRecPer = (MT * kRecRow + kThreads - 1) / kThreads;
+constexpr int kRecBytes = 7 * kBpGate * 16;  // one token's activation records (7 KiB)
+constexpr int kRecWaves = kWaves - MT;        // the wavefronts that route no token copy them
 struct UnitLoads {
-    uint64_t xv[kRecPer];  // this thread's share of the M rows' activation records
     uint4 ng[8], nu[8], sg, su;
 };
 
-// The records of the M rows (written by phase A), this thread's share of the
-// LDS image; issued when the layer's phase B starts, stored by store_records.
-__device__ __forceinline__ void record_loads(const StackArgs &a, UnitLoads &U) {
-#pragma unroll
-    for (int i = 0; i < kRecPer; ++i) {
-        const int k = (int)tid() + i * kThreads;
-        U.xv[i] = k < (int)a.m * kRecRow ? load_coherent_u64(reinterpret_cast<const uint64_t *>(a.xprep) + k) : 0;
-    }
-}
+// The records of the M rows (written by the previous layer's phase C) into
+// LDS, copied directly by wavefronts MT.. (1 KiB per instruction); the
+// caller waits for them (vmcnt) before the barrier that publishes them.
 template <int LPRD, int MAXP>
-__device__ __forceinline__ void store_records(const StackArgs &a, const UnitLoads &U) {
-    uint64_t *dst = reinterpret_cast<uint64_t *>(reinterpret_cast<uint8_t *>(s_dyn) + LdsLayout<LPRD, MAXP>::kXr);
-#pragma unroll
-    for (int i = 0; i < kRecPer; ++i) {
-        const int k = (int)tid() + i * kThreads;
-        if (k < (int)a.m * kRecRow) dst[k] = U.xv[i];
-    }
+__device__ __forceinline__ void record_copies(const StackArgs &a, int wave, int lane) {
+    if (wave < MT) return;
+    const uint32_t chunks = a.m * (kRecBytes / 1024);
+    for (uint32_t c = (uint32_t)(wave - MT); c < chunks; c += kRecWaves)
+        copy_to_lds_16_coherent(reinterpret_cast<const uint8_t *>(a.xprep) + (size_t)c * 1024 + lane * 16,
+                                lds_addr(LdsLayout<LPRD, MAXP>::kXr + c * 1024));
 }
 
 // ---- phase B: the shared expert's rows ------------------------------------------
@@ -489,7 +485,13 @@ __device__ void compute_routes(const StackArgs &a, uint32_t l, UnitLoads &U, Sha
         flag = load_coherent_u64(acc + (size_t)MT * (E + 1));
         sq = load_coherent(&a.ssq[(lane % kStackTeams) * MT + t]);
     }
-    record_loads(a, U);
+    // the records only once the routing words are in (their 7 MB over all
+    // workgroups would otherwise queue ahead of them), by the wavefronts
+    // that do not route
+    float v = 0.0f;
+    if (wave < (int)m) v = group_reduce<64>(lane < kStackTeams ? sq : 0.0f, AddOp());
+    lds_barrier();
+    record_copies<LPRD, MAXP>(a, wave, lane);
     {
         const uint32_t row = 2 * blockIdx.x + (wave & 1);
         if (row < a.F && (uint32_t)(wave >> 1) < m) shared_row_loads(a, row, S);
@@ -500,7 +502,6 @@ __device__ void compute_routes(const StackArgs &a, uint32_t l, UnitLoads &U, Sha
     float lv[4], glog = 0.0f;
     if (wave < (int)m) {
         // 1/rms (RMSNorm, weights.rs:216-239) of row t from the 32 teams' sums
-        const float v = group_reduce<64>(lane < kStackTeams ? sq : 0.0f, AddOp());
         const float inv = 1.0f / sqrtf(v / (float)H + 1e-6f);
         if (lane == 0) P.inv_rms[t] = inv;
 #pragma unroll
@@ -529,24 +530,51 @@ __device__ void compute_routes(const StackArgs &a, uint32_t l, UnitLoads &U, Sha
             ssum = group_reduce<64>(ssum, AddOp());
 #pragma unroll
             for (int i = 0; i < 4; ++i) p[i] = ((uint32_t)lane + 64u * i < E) ? p[i] / ssum : -1.0f;
-            // 8 rounds of: the wave's largest probability, then the lowest id
-            // holding it (ids ascend with i, then with the lane), via ballots
+            // top-8 by (probability descending, id ascending), as the stable
+            // descending sort of from_logits: each lane first orders its four
+            // entries (ids lane + 64 i), then 8 rounds take the largest lane
+            // head; among equal heads the lowest id wins (the common
+            // single-candidate case needs one ballot)
+            float q[4] = {p[0], p[1], p[2], p[3]};
+            int qi[4] = {0, 1, 2, 3};
+            auto order = [&](int x, int y) {
+                const bool sw = q[y] > q[x] || (q[y] == q[x] && qi[y] < qi[x]);
+                const float tq = sw ? q[y] : q[x], uq = sw ? q[x] : q[y];
+                const int ti = sw ? qi[y] : qi[x], ui = sw ? qi[x] : qi[y];
+                q[x] = tq;
+                q[y] = uq;
+                qi[x] = ti;
+                qi[y] = ui;
+            };
+            order(0, 1);
+            order(2, 3);
+            order(0, 2);
+            order(1, 3);
+            order(1, 2);
             float psel[kTopK];
             int idsel[kTopK];
 #pragma unroll
             for (int k = 0; k < kTopK; ++k) {
-                const float best =
-                    group_reduce<64>(fmaxf(fmaxf(p[0], p[1]), fmaxf(p[2], p[3])), MaxOp());
-                const uint64_t m0 = __ballot(p[0] == best), m1 = __ballot(p[1] == best);
-                const uint64_t m2 = __ballot(p[2] == best), m3 = __ballot(p[3] == best);
-                const int i_win = m0 ? 0 : m1 ? 1 : m2 ? 2 : 3;
-                const uint64_t mw = m0 ? m0 : m1 ? m1 : m2 ? m2 : m3;
-                const int l_win = __builtin_ctzll(mw);
+                const float best = wave_max_bcast(q[0]);
+                const uint64_t cand = __ballot(q[0] == best);
+                int l_win = (int)__builtin_ctzll(cand);
+                if (__builtin_popcountll(cand) > 1) {  // equal heads: the lowest id
+                    const uint64_t c0 = __ballot(q[0] == best && qi[0] == 0);
+                    const uint64_t c1 = __ballot(q[0] == best && qi[0] == 1);
+                    const uint64_t c2 = __ballot(q[0] == best && qi[0] == 2);
+                    l_win = (int)__builtin_ctzll(c0 ? c0 : c1 ? c1 : c2 ? c2 : cand);
+                }
                 psel[k] = best;
-                idsel[k] = l_win + 64 * i_win;
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (lane == l_win && i == i_win) p[i] = -1.0f;
+                idsel[k] = l_win + 64 * __builtin_amdgcn_readlane(qi[0], l_win);
+                if (lane == l_win) {
+                    q[0] = q[1];
+                    q[1] = q[2];
+                    q[2] = q[3];
+                    q[3] = -2.0f;
+                    qi[0] = qi[1];
+                    qi[1] = qi[2];
+                    qi[2] = qi[3];
+                }
             }
             // renormalise (experts/mod.rs:159-166): the total is the route-order
             // sum; each lane k < 8 divides its own weight
@@ -572,7 +600,7 @@ __device__ void compute_routes(const StackArgs &a, uint32_t l, UnitLoads &U, Sha
             if (lane == 0 && !(fabsf(wsum - 1.0f) <= 1e-4f)) P.bad = 1;
         }
     }
-    store_records<LPRD, MAXP>(a, U);  // waits for the record loads only
+    if (wave >= MT) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the record copies
     lds_barrier();
     pre = false;
     if (P.bad) {
