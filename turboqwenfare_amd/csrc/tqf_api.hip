@@ -173,13 +173,14 @@ int32_t ensure_moe_scratch(tqf_hip_ctx *ctx, uint32_t hidden, uint32_t width, ui
     (void)hipFree(sc.partial);
     (void)hipFree(sc.counters);
     sc.xprep = sc.hprep = sc.counters = nullptr;
-    sc.logits = sc.partial = nullptr;
+    sc.logits = nullptr;
+    sc.partial = nullptr;
     sc.plan = nullptr;
     sc.hidden = sc.width = sc.experts = 0;
     // padding records stay zero: kernels only write real blocks
     const size_t xprep = (size_t)kMaxTokens * padded_blocks(hidden / 32) * kXprepDwords * 4;
     const size_t hprep = (size_t)kMaxSlots * padded_blocks(width / 32) * kXprepDwords * 4;
-    const size_t logits = (size_t)kMaxTokens * (experts + 1) * 4;
+    const size_t logits = (size_t)kMaxTokens * (experts + 1) * 8;
     const size_t partial = (size_t)kMaxSlots * kMaxTokens * hidden * 4;
     const size_t counters = counter_count(hidden) * 4;
     TQF_HIP(ctx, hipMalloc(&sc.xprep, xprep));
@@ -192,6 +193,7 @@ int32_t ensure_moe_scratch(tqf_hip_ctx *ctx, uint32_t hidden, uint32_t width, ui
     TQF_HIP(ctx, hipMemset(sc.hprep, 0, hprep));
     TQF_HIP(ctx, hipMemset(sc.plan, 0, sizeof(Plan)));
     TQF_HIP(ctx, hipMemset(sc.counters, 0, counters));
+    TQF_HIP(ctx, hipMemset(sc.logits, 0, logits));  // zero carries no launch's tag
     sc.hidden = hidden;
     sc.width = width;
     sc.experts = experts;

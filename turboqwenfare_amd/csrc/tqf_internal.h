@@ -221,7 +221,7 @@ struct LayerDev {
 struct Scratch {
     uint32_t *xprep = nullptr;   // [kMaxTokens x padded(hidden/32) x 32]
     uint32_t *hprep = nullptr;   // [kMaxSlots x padded(width/32) x 32]
-    float *logits = nullptr;     // [kMaxTokens x (n_experts + 1)]
+    uint64_t *logits = nullptr;  // [kMaxTokens x (n_experts + 1)] tagged words (tag << 32 | f32 bits)
     Plan *plan = nullptr;
     float *partial = nullptr;    // [slot groups x kMaxTokens x hidden]
     uint32_t *counters = nullptr;  // last-arriver counters (see kCounter*)
@@ -392,9 +392,10 @@ struct tqf_hip_ctx {
 
 namespace tqf {
 
-// Counter array layout: [route (1) | pad | down (one per row group, at most
-// hidden / 16)].  Every counter returns to zero in the workgroup that
-// finishes its kernel.
+// Counter array layout: [route launch count (slot 1) | pad | down (one per
+// row group, at most hidden / 16)].  The down counters return to zero in the
+// workgroup that finishes its kernel; the route kernel's launch count only
+// grows (it tags that launch's logit words).
 constexpr int kCounterDown = 64;
 // [0, 64) route; [64, 64 + hidden / 16) the Q4_0 down kernel; then the Q4_K
 // down launch's combine fold, kMaxTokens x (hidden / 64) (token, row tile)

@@ -167,19 +167,27 @@ hipError_t launch_gemv(hipStream_t s, const uint8_t *const *d_tables, uint32_t c
 // shared-expert input gate, experts/mod.rs:1614).  Each workgroup
 //   1. loads h [m x hidden], applies RMSNorm when `norm` is given
 //      (weights.rs:216-239: x * (1/sqrt(mean(x^2) + 1e-6)) * w),
-//   2. writes the xprep records of the blocks assigned to it,
-//   3. computes its router logits (experts/mod.rs:1491 router matvec).
-// The last workgroup to finish turns the logits into routes
-// (RouterResult::from_logits, experts/mod.rs:134-167: softmax, stable
-// descending top-8 with ties to the lower id, renormalise) and the pair plan.
+//   2. computes its router logits (experts/mod.rs:1491 router matvec) and
+//      stores them as tagged words (tag << 32 | f32 bits; the tag is the
+//      launch count with the high bit set, so a word of an earlier launch,
+//      or the zeroed allocation, never matches),
+//   3. writes the xprep / Q8_K records of the blocks assigned to it
+//      (workgroups 1..).
+// Workgroup 0 polls every logit word of this launch, turns the logits into
+// routes (RouterResult::from_logits, experts/mod.rs:134-167: softmax, stable
+// descending top-8 with ties to the lower id, renormalise) and the pair
+// plan, and advances the launch count.  The poll is bounded in time; a
+// timeout writes a failed plan (TQF_HIP_ERR_DEVICE).
 // ---------------------------------------------------------------------------
 constexpr int kRouteRows = 2;
+constexpr int64_t kRouteSpinLimit = 2000000;  // wall-clock ticks (100 MHz): 20 ms
+constexpr int kRouteSeq = 1;                   // the launch count's counter slot
 
 template <int MT>
 __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__restrict__ h,
                                                     const float *__restrict__ norm, uint32_t m,
                                                     uint32_t bp, uint32_t *__restrict__ xprep,
-                                                    float *__restrict__ logits,
+                                                    uint64_t *__restrict__ logits,
                                                     Plan *__restrict__ plan,
                                                     uint32_t *__restrict__ counter,
                                                     uint16_t *__restrict__ ids_out,
@@ -192,8 +200,11 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
     __shared__ int s_bad;
     __shared__ int s_ids[kMaxTokens * kTopK];
     __shared__ float s_w[kMaxTokens * kTopK];
+    __shared__ float s_gate[kMaxTokens];
 
     const int tid = threadIdx.x;
+    const uint32_t seq = __hip_atomic_load(&counter[kRouteSeq], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t tag = 0x80000000u | (seq & 0x7FFFFFFFu);
     const uint32_t H = L.hidden, E = L.n_experts;
     const int vpt = (int)(H / 256);  // 1..8 elements per thread
     const uint32_t col0 = (uint32_t)tid * vpt;
@@ -276,17 +287,17 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
             const uint32_t r = blockIdx.x * kRouteRows + rr;
             if (r <= E)
                 for (int t = 0; t < (int)m; ++t)
-                    store_coherent(&logits[(size_t)t * (E + 1) + r], dots[rr * MT + t]);
+                    __hip_atomic_store(&logits[(size_t)t * (E + 1) + r],
+                                       ((uint64_t)tag << 32) | __float_as_uint(dots[rr * MT + t]),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        wait_own_stores();
-        s_last = (counter_arrive(counter) == gridDim.x - 1) ? 1 : 0;
     }
     // 3. xprep (when asked for) of block kb is held by threads [kb * 32/vpt,
-    //    (kb+1) * 32/vpt); records are strided by the gate/up matrices' padded
-    //    block count bp.  Written after the arrival, off the routing's
-    //    critical path: the kernels that read them start after this one ends.
+    //    (kb+1) * 32/vpt) of workgroup kb + 1 (workgroup 0 routes); records
+    //    are strided by the gate/up matrices' padded block count bp.  The
+    //    kernels that read them start after this one ends.
     const uint32_t KB = xprep ? H / 32 : 0;
-    for (uint32_t kb = blockIdx.x; kb < KB; kb += gridDim.x) {
+    for (uint32_t kb = blockIdx.x - 1; blockIdx.x > 0 && kb < KB; kb += gridDim.x - 1) {
         const int lpb = 32 / vpt;
         const int first = (int)kb * lpb;
         if (tid >= first && tid < first + lpb) {
@@ -313,13 +324,16 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
         }
     }
 
-    // 4. Q8_K records (when asked for): workgroup j < m * H / 256 quantizes
-    //    chunk c = j % (H / 256) of row t = j / (H / 256), staged in LDS in
-    //    the quantizer's lane order.  Also after the arrival.
+    // 4. Q8_K records (when asked for): chunk j < m * H / 256 (chunk c = j %
+    //    (H / 256) of row t = j / (H / 256)) by workgroup (j + 1) % grid, so
+    //    that workgroup 0, which routes, has one only when the grid has no
+    //    other workgroup left for it; staged in LDS in the quantizer's lane
+    //    order.
     const uint32_t cpr = H / 256;
-    if (q8 != nullptr && blockIdx.x < m * cpr) {
+    const uint32_t jq = blockIdx.x == 0 ? gridDim.x - 1 : blockIdx.x - 1;
+    if (q8 != nullptr && jq < m * cpr) {
         __shared__ float s_chunk[256];
-        const uint32_t t = blockIdx.x / cpr, c = blockIdx.x % cpr;
+        const uint32_t t = jq / cpr, c = jq % cpr;
 #pragma unroll
         for (int tt = 0; tt < MT; ++tt)
             if (tt == (int)t)
@@ -338,23 +352,58 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
         }
     }
 
-    __syncthreads();
-    if (!s_last) return;
+    if (blockIdx.x != 0) return;
 
-    // ---- last workgroup: routes and the pair plan --------------------------
+    // ---- workgroup 0: routes and the pair plan ------------------------------
     const int wave = tid / kWave, lane = tid % kWave;
-    if (tid == 0) s_bad = 0;
+    if (tid == 0) {
+        s_bad = 0;
+        s_last = 0;  // 1: the poll timed out
+    }
     __syncthreads();
     for (int t = wave; t < (int)m; t += 4) {
-        const float *lt = logits + (size_t)t * (E + 1);
+        // this token's E + 1 words: lane l takes experts l + 64 i, lane 0 also
+        // the gate word; until every word carries this launch's tag
+        const uint64_t *lt = logits + (size_t)t * (E + 1);
+        uint64_t w[5];
+        uint32_t need = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if ((uint32_t)lane + 64u * i < E) need |= 1u << i;
+        if (lane == 0) need |= 1u << 4;
+        int64_t t0 = 0;
+        for (uint32_t spin = 1;; ++spin) {
+#pragma unroll
+            for (int i = 0; i < 5; ++i) {
+                if ((need >> i) & 1u) {
+                    const uint32_t e = i < 4 ? (uint32_t)lane + 64u * i : E;
+                    w[i] = __hip_atomic_load(const_cast<uint64_t *>(lt + e), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+                    if ((uint32_t)(w[i] >> 32) == tag) need &= ~(1u << i);
+                }
+            }
+            if (__all(need == 0)) break;
+            if ((spin & 63) == 0) {
+                const int64_t now = wall_clock64();
+                if (t0 == 0) {
+                    t0 = now;
+                } else if (now - t0 > kRouteSpinLimit) {
+                    if (lane == 0) s_last = 1;
+                    break;
+                }
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (s_last) continue;
         float lv[4];
         bool fin = true;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t e = (uint32_t)lane + 64u * i;
-            lv[i] = e < E ? load_coherent(lt + e) : -INFINITY;
+            lv[i] = e < E ? __uint_as_float((uint32_t)w[i]) : -INFINITY;
             if (e < E && !(fabsf(lv[i]) <= 3.402823466e38f)) fin = false;
         }
+        if (lane == 0) s_gate[t] = __uint_as_float((uint32_t)w[4]);
         if (__any(!fin)) {
             if (lane == 0) s_bad = 1;
             continue;
@@ -370,23 +419,49 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
         ssum = group_reduce<64>(ssum, AddOp());
 #pragma unroll
         for (int i = 0; i < 4; ++i) p[i] = ((uint32_t)lane + 64u * i < E) ? p[i] / ssum : -1.0f;
+        // top-8 by (probability descending, id ascending): each lane orders
+        // its four entries (ids lane + 64 i), then 8 rounds take the largest
+        // lane head, the lowest id among equal heads
+        float q[4] = {p[0], p[1], p[2], p[3]};
+        int qi[4] = {0, 1, 2, 3};
+        auto order = [&](int x, int y) {
+            const bool sw = q[y] > q[x] || (q[y] == q[x] && qi[y] < qi[x]);
+            const float tq = sw ? q[y] : q[x], uq = sw ? q[x] : q[y];
+            const int ti = sw ? qi[y] : qi[x], ui = sw ? qi[x] : qi[y];
+            q[x] = tq;
+            q[y] = uq;
+            qi[x] = ti;
+            qi[y] = ui;
+        };
+        order(0, 1);
+        order(2, 3);
+        order(0, 2);
+        order(1, 3);
+        order(1, 2);
         float psel[kTopK];
         int idsel[kTopK];
 #pragma unroll
         for (int k = 0; k < kTopK; ++k) {
-            // lane's best: highest p, then lowest id (ids ascend with i)
-            float bp = p[0];
-            int bid = lane;
-#pragma unroll
-            for (int i = 1; i < 4; ++i)
-                if (p[i] > bp) { bp = p[i]; bid = lane + 64 * i; }
-            const float best = group_reduce<64>(bp, MaxOp());
-            const int win = group_reduce<64>(bp == best ? bid : 0x7FFFFFFF, MinOp());
+            const float best = wave_max_bcast(q[0]);
+            const uint64_t cand = __ballot(q[0] == best);
+            int l_win = (int)__builtin_ctzll(cand);
+            if (__builtin_popcountll(cand) > 1) {  // equal heads: the lowest id
+                const uint64_t c0 = __ballot(q[0] == best && qi[0] == 0);
+                const uint64_t c1 = __ballot(q[0] == best && qi[0] == 1);
+                const uint64_t c2 = __ballot(q[0] == best && qi[0] == 2);
+                l_win = (int)__builtin_ctzll(c0 ? c0 : c1 ? c1 : c2 ? c2 : cand);
+            }
             psel[k] = best;
-            idsel[k] = win;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (lane + 64 * i == win) p[i] = -1.0f;
+            idsel[k] = l_win + 64 * __builtin_amdgcn_readlane(qi[0], l_win);
+            if (lane == l_win) {
+                q[0] = q[1];
+                q[1] = q[2];
+                q[2] = q[3];
+                q[3] = -2.0f;
+                qi[0] = qi[1];
+                qi[1] = qi[2];
+                qi[2] = qi[3];
+            }
         }
         if (lane == 0) {
             float total = -0.0f;
@@ -403,16 +478,18 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
     }
     __syncthreads();
     const int n = (int)m * kTopK;
-    if (s_bad) {
+    if (tid == 0)  // every word of this launch has been read
+        __hip_atomic_store(&counter[kRouteSeq], seq + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (s_bad || s_last) {
+        const int32_t err = s_last ? TQF_HIP_ERR_DEVICE : TQF_HIP_ERR_ROUTER;
         if (wave == 0)
             for (int i = lane; i < (int)m * (kTopK + 1); i += kWave) plan->slots[i].token = -1;
         if (tid == 0) {
             plan->n_slots = 0;
             plan->n_union = 0;
-            plan->status = TQF_HIP_ERR_ROUTER;
+            plan->status = err;
             plan->m = (int)m;
-            if (status_out) *status_out = TQF_HIP_ERR_ROUTER;
-            counter_reset(counter);
+            if (status_out) *status_out = err;
         }
         return;
     }
@@ -459,7 +536,7 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
             if (w_out) w_out[lane] = wv;
         }
         if (lane < (int)m) {
-            const float gl = load_coherent(logits + (size_t)lane * (E + 1) + E);
+            const float gl = s_gate[lane];
             plan->gate_logit[lane] = gl;
             SlotRec rec;
             rec.mat[0] = L.mats[E * 3 + 0];
@@ -475,7 +552,6 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
             plan->n_slots = (int)m * (kTopK + 1);
             plan->status = 0;
             plan->m = (int)m;
-            counter_reset(counter);
         }
     }
 }
