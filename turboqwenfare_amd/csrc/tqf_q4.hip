@@ -408,7 +408,7 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
             if (lane == 0) s_bad = 1;
             continue;
         }
-        const float mx = group_reduce<64>(fmaxf(fmaxf(lv[0], lv[1]), fmaxf(lv[2], lv[3])), MaxOp());
+        const float mx = wave_max_bcast(fmaxf(fmaxf(lv[0], lv[1]), fmaxf(lv[2], lv[3])));
         float p[4], ssum = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -494,28 +494,27 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
         return;
     }
     // Pair plan, one route entry i = (t, k) per lane of wave 0 (n <= 64).
+    // The entries of one expert as the bits of one mask (broadcast LDS reads):
+    // a group starts at its lowest entry; base = the entries of the groups
+    // that start earlier, upos = those groups' count.
     if (wave == 0) {
+        __shared__ int s_first[kMaxTokens * kTopK];
         const int e_i = lane < n ? s_ids[lane] : -1;
-        int first = lane, cnt = 0, rank = 0;
-        for (int j = 0; j < n; ++j) {
-            const int ej = readlane_i(e_i, j);
-            if (ej == e_i) {
-                ++cnt;
-                if (j < lane) ++rank;
-                if (j < first) first = j;
-            }
-        }
+        uint64_t eq = 0;
+#pragma unroll
+        for (int j = 0; j < MT * kTopK; ++j) eq |= (j < n && s_ids[j] == e_i) ? (1ull << j) : 0ull;
+        const int rank = __builtin_popcountll(eq & ((1ull << lane) - 1ull));
+        const int first = lane < n ? (int)__builtin_ctzll(eq) : lane;
         const bool flag = lane < n && first == lane;
-        const int fc = flag ? cnt : 0;
-        int base = 0, upos = 0;
-        for (int j = 0; j < n; ++j) {
-            const int fcj = readlane_i(fc, j);
-            if (j < first) {
-                base += fcj;
-                upos += fcj ? 1 : 0;
-            }
-        }
-        const int nu = __builtin_popcountll(__ballot(flag));
+        const uint64_t F = __ballot(flag);
+        const int upos = __builtin_popcountll(F & ((1ull << first) - 1ull));
+        s_first[lane] = first;
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        int base = 0;
+#pragma unroll
+        for (int j = 0; j < MT * kTopK; ++j) base += (j < n && s_first[j] < first) ? 1 : 0;
+        const int nu = __builtin_popcountll(F);
         if (lane < n) {
             const int slot = (int)m + base + rank;
             const int t = lane / kTopK, k = lane % kTopK;

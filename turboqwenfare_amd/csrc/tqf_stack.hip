@@ -519,7 +519,7 @@ __device__ void compute_routes(const StackArgs &a, uint32_t l, UnitLoads &U, Sha
         if (__any(!fin)) {
             if (lane == 0) P.bad = 1;
         } else {
-            const float mx = group_reduce<64>(fmaxf(fmaxf(lv[0], lv[1]), fmaxf(lv[2], lv[3])), MaxOp());
+            const float mx = wave_max_bcast(fmaxf(fmaxf(lv[0], lv[1]), fmaxf(lv[2], lv[3])));
             float p[4], ssum = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
