@@ -488,6 +488,43 @@ def layer_bench(be, model, inputs, m: int, with_accept: bool, seed: int, iters: 
     return out
 
 
+def mtp_loop_bench(be, layers: int, seed: int, recipe: str, steps: int = 40, warmup: int = 4):
+    """The MTP decode loop (turboqwenfare_amd/mtp_loop.py) at full depth: the
+    40-layer target stack, the draft head's MoE layer, a Q4_0 embedding and
+    the Q6_K LM head over V = 151,936, stochastic at T = 0.7, k = 3.  Two
+    draft sources: the synthetic draft head (unrelated weights: its drafts
+    are rejected) and self-drafting (the target drafts for itself: drafts
+    accepted).  Wall time per step from the host, Python call overhead
+    included; the controller's policy as in MtpLoop."""
+    from turboqwenfare_amd.mtp_loop import DeviceEngine, MtpLoop, MtpModel
+
+    model = MtpModel(be, layers, V, seed=seed, recipe=recipe, log=log)
+    out = {}
+    try:
+        for name, self_draft in (("draft_head", False), ("self_draft", True)):
+            eng = DeviceEngine(be, model, k=K, temperature=TEMPERATURE, greedy=False, seed=seed,
+                               self_draft=self_draft)
+            loop = MtpLoop(eng, k=K, window=8)
+            try:
+                loop.run(1234, warmup)
+                be.synchronize()
+                t0 = time.perf_counter()
+                recs = [loop.step() for _ in range(steps)]
+                be.synchronize()
+                dt = time.perf_counter() - t0
+            finally:
+                eng.free()
+            spec = [r for r in recs if r.speculative]
+            emitted = sum(len(r.emitted) for r in recs)
+            out[name] = dict(steps=steps, ms_per_step=dt / steps * 1e3, tokens=emitted,
+                             tokens_per_s=emitted / dt, speculative_steps=len(spec),
+                             mean_accepted=(float(np.mean([r.accepted for r in spec])) if spec else None),
+                             controller_enabled=loop.controller.enabled)
+    finally:
+        model.free()
+    return out
+
+
 def kernel_source_digest() -> str:
     """sha256 of the dominant kernel's sources: a committed traffic profile
     counts for this build only when it was taken on the same sources."""
@@ -546,6 +583,8 @@ def main():
                          "taken with) and exit")
     ap.add_argument("--q4k-verify-only", action="store_true",
                     help="only the verify step with Q4_K expert layers")
+    ap.add_argument("--mtp-loop-only", action="store_true",
+                    help="only the MTP decode loop at full depth (draft head and self-drafting)")
     ap.add_argument("--q4k-only", action="store_true",
                     help="only run the Q4_K config-1 GEMV pools (the command their rocprofv3 "
                          "profiles are taken with) and exit")
@@ -576,6 +615,11 @@ def main():
         r = q4k_verify_bench(be, args.layers, args.seed, verify_inputs(args.seed),
                              steps=min(args.steps, 100))
         log("bench: Q4_K verify step " + json.dumps(r))
+        be.close()
+        return
+    if args.mtp_loop_only:
+        log("bench: MTP loop " + json.dumps(mtp_loop_bench(be, args.layers, args.seed, args.recipe,
+                                                           steps=min(args.steps, 40))))
         be.close()
         return
     if args.lm_head_only:

@@ -194,9 +194,14 @@ class DeviceEngine:
         self.d_x, self.d_xn, self.d_hprev = be.alloc(4 * H), be.alloc(4 * H), be.alloc(4 * H)
         self.d_t4, self.d_l4 = be.alloc(16 * m), be.alloc(16 * m)
         self.d_ids, self.d_w = be.alloc(2 * 8 * m * L), be.alloc(4 * 8 * m * L)
-        self.d_u, self.d_ur = be.alloc(4 * k), be.alloc(4 * m)
-        self.d_acc, self.d_toks, self.d_status = be.alloc(4), be.alloc(4 * m), be.alloc(4)
+        self.d_status = be.alloc(4)
         self.d_sel_u, self.d_sel_acc, self.d_sel_tok = be.alloc(4), be.alloc(4), be.alloc(4 * m)
+        # a speculative step's host traffic, one write and one read: the verify
+        # rows' tokens (boundary, then the drafts as the device picks them),
+        # the uniforms u [k], ur [k + 1], ud [k], then the acceptance's outputs
+        # (accepted length, emitted tokens [k + 1])
+        self.io_words = (k + 1) + k + (k + 1) + k + 1 + (k + 1)
+        self.d_io = be.alloc(4 * self.io_words)
         be.write(self.d_status, np.zeros(1, np.int32))
 
     # ---- stages ------------------------------------------------------------------------
@@ -257,20 +262,33 @@ class DeviceEngine:
         self.be.copy_device(self.d_hprev, self.d_h, 4 * H)
         return t, self._plain_trace([boundary], u)
 
+    def _io(self, word: int, n: int = 1) -> DeviceBuffer:
+        return self.be.view(self.d_io, 4 * word, 4 * n)
+
     def speculative(self, step: int, boundary: int):
-        """Draft k tokens, verify [boundary, drafts], accept."""
+        """Draft k tokens, verify [boundary, drafts], accept.  The drafts are
+        picked on the device and feed the next draft's embedding from device
+        memory, so the step's only host traffic is one write (tokens and
+        uniforms) before it and one read (drafts, acceptance) after it, unless
+        tracing."""
         be, md, k, V = self.be, self.model, self.k, self.model.vocab
         u = synth.philox_uniforms(self.seed + step, 0, k)
         ur = synth.philox_uniforms(self.seed + step, 1, k + 1)
         ud = synth.philox_uniforms(self.seed + step, 2, k)
+        w_tok, w_u, w_ur, w_ud = 0, k + 1, 2 * k + 1, 3 * k + 2
+        w_acc, w_toks = 4 * k + 2, 4 * k + 3
+        io = np.zeros(w_acc, np.uint32)
+        io[w_tok] = boundary
+        io[w_u:w_u + k] = u.view(np.uint32)
+        io[w_ur:w_ur + k + 1] = ur.view(np.uint32)
+        io[w_ud:w_ud + k] = ud.view(np.uint32)
+        be.write(self.d_io, io)
         trace = dict(draft_x=[], draft_y=[], draft_yn=[]) if self.trace_on else {}
         # draft: x = h_prev + embed(d_prev); x += MoE_mtp(rmsnorm(x)); logits
-        drafts, prev = [], boundary
         stack, norm = (md.target, md.norm) if self.self_draft else (md.draft, md.draft_norm)
         be.copy_device(self.d_x, self.d_hprev, 4 * H)
         for i in range(k):
-            be.write(self.d_tok, np.array([prev], np.int32))
-            be.embed_rows_device(md.embed, self.d_tok, 1, self.d_x,
+            be.embed_rows_device(md.embed, self._io(w_tok + i), 1, self.d_x,
                                  d_add=None if self.self_draft else self.d_x, d_status=self.d_status)
             if self.trace_on:
                 trace["draft_x"].append(self._snap(self.d_x, (H,)))
@@ -281,29 +299,44 @@ class DeviceEngine:
             if self.trace_on:
                 trace["draft_y"].append(self._snap(self.d_x, (H,)))
                 trace["draft_yn"].append(self._snap(self.d_xn, (H,)))
-            prev = self._pick(d_row, 0, float(ud[i]))
-            drafts.append(prev)
+            # the draft token, into the verify rows: the fused top-1, or one
+            # draw (the acceptance at k = 0 with its uniform ud[i])
+            if self.greedy:
+                src = be.view(self.d_t4, 0, 4)
+            else:
+                d_ud = self._io(w_ud + i)
+                be.accept_device(d_row, d_row, self._io(w_tok), 0, V, self.T, False, d_ud, d_ud,
+                                 self.d_sel_acc, self.d_sel_tok)
+                src = be.view(self.d_sel_tok, 0, 4)
+            be.copy_device(self._io(w_tok + 1 + i), src, 4)
         # verify and accept
-        rows = [boundary] + drafts
-        self._target_pass(rows)
-        be.write(self.d_tok, np.asarray(drafts, np.int32))
-        be.write(self.d_u, u)
-        be.write(self.d_ur, ur)
-        be.accept_device(self.d_target, None if self.greedy else self.d_draft, self.d_tok, k, V,
-                         self.T, self.greedy, None if self.greedy else self.d_u,
-                         None if self.greedy else self.d_ur, self.d_acc, self.d_toks)
-        a = int(be.read(self.d_acc, np.int32, (1,))[0])
-        toks = be.read(self.d_toks, np.int32, (k + 1,))
+        self._target_pass_device(self._io(w_tok, k + 1), k + 1)
+        be.accept_device(self.d_target, None if self.greedy else self.d_draft, self._io(w_tok + 1, k),
+                         k, V, self.T, self.greedy, None if self.greedy else self._io(w_u, k),
+                         None if self.greedy else self._io(w_ur, k + 1), self._io(w_acc),
+                         self._io(w_toks, k + 1))
+        out = be.read(self.d_io, np.int32, (self.io_words,))
         self._check_status()
+        drafts = [int(v) for v in out[w_tok + 1:w_tok + 1 + k]]
+        a = int(out[w_acc])
         if a < 0:
             raise RuntimeError("the acceptance kernel reported a timed-out exchange")
-        emitted = [int(v) for v in toks[: a + 1]]
+        emitted = [int(v) for v in out[w_toks:w_toks + a + 1]]
         if self.trace_on:
-            trace.update(self._plain_trace(rows, None))
+            trace.update(self._plain_trace([boundary] + drafts, None))
             trace.update(drafts=drafts, u=u, ur=ur, ud=ud, draft=self._snap(self.d_draft, (k, V)))
         # the hidden row whose prediction produced the last emitted token
         be.copy_device(self.d_hprev, be.view(self.d_h, 4 * a * H, 4 * H), 4 * H)
         return emitted, a, trace
+
+    def _target_pass_device(self, d_tokens: DeviceBuffer, n: int) -> None:
+        """_target_pass over tokens already on the device."""
+        be, md = self.be, self.model
+        be.embed_rows_device(md.embed, d_tokens, n, self.d_hin, d_status=self.d_status)
+        be.copy_device(self.d_h, self.d_hin, 4 * n * H)
+        be.stack_forward_device(md.target.stack, self.d_h, n, self.d_ids, self.d_w, self.d_status)
+        be.rmsnorm_rows_device(self.d_h, n, H, md.norm, self.d_hn)
+        be.lm_head_logits_device(md.lm_head, self.d_hn, n, self.d_target, self.d_t4, self.d_l4)
 
     def free(self) -> None:
         for name, b in list(vars(self).items()):
