@@ -71,7 +71,12 @@ def test_q6k_matvec_reference_kat(backend):
 
 @pytest.mark.parametrize("rows,cols,m", [(1, 256, 1), (17, 512, 1), (512, 2048, 4),
                                          (2048, 512, 4), (65, 2304, 3), (130, 4096, 8),
-                                         (200, 768, 2)])
+                                         (200, 768, 2),
+                                         # the streamed kernel (64 blocks a row): padded
+                                         # super-blocks, padded rows, two token passes,
+                                         # two rounds of row octets per wavefront
+                                         (100, 1536, 3), (70, 2048, 8), (3001, 1792, 2),
+                                         (20000, 2048, 2)])
 def test_q6k_matvec_bit_identical(backend, rows, cols, m):
     w_bytes = q6_k_matrix(rows, cols, 3 * rows + cols)
     x = np.random.default_rng(rows + 7 * m).standard_normal((m, cols)).astype(np.float32)
@@ -121,6 +126,32 @@ def test_lm_head_candidates_ties_and_nan(backend):
     tw, lw = oracle_top4(want)
     assert np.array_equal(t4, tw) and same_bits(l4, lw)
     assert list(t4[0]) == [5, 41, 600, 700]
+    backend.free_weights(w)
+
+
+@pytest.mark.parametrize("m", [1, 5])
+def test_lm_head_candidates_ties_and_nan_streamed(backend, m):
+    # the streamed kernel's per-lane lists: tied logits (0.0) in rows that one
+    # lane meets in both of its rounds (5 and 16389, 16384 rows a round),
+    # NaN rows in both rounds, the rest negative; m = 5 runs two token passes
+    rows, cols = 20000, 2048
+    w_bytes = q6_k_matrix(rows, cols, 14).reshape(rows, 8, 210)
+    w_bytes[:, :, 208:210] = np.array([0.01], np.float16).view(np.uint8)
+    w_bytes[:, :, 0:192] = 0x00
+    w_bytes[:, :, 192:208] = 1
+    x = np.ones((m, cols), np.float32)
+    for r in (16389, 5, 19999, 600, 41):
+        w_bytes[r, :, 208:210] = 0
+    for r in (2, 16384):
+        w_bytes[r, :, 208:210] = np.array([np.nan], np.float16).view(np.uint8)
+    w_bytes = w_bytes.reshape(-1)
+    w = backend.upload_q6_k(w_bytes, rows, cols)
+    y, t4, l4 = backend.lm_head_logits(w, x)
+    want = np.stack([orc.q6_k_matvec(w_bytes, rows, cols, x[t]) for t in range(m)])
+    assert same_bits(y, want)
+    tw, lw = oracle_top4(want)
+    assert np.array_equal(t4, tw) and same_bits(l4, lw)
+    assert list(t4[0]) == [5, 41, 600, 16389]
     backend.free_weights(w)
 
 
