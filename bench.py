@@ -289,6 +289,30 @@ def q4k_verify_bench(be, n_layers: int, seed: int, inputs, steps: int = 50, warm
     return out
 
 
+def gemv_pool_bench(be, n_mats: int, seed: int):
+    """Config-1 GEMV bandwidth: one token against a rotating pool of distinct
+    512 x 2048 Q4_0 matrices (far beyond the 256 MB Infinity Cache), one launch
+    per call, HIP events around the launches."""
+    from turboqwenfare_amd import _lib, synth
+
+    pool = [be.synth_q4_0(512, 2048, 900_000 + i, seed) for i in range(n_mats)]
+    dx = be.to_device(synth.normal((2048,), seed=seed))
+    dy = be.alloc(n_mats * 512 * 4)
+    be.q4_gemv_batched_device(pool, dx, dy)
+    be.profile_enable(True)
+    for _ in range(10):
+        be.q4_gemv_batched_device(pool, dx, dy)
+    n, ms, by = be.profile_read(_lib.KERNEL_GEMV)
+    be.profile_enable(False)
+    gemv = dict(matrices=n_mats, bytes_per_launch=by / n, avg_us=ms / n * 1e3, gbs=by / (ms * 1e-3) / 1e9)
+    gemv["frac"] = gemv["gbs"] / HBM_PEAK_GBS
+    for w in pool:
+        be.free_weights(w)
+    be.free(dx)
+    be.free(dy)
+    return gemv
+
+
 def lm_head_bench(be, seed: int, iters: int = 20):
     """The LM head at the configs' vocabulary: Q6_K [151,936 x 2048] (255 MB,
     the canonical checkpoint's lm_head format) against the M = 4 verify rows,
@@ -585,6 +609,9 @@ def main():
                     help="only the verify step with Q4_K expert layers")
     ap.add_argument("--mtp-loop-only", action="store_true",
                     help="only the MTP decode loop at full depth (draft head and self-drafting)")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="only run the Q4_0 config-1 GEMV pool (the command its rocprofv3 profile "
+                         "is taken with) and exit")
     ap.add_argument("--q4k-only", action="store_true",
                     help="only run the Q4_K config-1 GEMV pools (the command their rocprofv3 "
                          "profiles are taken with) and exit")
@@ -624,6 +651,10 @@ def main():
         return
     if args.lm_head_only:
         log("bench: LM head " + json.dumps(lm_head_bench(be, args.seed)))
+        be.close()
+        return
+    if args.gemv_only:
+        log("bench: config-1 GEMV pool " + json.dumps(gemv_pool_bench(be, args.gemv_pool, args.seed)))
         be.close()
         return
     if args.q4k_only:
@@ -674,26 +705,7 @@ def main():
         extras[f"{other}_recipe"]["stack_us"] = r["kernels"].get("stack", {}).get("avg_us")
         log(f"bench: {other} recipe " + json.dumps(extras[f"{other}_recipe"]))
 
-        # Config-1 GEMV bandwidth: a rotating pool of distinct 512x2048
-        # matrices (far beyond the 256 MB Infinity Cache), one launch.
-        from turboqwenfare_amd import _lib, synth
-
-        pool = [be.synth_q4_0(512, 2048, 900_000 + i, args.seed) for i in range(args.gemv_pool)]
-        dx = be.to_device(synth.normal((2048,), seed=args.seed))
-        dy = be.alloc(args.gemv_pool * 512 * 4)
-        be.q4_gemv_batched_device(pool, dx, dy)
-        be.profile_enable(True)
-        for _ in range(10):
-            be.q4_gemv_batched_device(pool, dx, dy)
-        n, ms, by = be.profile_read(_lib.KERNEL_GEMV)
-        be.profile_enable(False)
-        gemv = dict(matrices=args.gemv_pool, bytes_per_launch=by / n, avg_us=ms / n * 1e3,
-                    gbs=by / (ms * 1e-3) / 1e9)
-        gemv["frac"] = gemv["gbs"] / HBM_PEAK_GBS
-        for w in pool:
-            be.free_weights(w)
-        be.free(dx)
-        be.free(dy)
+        gemv = gemv_pool_bench(be, args.gemv_pool, args.seed)
         extras["gemv_config1"] = gemv
         log("bench: config-1 GEMV pool " + json.dumps(gemv))
         extras["q4k_config1"] = q4k_pool_bench(be, args.gemv_pool, args.seed)
