@@ -181,8 +181,9 @@ int32_t tqf_hip_stack_free(tqf_hip_ctx *ctx, tqf_hip_stack *stack);
  * caller) is set to TQF_HIP_ERR_ROUTER if any layer's routing fails.
  * Every layer of a stack has one expert format.  For Q4_0 layers with
  * m <= 4 on the model geometry (hidden 2048, width <= 2048, <= 256
- * experts) the whole stack runs as one persistent cooperative launch (a
- * failed co-scheduling wait reports TQF_HIP_ERR_DEVICE in *d_status);
+ * experts) the whole stack runs as one persistent launch of one workgroup
+ * per CU (a failed co-scheduling wait reports TQF_HIP_ERR_DEVICE in
+ * *d_status);
  * otherwise the per-layer kernels are captured once into a HIP graph per
  * argument set and replayed. */
 int32_t tqf_hip_stack_forward_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack,

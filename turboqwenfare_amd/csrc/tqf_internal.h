@@ -324,7 +324,8 @@ struct StackScratch {
     uint32_t experts = 0, bp_down = 0, members = 0;
 };
 // Workgroups of a persistent launch (0 if the device cannot co-schedule it)
-// and the launcher; `grid` workgroups must be co-resident (cooperative launch).
+// and the launcher; `grid` workgroups must be co-resident (they are when the
+// device runs nothing else; a grid-barrier wait that times out reports an error).
 uint32_t stack_grid(int device, uint32_t bp_down);
 hipError_t launch_stack(hipStream_t s, const StackArgs &a, uint32_t grid, uint32_t bp_down);
 size_t stack_lds_bytes(uint32_t bp_down, uint32_t members);

@@ -1,6 +1,7 @@
 // tqf_stack.hip -- the persistent MoE-stack kernel for gfx950.
 //
-// One cooperative launch runs every layer of a stack over M <= 4 verify rows:
+// One persistent launch (one workgroup per CU, all co-resident) runs every
+// layer of a stack over M <= 4 verify rows:
 //   h <- h + MoE_l(rmsnorm_l(h))        (model/qwen36/runtime.rs:777-802)
 // with MoE_l = shared expert * sigmoid(gate . x) + sum_k w_k expert_k(x) over
 // the router's top-8 (experts/mod.rs:1540-1634).  Per layer two phases are
@@ -1260,13 +1261,18 @@ uint32_t stack_grid(int device, uint32_t bp_down) {
     return grid;
 }
 
+// A plain launch: the grid (one workgroup per compute unit, checked against
+// the occupancy limit by stack_grid) is co-resident whenever the device runs
+// nothing else, and every grid-barrier wait is bounded (a timeout reports
+// TQF_HIP_ERR_DEVICE), so the cooperative launch's guarantee is not needed;
+// it cost about 15 us of dispatch per launch.
 hipError_t launch_stack(hipStream_t s, const StackArgs &a, uint32_t grid, uint32_t bp_down) {
     const void *k = kernel_for(bp_down, a.members);
     if (!k) return hipErrorInvalidValue;
     StackArgs args = a;
     void *params[] = {&args};
-    return hipLaunchCooperativeKernel(k, dim3(grid), dim3(kThreads), params,
-                                      (unsigned int)stack_lds_bytes(bp_down, a.members), s);
+    return hipLaunchKernel(k, dim3(grid), dim3(kThreads), params, (unsigned int)stack_lds_bytes(bp_down, a.members),
+                           s);
 }
 
 }  // namespace tqf
