@@ -284,6 +284,11 @@ struct StackLayer {
 constexpr int kStackMT = 4;        // tokens of one persistent launch (k <= 3)
 constexpr int kStackHidden = 2048; // the persistent kernel's hidden size
 constexpr int kStackTeams = kStackHidden / 64;
+// Grid-barrier arrivals go through two levels of counters: 256 same-address
+// atomics from every compute unit serialise at the coherence point, and
+// groups of workgroups (blockIdx mod 8 is one XCD under the round-robin
+// dispatch) counting on lines of their own first shorten that chain.
+constexpr int kStackBarrierGroups = 8;
 struct StackSync {
     uint32_t barrier;  // arrivals (atomic adds only)
     uint32_t exit;
@@ -292,6 +297,10 @@ struct StackSync {
     uint32_t abort;    // one 64-bit poll load, on its own cache line
     uint32_t pad1[30];
     uint32_t seq;  // launches completed (every launch advances it once, at its exit)
+    uint32_t pad2[31];
+    // first-level arrivals: workgroup b counts on line b % kStackBarrierGroups
+    // (one line per group; the last arrival of a group counts on `barrier`)
+    uint32_t group[kStackBarrierGroups][32];
 };
 struct StackArgs {
     const StackLayer *layers;

@@ -223,8 +223,13 @@ __device__ void barrier_arrive(StackSync *sync, uint32_t &epoch) {
     lds_barrier();
     ++epoch;
     if (tid() == kPoller) {
-        const uint32_t target = epoch * gridDim.x;
-        const bool last = counter_arrive(&sync->barrier) + 1 == target;
+        // first the workgroup's group line, then (last of its group) the grid's
+        const uint32_t G = kStackBarrierGroups;
+        const uint32_t grp = blockIdx.x % G, groups = gridDim.x < G ? gridDim.x : G;
+        const uint32_t per = (gridDim.x - grp + G - 1) / G;  // workgroups in group grp
+        bool last = false;
+        if (counter_arrive(&sync->group[grp][0]) + 1 == epoch * per)
+            last = counter_arrive(&sync->barrier) + 1 == epoch * groups;
         // last arrival: release everyone (the poll line sees no atomics)
         if (last) __hip_atomic_store(&sync->release, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         P.arrived_last = last ? 1 : 0;
@@ -301,6 +306,7 @@ __device__ void stack_exit(StackSync *sync, uint64_t *lacc, uint32_t seq) {
         if (counter_arrive(&sync->exit) == gridDim.x - 1) {
             P.last = __hip_atomic_load(&sync->abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ? 2 : 1;
             counter_reset(&sync->barrier);
+            for (int g = 0; g < kStackBarrierGroups; ++g) counter_reset(&sync->group[g][0]);
             counter_reset(&sync->release);
             counter_reset(&sync->abort);
             counter_reset(&sync->exit);
