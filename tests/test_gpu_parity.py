@@ -8,7 +8,7 @@ import pytest
 import cpu_oracle as orc
 from conftest import rel_err
 from turboqwenfare_amd import _lib, mtp, synth
-from turboqwenfare_amd._lib import ERR_INVALID, ERR_ROUTER, HipError
+from turboqwenfare_amd._lib import ERR_DEVICE, ERR_INVALID, ERR_ROUTER, HipError
 
 pytestmark = pytest.mark.gpu
 
@@ -476,6 +476,29 @@ def test_persistent_stack_reports_router_error(backend, stack3):
     h0[2, 100] = np.inf
     _, _, _, status = _stack_run(backend, st, h0, 4, 3, True)
     assert status == ERR_ROUTER
+
+
+@pytest.mark.parametrize("fail_at", [0, 2])
+def test_persistent_stack_abort_leaves_clean_state(backend, stack3, monkeypatch, fail_at):
+    """A grid-barrier wait that times out aborts the launch: every workgroup
+    leaves at its next bounded wait, the launch reports TQF_HIP_ERR_DEVICE,
+    and the last workgroup out resets the barrier state (both counter levels,
+    release, abort) and the logit accumulators, so the following launches are
+    bit-identical to one before the failure.  The timeout is forced from the
+    host (workgroup 0 takes the barrier-B wait of layer `fail_at` as timed
+    out), so every kernel exits normally."""
+    _, _, st = stack3
+    h0 = synth.normal((4, 2048), seed=413)
+    first = _stack_run(backend, st, h0, 4, 3, True)
+    assert first[3] == 0
+    monkeypatch.setenv("TQF_HIP_STACK_FAIL_AT_LAYER", str(fail_at))
+    _, _, _, status = _stack_run(backend, st, h0, 4, 3, True)
+    assert status == ERR_DEVICE
+    monkeypatch.delenv("TQF_HIP_STACK_FAIL_AT_LAYER")
+    for _ in range(2):
+        again = _stack_run(backend, st, h0, 4, 3, True)
+        assert again[3] == 0
+        assert np.array_equal(again[0], first[0]) and np.array_equal(again[1], first[1])
 
 
 @pytest.mark.parametrize("persistent", [True, False], ids=["persistent", "per_layer"])

@@ -503,6 +503,10 @@ int32_t enqueue_stack_persistent(tqf_hip_ctx *ctx, const tqf_hip_stack *st, cons
     a.ssq = sc.ssq;
     a.sync = sc.sync;
     a.members = members;
+    // a barrier timeout forced from the host, for the tests of the abort path
+    // (TQF_HIP_STACK_FAIL_AT_LAYER = l); read at every launch
+    const char *fail_at = std::getenv("TQF_HIP_STACK_FAIL_AT_LAYER");
+    a.fail_at = fail_at && *fail_at ? (uint32_t)std::strtoul(fail_at, nullptr, 10) : ~0u;
     Prof p(ctx);
     hipError_t e = launch_stack(ctx->stream, a, grid, bp_down);
     if (e != hipSuccess) return hip_fail(ctx, "persistent stack kernel launch", e);

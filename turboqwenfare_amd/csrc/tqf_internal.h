@@ -318,6 +318,7 @@ struct StackArgs {
     float *ssq;         // [teams x kStackMT]
     StackSync *sync;
     uint32_t members;   // workgroups per 64-row team in phase C
+    uint32_t fail_at;   // layer whose barrier-B wait workgroup 0 takes as timed out (~0u: none)
 };
 // Words of one parity of the logit accumulator: kStackMT rows of the 256
 // routed experts and the shared-expert gate, then a non-finite flag.

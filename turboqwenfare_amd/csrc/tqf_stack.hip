@@ -247,10 +247,18 @@ __device__ __forceinline__ uint64_t poll_load(const uint64_t *word) {
 
 // The poller keeps three loads of the release word in flight, so a release
 // is seen about one round trip after it lands rather than up to two.
-__device__ bool grid_wait(StackSync *sync, uint32_t epoch, int32_t *status) {
+// `fail` takes the wait as timed out without polling (a timeout forced from
+// the host, so that the abort path can be tested with every wait bounded).
+__device__ bool grid_wait(StackSync *sync, uint32_t epoch, int32_t *status, bool fail = false) {
     if (tid() == kPoller) {
         int ok = 1;
-        if (!P.arrived_last) {
+        if (fail) {
+            __hip_atomic_store(&sync->abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (status)
+                __hip_atomic_store(status, (int32_t)TQF_HIP_ERR_DEVICE, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            ok = 0;
+        } else if (!P.arrived_last) {
             const uint64_t *word = reinterpret_cast<const uint64_t *>(&sync->release);
             uint64_t v0 = poll_load(word);
             __builtin_amdgcn_s_sleep(1);
@@ -1173,7 +1181,7 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
         // this member's share of the next layer's router rows, gate and norm
         ShareLoads SL;
         if (l + 1 < a.n_layers) share_loads(a, l + 1, SL);
-        if (!(ok = grid_wait(a.sync, epoch, a.status))) break;
+        if (!(ok = grid_wait(a.sync, epoch, a.status, l == a.fail_at && blockIdx.x == 0))) break;
         // the next layer's expert-matrix table: loads now, LDS after phase C
         // (whose down weights still come from this layer's table)
         const bool more = l + 1 < a.n_layers;
