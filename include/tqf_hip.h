@@ -201,7 +201,9 @@ int32_t tqf_hip_stack_forward_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stac
  * norm(max(0, p - q)) with u_resample[i]; if all k are accepted the bonus
  * token is drawn from p_k with u_resample[k].  Writes *accepted (0..k) and
  * tokens_out[k+1] (tokens_out[0..accepted] are emitted, the rest are -1).
- * Bit-exact with the CPU definition for identical inputs. */
+ * Bit-exact with the CPU definition for identical inputs.  An exchange
+ * between workgroups that does not complete within 20 ms writes
+ * *accepted = -1; the next call runs normally. */
 int32_t tqf_hip_accept(tqf_hip_ctx *ctx, const float *target, const float *draft,
                        const int32_t *draft_tokens, uint32_t k, uint32_t vocab, float temperature,
                        int32_t greedy, const float *u, const float *u_resample, int32_t *accepted,

@@ -176,6 +176,34 @@ def test_device_entry_point_matches_host(backend):
         backend.free(b)
 
 
+def test_poll_timeout_reports_failure_and_recovers(backend, monkeypatch):
+    """An exchange that times out makes the one-launch acceptance write
+    accepted = -1, and every workgroup still leaves (the others time out on
+    the first one's missing sums within 20 ms); the next call is bit-exact
+    again.  The timeout is forced from the host (workgroup 0 takes its first
+    exchange as timed out), so the kernel exits normally."""
+    target, draft, dtok, u, ur = case(17)
+    bufs = [backend.to_device(a) for a in (target, draft, dtok, u, ur)]
+    acc = backend.alloc(4)
+    toks = backend.alloc(16)
+    want = orc.accept(target, draft, dtok, 0.7, False, u, ur)
+
+    def run():
+        backend.accept_device(bufs[0], bufs[1], bufs[2], 3, V, 0.7, False, bufs[3], bufs[4], acc,
+                              toks)
+        a = int(backend.read(acc, np.int32, (1,))[0])
+        return a, [int(v) for v in backend.read(toks, np.int32, (4,))[: a + 1]]
+
+    assert run() == want
+    monkeypatch.setenv("TQF_HIP_ACCEPT_FAIL_POLL", "1")
+    assert run()[0] == -1
+    monkeypatch.delenv("TQF_HIP_ACCEPT_FAIL_POLL")
+    for _ in range(2):
+        assert run() == want
+    for b in bufs + [acc, toks]:
+        backend.free(b)
+
+
 def test_matches_committed_golden(backend):
     """The committed oracle outcomes (tests/golden/oracle_vectors.npz) for
     seeds 0..63, greedy and stochastic, at V = 1000, k = 3."""

@@ -31,6 +31,8 @@
 // counters return to zero in the workgroup that finishes the kernel.
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
+
 #include "tqf_device.h"
 #include "tqf_internal.h"
 
@@ -306,6 +308,7 @@ struct AccArgs {
     int32_t *tokens;
     uint8_t *scratch;
     uint32_t ept;  // one-launch path: elements per thread
+    uint32_t fail_poll;  // one-launch path: workgroup 0 takes its first exchange as timed out
 };
 
 struct Acc {
@@ -1017,7 +1020,8 @@ __global__ __launch_bounds__(kFuseThreads) void acc_fused_kernel(AccArgs a) {
     }
     // ---- 2: row maxima, then the chunk's exact sums of E_x ---------------------
     if (__syncthreads_or(!fuse_poll(xmax, nullptr, rows * nch, tag,
-                                    [&](uint32_t i, uint64_t p) { atomicMax(&s_key[i / nch], (uint32_t)p); }))) {
+                                    [&](uint32_t i, uint64_t p) { atomicMax(&s_key[i / nch], (uint32_t)p); }) ||
+                         (a.fail_poll && c == 0))) {
         fail();
         return;
     }
@@ -1296,8 +1300,12 @@ hipError_t launch_accept(hipStream_t s, const float *target, const float *draft,
                          const int32_t *dtok, uint32_t k, uint32_t vocab, float temperature,
                          int32_t greedy, const float *u, const float *ures, int32_t *accepted,
                          int32_t *tokens, void *scratch, hipEvent_t ev_start, hipEvent_t ev_stop) {
+    // a poll timeout forced from the host, for the tests of the failure path
+    // (TQF_HIP_ACCEPT_FAIL_POLL = 1); read at every launch
+    const char *fail_poll = std::getenv("TQF_HIP_ACCEPT_FAIL_POLL");
     AccArgs a{target, draft, dtok, k, vocab, temperature, greedy, u, ures, accepted, tokens,
-              reinterpret_cast<uint8_t *>(scratch), fuse_ept(vocab)};
+              reinterpret_cast<uint8_t *>(scratch), fuse_ept(vocab),
+              fail_poll && fail_poll[0] && fail_poll[0] != '0' ? 1u : 0u};
     if (ev_start) (void)hipEventRecord(ev_start, s);
     if (fuse_fits(k, vocab)) {
         // one plain launch: a cooperative launch measured about 15 us of
