@@ -175,3 +175,35 @@ def test_verify_step40_matches_stack_and_acceptance_oracle(backend, model40, gre
         assert (a, [int(v) for v in tk[: a + 1]]) == want
     for b in list(bufs.values()) + [dh, acc, toks, dst]:
         be.free(b)
+
+
+def test_verify_step40_repeats_bit_identically(backend, model40):
+    """300 verify steps in a row at full depth: every step's h, accepted
+    length and tokens bit-identical to the first, status zero.  The barrier
+    counters of both levels, the logit accumulators and the partial-word tags
+    return to their start state at every launch."""
+    be, m, k, vocab, T = backend, 4, 3, 151936, 0.7
+    rng = np.random.default_rng(12)
+    target = (rng.standard_normal((k + 1, vocab)) * 3.0).astype(np.float32)
+    draft = (rng.standard_normal((k, vocab)) * 3.0).astype(np.float32)
+    dtok = np.argmax(draft, axis=1).astype(np.int32)
+    u = synth.philox_uniforms(1, 0, k)
+    ur = synth.philox_uniforms(1, 1, k + 1)
+    bufs = {n: be.to_device(a) for n, a in dict(t=target, d=draft, dt=dtok, u=u, ur=ur,
+                                                 h0=h0_rows(m)).items()}
+    dh, acc, toks = be.alloc(m * H * 4), be.alloc(4), be.alloc(4 * (k + 1))
+    dst = be.to_device(np.zeros(1, np.int32))
+    first = None
+    for rep in range(300):
+        be.verify_step_device(model40.stack, bufs["h0"], dh, m, bufs["t"], bufs["d"], bufs["dt"],
+                              vocab, T, False, bufs["u"], bufs["ur"], acc, toks, dst)
+        out = (be.read(dh, np.float32, (m, H)).view(np.uint32), int(be.read(acc, np.int32, (1,))[0]),
+               be.read(toks, np.int32, (k + 1,)).copy(), int(be.read(dst, np.int32, (1,))[0]))
+        assert out[3] == 0, f"step {rep}: status {out[3]}"
+        if first is None:
+            first = out
+        else:
+            assert out[1] == first[1] and np.array_equal(out[2], first[2]), f"step {rep}: tokens differ"
+            assert np.array_equal(out[0], first[0]), f"step {rep}: h differs"
+    for b in list(bufs.values()) + [dh, acc, toks, dst]:
+        be.free(b)
