@@ -743,7 +743,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 weights, fp32 activations, int8 dot4 + fp32 accumulate",
+        "dtype": "q4_0 weights; activations as block fixed point (each value a 22-bit integer "
+                 "times its 32-element block's power-of-two scale, i.e. rounded to 2^-23 of the "
+                 "block maximum), exact int4 digit dots into int32, fp32 accumulate",
         "data": f"synthetic (seeded Philox Q4_0 experts, nibble recipe {args.recipe}, N(0,1) "
                 f"activations, N(0,9) logits)",
         "config": {"workload": f"config 4: full-depth MTP verify step, 40 MoE layers at M=4 (k=3) "

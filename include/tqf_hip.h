@@ -182,9 +182,14 @@ int32_t tqf_hip_stack_free(tqf_hip_ctx *ctx, tqf_hip_stack *stack);
  * Every layer of a stack has one expert format.  For Q4_0 layers with
  * m <= 4 on the model geometry (hidden 2048, width <= 2048, <= 256
  * experts) the whole stack runs as one persistent launch of one workgroup
- * per CU (a failed co-scheduling wait reports TQF_HIP_ERR_DEVICE in
- * *d_status);
- * otherwise the per-layer kernels are captured once into a HIP graph per
+ * per CU, which needs every workgroup resident at once.  If other work on
+ * the device keeps it from being co-scheduled, its waits time out after
+ * 20 ms; with TQF_HIP_VARIANT_RECOVER (the default) the call then re-runs the
+ * stack through the per-layer kernels and returns their result (counted by
+ * tqf_hip_recovery_counts), for which it waits for the persistent launch
+ * before returning; with the variant off the call stays asynchronous and a
+ * timed-out launch reports TQF_HIP_ERR_DEVICE in *d_status, d_h undefined.
+ * Otherwise the per-layer kernels are captured once into a HIP graph per
  * argument set and replayed. */
 int32_t tqf_hip_stack_forward_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack,
                                      const float *d_h_in, float *d_h, uint32_t m,
@@ -201,9 +206,15 @@ int32_t tqf_hip_stack_forward_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stac
  * norm(max(0, p - q)) with u_resample[i]; if all k are accepted the bonus
  * token is drawn from p_k with u_resample[k].  Writes *accepted (0..k) and
  * tokens_out[k+1] (tokens_out[0..accepted] are emitted, the rest are -1).
- * Bit-exact with the CPU definition for identical inputs.  An exchange
- * between workgroups that does not complete within 20 ms writes
- * *accepted = -1; the next call runs normally. */
+ * Bit-exact with the CPU definition for identical inputs.  Vocabularies up
+ * to about one million run as one launch whose workgroups exchange partials
+ * and so must all be resident at once.  An exchange that does not complete
+ * within 20 ms (other work holding compute units) makes that launch write
+ * *accepted = -1; with TQF_HIP_VARIANT_RECOVER (the default) the call then
+ * re-runs the acceptance through the three-kernel path (no waits between
+ * workgroups; the same bits) and returns its result, for which the device
+ * form waits for the launch before returning; with the variant off the -1
+ * stays and the next call runs normally. */
 int32_t tqf_hip_accept(tqf_hip_ctx *ctx, const float *target, const float *draft,
                        const int32_t *draft_tokens, uint32_t k, uint32_t vocab, float temperature,
                        int32_t greedy, const float *u, const float *u_resample, int32_t *accepted,
@@ -356,7 +367,9 @@ int32_t tqf_hip_lm_head_logits_device(tqf_hip_ctx *ctx, const tqf_hip_weights *w
  * dequantize_q4_0(row d_tokens[i] of emb) (+ d_add[i] when d_add is given),
  * [n x cols] f32.  emb is a Q4_0 handle [V x cols].  A token outside [0, V)
  * gives a NaN row and, when d_status is given, TQF_HIP_ERR_INVALID there
- * (the reference's ModelError::Shape, runtime.rs:392-399). */
+ * (the reference's ModelError::Shape, runtime.rs:392-399).  d_add may be
+ * d_out (in place: each element is read, then written, by the same thread);
+ * any other overlap of d_add and d_out is not allowed. */
 int32_t tqf_hip_embed_rows_device(tqf_hip_ctx *ctx, const tqf_hip_weights *emb, const int32_t *d_tokens,
                                   uint32_t n, const float *d_add, float *d_out, int32_t *d_status);
 /* RMSNorm rows: the final norm ahead of the LM head (runtime.rs:430-431,
@@ -372,10 +385,13 @@ int32_t tqf_hip_rmsnorm_rows_device(tqf_hip_ctx *ctx, const float *d_x, uint32_t
  *      d_status (device int32, may be null): the stack's device status, as
  *      tqf_hip_stack_forward_device writes it -- TQF_HIP_ERR_ROUTER for a
  *      non-finite router logit (RouterResult::from_logits, experts/mod.rs:
- *      140-145), TQF_HIP_ERR_DEVICE for a timed-out grid barrier; never
- *      cleared by the library, so the caller zeroes it and checks it after
- *      the step.  A step that sets it has left d_h undefined; the acceptance,
- *      which reads only the logits, still runs. ---------------------------- */
+ *      140-145), TQF_HIP_ERR_DEVICE for a timed-out grid barrier when
+ *      TQF_HIP_VARIANT_RECOVER is off (with it on, the library re-runs the
+ *      timed-out part itself, as tqf_hip_stack_forward_device and
+ *      tqf_hip_accept_device do, and the call returns once the step is
+ *      complete); never cleared by the library, so the caller zeroes it and
+ *      checks it after the step.  A step that sets it has left d_h
+ *      undefined; the acceptance, which reads only the logits, still runs. */
 int32_t tqf_hip_verify_step_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack,
                                    const float *d_h_in, float *d_h, uint32_t m,
                                    const float *d_target, const float *d_draft,
@@ -387,19 +403,30 @@ int32_t tqf_hip_verify_step_device(tqf_hip_ctx *ctx, const tqf_hip_stack *stack,
 /* ---- kernel variants: the counterpart of GpuKernelKind::from_env and
  *      GpuExecutionState::kernel_kind (backend/metal/expert.rs:56-92).  Each
  *      selector starts from the environment when the context is created
- *      (TQF_HIP_PERSISTENT, TQF_HIP_Q4K_FOLD, TQF_HIP_GRAPHS: "0" selects 0,
- *      anything else or unset 1) and is changed per context here; a change
- *      drops the context's captured graphs, so no replay keeps an old
- *      choice. ----------------------------------------------------------- */
+ *      (TQF_HIP_PERSISTENT, TQF_HIP_Q4K_FOLD, TQF_HIP_GRAPHS,
+ *      TQF_HIP_RECOVER: "0" selects 0, anything else or unset 1) and is
+ *      changed per context here; a change drops the context's captured
+ *      graphs, so no replay keeps an old choice. ------------------------- */
 #define TQF_HIP_VARIANT_PERSISTENT 0 /* 1: the persistent stack kernel where it applies;
                                         0: per-layer kernels (graph-replayed)          */
 #define TQF_HIP_VARIANT_Q4K_FOLD 1   /* 1: a Q4_K layer's combine folded into its down
                                         launch; 0: the separate combine launch          */
 #define TQF_HIP_VARIANT_GRAPHS 2     /* 1: multi-launch paths replay HIP graphs;
                                         0: eager launches of the same kernels           */
-#define TQF_HIP_VARIANTS 3
+#define TQF_HIP_VARIANT_RECOVER 3    /* 1: a persistent launch whose cross-workgroup
+                                        wait times out is re-run through kernels that
+                                        do not wait on one another (the entry points
+                                        that launch one wait for it); 0: asynchronous,
+                                        the timeout reported as an error            */
+#define TQF_HIP_VARIANTS 4
 int32_t tqf_hip_set_variant(tqf_hip_ctx *ctx, int32_t variant, int32_t value);
 int32_t tqf_hip_get_variant(tqf_hip_ctx *ctx, int32_t variant, int32_t *value);
+/* Re-runs so far on this context after a timed-out persistent launch: of the
+ * stack (per-layer kernels) and of the acceptance (three-kernel path).  The
+ * counterpart of the reference's fallback when the GPU path cannot run
+ * (experts/mod.rs:480-497), reported the way ExpertCacheStats reports cache
+ * events (experts/mod.rs:201-234). */
+int32_t tqf_hip_recovery_counts(tqf_hip_ctx *ctx, uint64_t *stack_reruns, uint64_t *accept_reruns);
 
 /* ---- profiling: the HIP counterpart of backend/metal/timing.rs:23-80 ----- */
 #define TQF_HIP_KERNEL_ROUTE 0    /* rmsnorm + router + top-8 + union plan    */

@@ -5,6 +5,7 @@ import pytest
 
 import cpu_oracle as orc
 from turboqwenfare_amd import mtp, synth
+from turboqwenfare_amd import _lib
 from turboqwenfare_amd._lib import ERR_INVALID, HipError
 
 pytestmark = pytest.mark.gpu
@@ -176,30 +177,41 @@ def test_device_entry_point_matches_host(backend):
         backend.free(b)
 
 
-def test_poll_timeout_reports_failure_and_recovers(backend, monkeypatch):
+@pytest.mark.parametrize("greedy", [False, True])
+def test_poll_timeout_reports_failure_and_recovers(backend, monkeypatch, greedy):
     """An exchange that times out makes the one-launch acceptance write
-    accepted = -1, and every workgroup still leaves (the others time out on
-    the first one's missing sums within 20 ms); the next call is bit-exact
-    again.  The timeout is forced from the host (workgroup 0 takes its first
-    exchange as timed out), so the kernel exits normally."""
+    accepted = -1, and every workgroup still leaves (stochastic: the others
+    time out on the first one's missing sums within 20 ms; greedy: only
+    workgroup 0 gathers); the next call is bit-exact again.  The timeout is
+    forced from the host (workgroup 0 takes its first exchange, or the greedy
+    arg-max gather, as timed out), so the kernel exits normally."""
     target, draft, dtok, u, ur = case(17)
     bufs = [backend.to_device(a) for a in (target, draft, dtok, u, ur)]
     acc = backend.alloc(4)
     toks = backend.alloc(16)
-    want = orc.accept(target, draft, dtok, 0.7, False, u, ur)
+    want = orc.accept(target, draft, dtok, 0.7, greedy, u, ur)
 
     def run():
-        backend.accept_device(bufs[0], bufs[1], bufs[2], 3, V, 0.7, False, bufs[3], bufs[4], acc,
+        backend.accept_device(bufs[0], bufs[1], bufs[2], 3, V, 0.7, greedy, bufs[3], bufs[4], acc,
                               toks)
         a = int(backend.read(acc, np.int32, (1,))[0])
         return a, [int(v) for v in backend.read(toks, np.int32, (4,))[: a + 1]]
 
-    assert run() == want
-    monkeypatch.setenv("TQF_HIP_ACCEPT_FAIL_POLL", "1")
-    assert run()[0] == -1
-    monkeypatch.delenv("TQF_HIP_ACCEPT_FAIL_POLL")
-    for _ in range(2):
+    with backend.variant(_lib.VARIANT_RECOVER, False):
         assert run() == want
+        monkeypatch.setenv("TQF_HIP_ACCEPT_FAIL_POLL", "1")
+        assert run()[0] == -1
+        monkeypatch.delenv("TQF_HIP_ACCEPT_FAIL_POLL")
+        for _ in range(2):
+            assert run() == want
+    # with recovery (the default) the timed-out launch is re-run through the
+    # three-kernel path: the same bits, one re-run counted
+    before = backend.recovery_counts()
+    monkeypatch.setenv("TQF_HIP_ACCEPT_FAIL_POLL", "1")
+    assert run() == want
+    monkeypatch.delenv("TQF_HIP_ACCEPT_FAIL_POLL")
+    assert backend.recovery_counts() == (before[0], before[1] + 1)
+    assert run() == want and backend.recovery_counts() == (before[0], before[1] + 1)
     for b in bufs + [acc, toks]:
         backend.free(b)
 

@@ -489,16 +489,79 @@ def test_persistent_stack_abort_leaves_clean_state(backend, stack3, monkeypatch,
     out), so every kernel exits normally."""
     _, _, st = stack3
     h0 = synth.normal((4, 2048), seed=413)
-    first = _stack_run(backend, st, h0, 4, 3, True)
-    assert first[3] == 0
+    with backend.variant(_lib.VARIANT_RECOVER, False):
+        first = _stack_run(backend, st, h0, 4, 3, True)
+        assert first[3] == 0
+        monkeypatch.setenv("TQF_HIP_STACK_FAIL_AT_LAYER", str(fail_at))
+        _, _, _, status = _stack_run(backend, st, h0, 4, 3, True)
+        assert status == ERR_DEVICE
+        monkeypatch.delenv("TQF_HIP_STACK_FAIL_AT_LAYER")
+        for _ in range(2):
+            again = _stack_run(backend, st, h0, 4, 3, True)
+            assert again[3] == 0
+            assert np.array_equal(again[0], first[0]) and np.array_equal(again[1], first[1])
+
+
+@pytest.mark.parametrize("fail_at", [0, 2])
+@pytest.mark.parametrize("m", [1, 4])
+def test_persistent_stack_abort_is_recovered(backend, stack3, monkeypatch, fail_at, m):
+    """With recovery on (the default), a persistent launch whose barrier wait
+    times out is re-run by the library through the per-layer kernels from the
+    copy of h_in the launch's prologue made -- also in place, where the launch
+    itself updates h: the call reports status 0, returns exactly the per-layer
+    path's h and routes, and counts one stack re-run.  The timeout is forced
+    from the host (TQF_HIP_STACK_FAIL_AT_LAYER), so every wait still ends."""
+    _, _, st = stack3
+    h0 = synth.normal((4, 2048), seed=415 + m)
+    want = _stack_run(backend, st, h0, m, 3, False)
+    assert want[3] == 0
+    before = backend.recovery_counts()
     monkeypatch.setenv("TQF_HIP_STACK_FAIL_AT_LAYER", str(fail_at))
-    _, _, _, status = _stack_run(backend, st, h0, 4, 3, True)
-    assert status == ERR_DEVICE
+    got = _stack_run(backend, st, h0, m, 3, True)
     monkeypatch.delenv("TQF_HIP_STACK_FAIL_AT_LAYER")
-    for _ in range(2):
-        again = _stack_run(backend, st, h0, 4, 3, True)
-        assert again[3] == 0
-        assert np.array_equal(again[0], first[0]) and np.array_equal(again[1], first[1])
+    after = backend.recovery_counts()
+    assert got[3] == 0
+    assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
+    assert np.array_equal(got[2], want[2])
+    assert after == (before[0] + 1, before[1])
+    # the next launch is the persistent path again, unrecovered
+    again = _stack_run(backend, st, h0, m, 3, True)
+    assert again[3] == 0 and backend.recovery_counts() == after
+    assert np.array_equal(again[1], want[1]) and rel_err(again[0], want[0]) < FFN_TOL
+
+
+def test_verify_step_recovers_both_parts(backend, stack3, monkeypatch):
+    """A verify step whose persistent stack and one-launch acceptance both
+    time out (forced from the host) still returns the per-layer stack's h
+    and the oracle's acceptance, with one re-run of each counted."""
+    _, _, st = stack3
+    vocab, k = 151936, 3
+    rng = np.random.default_rng(33)
+    target = (rng.standard_normal((k + 1, vocab)) * 3).astype(np.float32)
+    draft = (rng.standard_normal((k, vocab)) * 3).astype(np.float32)
+    dtok = rng.integers(0, vocab, k).astype(np.int32)
+    u = rng.random(k).astype(np.float32)
+    ur = rng.random(k + 1).astype(np.float32)
+    want_acc = orc.accept(target, draft, dtok, 0.7, False, u, ur)
+    h0 = synth.normal((4, 2048), seed=431)
+    want_h = _stack_run(backend, st, h0, 4, 3, False)[0]
+    bufs = {n: backend.to_device(v) for n, v in dict(t=target, d=draft, dt=dtok, u=u, ur=ur, h0=h0).items()}
+    dh, acc, toks = backend.alloc(4 * 2048 * 4), backend.alloc(4), backend.alloc(4 * (k + 1))
+    dst = backend.to_device(np.zeros(1, np.int32))
+    before = backend.recovery_counts()
+    monkeypatch.setenv("TQF_HIP_STACK_FAIL_AT_LAYER", "1")
+    monkeypatch.setenv("TQF_HIP_ACCEPT_FAIL_POLL", "1")
+    backend.verify_step_device(st, bufs["h0"], dh, 4, bufs["t"], bufs["d"], bufs["dt"], vocab, 0.7, False,
+                               bufs["u"], bufs["ur"], acc, toks, dst)
+    monkeypatch.delenv("TQF_HIP_STACK_FAIL_AT_LAYER")
+    monkeypatch.delenv("TQF_HIP_ACCEPT_FAIL_POLL")
+    assert backend.recovery_counts() == (before[0] + 1, before[1] + 1)
+    assert int(backend.read(dst, np.int32, (1,))[0]) == 0
+    assert np.array_equal(backend.read(dh, np.float32, (4, 2048)), want_h)
+    a = int(backend.read(acc, np.int32, (1,))[0])
+    assert (a, [int(v) for v in backend.read(toks, np.int32, (k + 1,))[: a + 1]]) == want_acc
+    for b in list(bufs.values()) + [dh, acc, toks, dst]:
+        backend.free(b)
 
 
 @pytest.mark.parametrize("persistent", [True, False], ids=["persistent", "per_layer"])

@@ -35,6 +35,7 @@ KERNEL_KINDS = 12
 VARIANT_PERSISTENT = 0
 VARIANT_Q4K_FOLD = 1
 VARIANT_GRAPHS = 2
+VARIANT_RECOVER = 3
 FORMAT_Q4_0 = 0
 FORMAT_Q4_K = 1
 FORMAT_Q6_K = 2
@@ -134,6 +135,7 @@ SIGNATURES = {
                _vp]),
     "tqf_hip_set_variant": (_i32, [_vp, _i32, _i32]),
     "tqf_hip_get_variant": (_i32, [_vp, _i32, C.POINTER(_i32)]),
+    "tqf_hip_recovery_counts": (_i32, [_vp, C.POINTER(_u64), C.POINTER(_u64)]),
     "tqf_hip_profile_enable": (_i32, [_vp, _i32]),
     "tqf_hip_profile_read": (_i32, [_vp, _i32, C.POINTER(_u64), C.POINTER(C.c_double),
                                     C.POINTER(C.c_double)]),

@@ -585,6 +585,13 @@ class HipBackend:
         finally:
             self.set_variant(variant, old)
 
+    def recovery_counts(self) -> tuple[int, int]:
+        """(stack re-runs, acceptance re-runs) after timed-out persistent launches."""
+        st = C.c_uint64()
+        ac = C.c_uint64()
+        self._check(self.lib.tqf_hip_recovery_counts(self.ctx, C.byref(st), C.byref(ac)))
+        return st.value, ac.value
+
     # ---- profiling ---------------------------------------------------------------------
     def profile_enable(self, enable: bool = True) -> None:
         self._check(self.lib.tqf_hip_profile_enable(self.ctx, 1 if enable else 0))

@@ -308,7 +308,9 @@ struct AccArgs {
     int32_t *tokens;
     uint8_t *scratch;
     uint32_t ept;  // one-launch path: elements per thread
-    uint32_t fail_poll;  // one-launch path: workgroup 0 takes its first exchange as timed out
+    uint32_t fail_poll;  // one-launch path: workgroup 0 takes its first exchange (greedy: its
+                         // arg-max gather) as timed out
+    int32_t *host_flag;  // one-launch path: pinned host word set to 1 by a timed-out wait
 };
 
 struct Acc {
@@ -996,13 +998,18 @@ __global__ __launch_bounds__(kFuseThreads) void acc_fused_kernel(AccArgs a) {
         if (tid == 0) *a.accepted = (int32_t)istar;
     };
     auto fail = [&]() {
-        if (tid == 0) __hip_atomic_store(a.accepted, -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) {
+            __hip_atomic_store(a.accepted, -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (a.host_flag) __hip_atomic_store(a.host_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
         fuse_exit(ctl, tag);
     };
     // ---- greedy: workgroup 0 decides -------------------------------------------
     if (a.greedy) {
         if (c == 0) {
-            if (__syncthreads_or(!argmax_rows(0, k))) {
+            // (a forced timeout, TQF_HIP_ACCEPT_FAIL_POLL, takes this gather as
+            // timed out once its words are in)
+            if (__syncthreads_or(!argmax_rows(0, k) || a.fail_poll)) {
                 fail();
                 return;
             }
@@ -1295,19 +1302,22 @@ void accept_warm() {
 size_t accept_scratch_bytes(uint32_t k, uint32_t vocab) {
     return fuse_fits(k, vocab) ? fuse_layout(k, vocab, fuse_ept(vocab)).total : acc_layout(k, vocab).total;
 }
+size_t accept_multi_scratch_bytes(uint32_t k, uint32_t vocab) { return acc_layout(k, vocab).total; }
+bool accept_one_launch(uint32_t k, uint32_t vocab) { return fuse_fits(k, vocab); }
 
 hipError_t launch_accept(hipStream_t s, const float *target, const float *draft,
                          const int32_t *dtok, uint32_t k, uint32_t vocab, float temperature,
                          int32_t greedy, const float *u, const float *ures, int32_t *accepted,
-                         int32_t *tokens, void *scratch, hipEvent_t ev_start, hipEvent_t ev_stop) {
+                         int32_t *tokens, void *scratch, hipEvent_t ev_start, hipEvent_t ev_stop,
+                         bool multi, int32_t *host_flag) {
     // a poll timeout forced from the host, for the tests of the failure path
     // (TQF_HIP_ACCEPT_FAIL_POLL = 1); read at every launch
     const char *fail_poll = std::getenv("TQF_HIP_ACCEPT_FAIL_POLL");
     AccArgs a{target, draft, dtok, k, vocab, temperature, greedy, u, ures, accepted, tokens,
               reinterpret_cast<uint8_t *>(scratch), fuse_ept(vocab),
-              fail_poll && fail_poll[0] && fail_poll[0] != '0' ? 1u : 0u};
+              fail_poll && fail_poll[0] && fail_poll[0] != '0' ? 1u : 0u, host_flag};
     if (ev_start) (void)hipEventRecord(ev_start, s);
-    if (fuse_fits(k, vocab)) {
+    if (!multi && fuse_fits(k, vocab)) {
         // one plain launch: a cooperative launch measured about 15 us of
         // extra dispatch time, and the grid fits co-resident anyway
         const dim3 grid(fuse_layout(k, vocab, a.ept).nch);

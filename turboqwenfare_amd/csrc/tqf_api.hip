@@ -61,6 +61,9 @@ constexpr size_t kSlabBytes = size_t(256) << 20;
 constexpr size_t kAlign = 256;
 constexpr int kRingSize = 4096;
 constexpr size_t kMaxGraphs = 16;
+// the context's pinned abort flags (tqf_hip_ctx::h_flags)
+constexpr int kFlagStack = 0;
+constexpr int kFlagAccept = 1;
 
 int32_t fail(tqf_hip_ctx *ctx, int32_t code, const std::string &msg) {
     if (ctx) ctx->last_error = msg;
@@ -228,6 +231,7 @@ int32_t ensure_stack_scratch(tqf_hip_ctx *ctx, uint32_t experts, uint32_t bp_dow
     (void)hipFree(sc.hshared);
     (void)hipFree(sc.partial);
     (void)hipFree(sc.ssq);
+    (void)hipFree(sc.h_save);
     sc = StackScratch();
     TQF_HIP(ctx, hipMalloc(&sc.sync, sizeof(StackSync)));
     TQF_HIP(ctx, hipMemset(sc.sync, 0, sizeof(StackSync)));
@@ -242,6 +246,7 @@ int32_t ensure_stack_scratch(tqf_hip_ctx *ctx, uint32_t experts, uint32_t bp_dow
     TQF_HIP(ctx, hipMemset(sc.partial, 0, (size_t)kStackTeams * members * kStackMT * 64 * 8));
     TQF_HIP(ctx, hipMalloc(&sc.ssq, (size_t)kStackTeams * kStackMT * 4));
     TQF_HIP(ctx, hipMemset(sc.ssq, 0, (size_t)kStackTeams * kStackMT * 4));
+    TQF_HIP(ctx, hipMalloc(&sc.h_save, (size_t)kStackMT * kStackHidden * 4));
     sc.experts = experts;
     sc.bp_down = bp_down;
     sc.members = members;
@@ -476,9 +481,13 @@ bool stack_persistent_ok(tqf_hip_ctx *ctx, const tqf_hip_stack *st, uint32_t m) 
     return ctx->stack_grid >= (uint32_t)kStackTeams && ctx->stack_grid >= (uint32_t)kStackMT * 32;
 }
 
+// recover: the launch reports an abort in the context's host flag (set to -1
+// here, 0 or 1 by the launch's last workgroup) instead of TQF_HIP_ERR_DEVICE
+// in d_status, and copies h_in to the stack scratch's h_save, from which
+// rerun_stack restarts.
 int32_t enqueue_stack_persistent(tqf_hip_ctx *ctx, const tqf_hip_stack *st, const float *d_h_in,
                                  float *d_h, uint32_t m, uint16_t *d_ids, float *d_w,
-                                 int32_t *d_status) {
+                                 int32_t *d_status, bool recover) {
     const uint32_t bp_down = padded_blocks(st->width / 32);
     const uint32_t grid = ctx->stack_grid;
     const uint32_t members = grid / kStackTeams;
@@ -503,6 +512,10 @@ int32_t enqueue_stack_persistent(tqf_hip_ctx *ctx, const tqf_hip_stack *st, cons
     a.ssq = sc.ssq;
     a.sync = sc.sync;
     a.members = members;
+    a.dev_status = recover ? nullptr : d_status;
+    a.h_save = sc.h_save;
+    a.host_flag = recover ? ctx->d_flags + kFlagStack : nullptr;
+    if (recover) ctx->h_flags[kFlagStack] = -1;  // no launch on this context is in flight
     // a barrier timeout forced from the host, for the tests of the abort path
     // (TQF_HIP_STACK_FAIL_AT_LAYER = l); read at every launch
     const char *fail_at = std::getenv("TQF_HIP_STACK_FAIL_AT_LAYER");
@@ -514,13 +527,18 @@ int32_t enqueue_stack_persistent(tqf_hip_ctx *ctx, const tqf_hip_stack *st, cons
     return TQF_HIP_OK;
 }
 
+// recover: a timed-out one-launch acceptance reports in the context's host
+// flag (zeroed here) as well as in *acc.  multi: the three-kernel path.
 int32_t enqueue_accept(tqf_hip_ctx *ctx, const float *t, const float *d, const int32_t *dt,
                        uint32_t k, uint32_t vocab, float T, int32_t greedy, const float *u,
-                       const float *ur, int32_t *acc, int32_t *tok) {
+                       const float *ur, int32_t *acc, int32_t *tok, bool recover = false,
+                       bool multi = false) {
     hipEvent_t e0 = nullptr, e1 = nullptr;
     Prof p(ctx);
+    if (recover) ctx->h_flags[kFlagAccept] = 0;
     hipError_t e = launch_accept(ctx->stream, t, d, dt, k, vocab, T, greedy, u, ur, acc, tok,
-                                 ctx->scratch.accept, e0, e1);
+                                 ctx->scratch.accept, e0, e1, multi,
+                                 recover ? ctx->d_flags + kFlagAccept : nullptr);
     if (e != hipSuccess) return hip_fail(ctx, "acceptance kernel launch", e);
     p.end(TQF_HIP_KERNEL_ACCEPT, (double)(greedy ? k + 1 : 2 * k + 1) * vocab * 4, 0, nullptr);
     return TQF_HIP_OK;
@@ -570,6 +588,39 @@ int32_t run_graphed(tqf_hip_ctx *ctx, const std::vector<uint64_t> &key, F enqueu
 
 uint64_t k64(const void *p) { return (uint64_t)(uintptr_t)p; }
 
+// ---- recovery from a timed-out persistent launch -----------------------------
+// The persistent stack kernel and the one-launch acceptance need every
+// workgroup resident at once.  When other work holds compute units, their
+// waits time out after 20 ms and the launch aborts (TQF_HIP_ERR_DEVICE /
+// accepted = -1).  With TQF_HIP_VARIANT_RECOVER (the default) the entry
+// points that run one wait for it, read the flag the launch leaves in pinned
+// host memory, and after an abort re-run the work through kernels that never
+// wait on one another: the per-layer stack kernels from the copy of h_in the
+// persistent prologue made, and the three-kernel acceptance.  The reruns are
+// counted (tqf_hip_recovery_counts).  This is the GPU-side counterpart of the
+// reference's fallback from a failed GPU path to a working one
+// (experts/mod.rs:480-497).
+bool recovering(const tqf_hip_ctx *ctx) {
+    return ctx->variant[TQF_HIP_VARIANT_RECOVER] != 0 && ctx->d_flags != nullptr;
+}
+
+int32_t rerun_stack(tqf_hip_ctx *ctx, const tqf_hip_stack *st, float *d_h, uint32_t m, uint16_t *d_ids,
+                    float *d_w, int32_t *d_status) {
+    ++ctx->reruns[kFlagStack];
+    if (int32_t rc = ensure_layer_scratch(ctx, st->layers[0]->dev, st->format)) return rc;
+    const float *h_in = ctx->stack.h_save;
+    std::vector<uint64_t> key = {3, k64(st), k64(h_in), k64(d_h), m, k64(d_ids), k64(d_w), k64(d_status)};
+    return run_graphed(ctx, key, [&]() { return enqueue_stack(ctx, st, h_in, d_h, m, d_ids, d_w, d_status); });
+}
+
+int32_t rerun_accept(tqf_hip_ctx *ctx, const float *t, const float *d, const int32_t *dt, uint32_t k,
+                     uint32_t vocab, float T, int32_t greedy, const float *u, const float *ur, int32_t *acc,
+                     int32_t *tok) {
+    ++ctx->reruns[kFlagAccept];
+    if (int32_t rc = ensure_accept_scratch(ctx, accept_multi_scratch_bytes(k, vocab))) return rc;
+    return enqueue_accept(ctx, t, d, dt, k, vocab, T, greedy, u, ur, acc, tok, false, true);
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -614,9 +665,21 @@ extern "C" int32_t tqf_hip_create(int32_t device, tqf_hip_ctx **out) {
         delete ctx;
         return TQF_HIP_ERR_DEVICE;
     }
+    // the abort flags the persistent launches write for the host (recovery)
+    if (hipHostMalloc(reinterpret_cast<void **>(&ctx->h_flags), 2 * sizeof(int32_t), hipHostMallocMapped) !=
+            hipSuccess ||
+        hipHostGetDevicePointer(reinterpret_cast<void **>(&ctx->d_flags), ctx->h_flags, 0) != hipSuccess) {
+        (void)hipHostFree(ctx->h_flags);
+        (void)hipFree(p);
+        (void)hipHostFree(ctx->prof_ring);
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return TQF_HIP_ERR_NOMEM;
+    }
+    ctx->h_flags[kFlagStack] = ctx->h_flags[kFlagAccept] = 0;
     tqf::accept_warm();  // device queries of the acceptance launch, outside any capture
     static const char *const kVariantEnv[TQF_HIP_VARIANTS] = {"TQF_HIP_PERSISTENT", "TQF_HIP_Q4K_FOLD",
-                                                              "TQF_HIP_GRAPHS"};
+                                                              "TQF_HIP_GRAPHS", "TQF_HIP_RECOVER"};
     for (int i = 0; i < TQF_HIP_VARIANTS; ++i) {
         const char *v = std::getenv(kVariantEnv[i]);
         ctx->variant[i] = (v && v[0] == '0') ? 0 : 1;
@@ -669,6 +732,7 @@ extern "C" int32_t tqf_hip_destroy(tqf_hip_ctx *ctx) {
     (void)hipFree(ctx->stack.hshared);
     (void)hipFree(ctx->stack.partial);
     (void)hipFree(ctx->stack.ssq);
+    (void)hipFree(ctx->stack.h_save);
     (void)hipFree(ctx->d_stage);
     (void)hipFree(ctx->d_table);
     (void)hipFree(ctx->d_gemv_xprep);
@@ -678,6 +742,7 @@ extern "C" int32_t tqf_hip_destroy(tqf_hip_ctx *ctx) {
     (void)hipFree(const_cast<const uint8_t **>(ctx->d_adhoc_mats));
     for (Slab &s : ctx->slabs) (void)hipFree(s.base);
     (void)hipHostFree(ctx->prof_ring);
+    (void)hipHostFree(ctx->h_flags);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return TQF_HIP_OK;
@@ -1707,8 +1772,15 @@ extern "C" int32_t tqf_hip_stack_forward_device(tqf_hip_ctx *ctx, const tqf_hip_
     TQF_ENTER(ctx);
     if (!stack || !d_h) return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
     if (m == 0 || m > kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "m must be in 1..8");
-    if (stack_persistent_ok(ctx, stack, m))
-        return enqueue_stack_persistent(ctx, stack, d_h_in, d_h, m, d_ids, d_w, d_status);
+    if (stack_persistent_ok(ctx, stack, m)) {
+        const bool rec = recovering(ctx);
+        if (int32_t rc = enqueue_stack_persistent(ctx, stack, d_h_in, d_h, m, d_ids, d_w, d_status, rec))
+            return rc;
+        if (!rec) return TQF_HIP_OK;
+        TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (ctx->h_flags[kFlagStack] != 0) return rerun_stack(ctx, stack, d_h, m, d_ids, d_w, d_status);
+        return TQF_HIP_OK;
+    }
     if (int32_t rc = ensure_layer_scratch(ctx, stack->layers[0]->dev, stack->format)) return rc;
     std::vector<uint64_t> key = {1, k64(stack), k64(d_h_in), k64(d_h), m, k64(d_ids), k64(d_w),
                                  k64(d_status)};
@@ -1747,8 +1819,16 @@ extern "C" int32_t tqf_hip_accept_device(tqf_hip_ctx *ctx, const float *d_target
                                   d_u != nullptr && d_ures != nullptr))
         return rc;
     if (int32_t rc = ensure_accept_scratch(ctx, accept_scratch_bytes(k, vocab))) return rc;
-    return enqueue_accept(ctx, d_target, d_draft, d_draft_tokens, k, vocab, temperature, greedy,
-                          d_u, d_ures, d_accepted, d_tokens);
+    const bool rec = recovering(ctx) && accept_one_launch(k, vocab);
+    if (int32_t rc = enqueue_accept(ctx, d_target, d_draft, d_draft_tokens, k, vocab, temperature, greedy,
+                                    d_u, d_ures, d_accepted, d_tokens, rec))
+        return rc;
+    if (!rec) return TQF_HIP_OK;
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->h_flags[kFlagAccept] != 0)
+        return rerun_accept(ctx, d_target, d_draft, d_draft_tokens, k, vocab, temperature, greedy, d_u, d_ures,
+                            d_accepted, d_tokens);
+    return TQF_HIP_OK;
 }
 
 extern "C" int32_t tqf_hip_embed_rows_device(tqf_hip_ctx *ctx, const tqf_hip_weights *emb,
@@ -1841,12 +1921,20 @@ extern "C" int32_t tqf_hip_accept(tqf_hip_ctx *ctx, const float *target, const f
         TQF_HIP(ctx, hipMemcpyAsync(dur, u_resample, (k + 1) * 4, hipMemcpyHostToDevice, ctx->stream));
     }
     if (k) TQF_HIP(ctx, hipMemcpyAsync(dtok, draft_tokens, k * 4, hipMemcpyHostToDevice, ctx->stream));
+    const bool rec = recovering(ctx) && accept_one_launch(k, vocab);
     if (int32_t rc = enqueue_accept(ctx, dt, dd, k ? dtok : nullptr, k, vocab, temperature, greedy,
-                                    greedy ? nullptr : du, greedy ? nullptr : dur, dout, dout + 1))
+                                    greedy ? nullptr : du, greedy ? nullptr : dur, dout, dout + 1, rec))
         return rc;
     std::vector<int32_t> res(k + 2);
     TQF_HIP(ctx, hipMemcpyAsync(res.data(), dout, (k + 2) * 4, hipMemcpyDeviceToHost, ctx->stream));
     TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (rec && ctx->h_flags[kFlagAccept] != 0) {
+        if (int32_t rc = rerun_accept(ctx, dt, dd, k ? dtok : nullptr, k, vocab, temperature, greedy,
+                                      greedy ? nullptr : du, greedy ? nullptr : dur, dout, dout + 1))
+            return rc;
+        TQF_HIP(ctx, hipMemcpyAsync(res.data(), dout, (k + 2) * 4, hipMemcpyDeviceToHost, ctx->stream));
+        TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    }
     *accepted = res[0];
     std::memcpy(tokens_out, res.data() + 1, (k + 1) * 4);
     return TQF_HIP_OK;
@@ -1993,24 +2081,49 @@ extern "C" int32_t tqf_hip_verify_step_device(tqf_hip_ctx *ctx, const tqf_hip_st
                                   d_u != nullptr && d_ures != nullptr))
         return rc;
     if (int32_t rc = ensure_accept_scratch(ctx, accept_scratch_bytes(k, vocab))) return rc;
+    const bool rec_accept = recovering(ctx) && accept_one_launch(k, vocab);
+    bool rec_stack = false;
     if (stack_persistent_ok(ctx, stack, m)) {
-        if (int32_t rc = enqueue_stack_persistent(ctx, stack, d_h_in, d_h, m, nullptr, nullptr, d_status))
+        rec_stack = recovering(ctx);
+        if (int32_t rc = enqueue_stack_persistent(ctx, stack, d_h_in, d_h, m, nullptr, nullptr, d_status,
+                                                  rec_stack))
             return rc;
-        return enqueue_accept(ctx, d_target, d_draft, d_dtok, k, vocab, temperature, greedy, d_u,
-                              d_ures, d_accepted, d_tokens);
+        if (int32_t rc = enqueue_accept(ctx, d_target, d_draft, d_dtok, k, vocab, temperature, greedy, d_u,
+                                        d_ures, d_accepted, d_tokens, rec_accept))
+            return rc;
+    } else {
+        if (int32_t rc = ensure_layer_scratch(ctx, stack->layers[0]->dev, stack->format)) return rc;
+        uint32_t tbits;
+        std::memcpy(&tbits, &temperature, 4);
+        std::vector<uint64_t> key = {2,          k64(stack), k64(d_h_in), k64(d_h), m, k64(d_target),
+                                     k64(d_draft), k64(d_dtok), vocab,     tbits,       (uint64_t)greedy,
+                                     k64(d_u),   k64(d_ures), k64(d_accepted), k64(d_tokens),
+                                     k64(d_status), (uint64_t)rec_accept};
+        // the captured acceptance reports to the same host flag at every replay
+        if (rec_accept) ctx->h_flags[kFlagAccept] = 0;
+        if (int32_t rc = run_graphed(ctx, key, [&]() {
+                if (int32_t rc = enqueue_stack(ctx, stack, d_h_in, d_h, m, nullptr, nullptr, d_status)) return rc;
+                return enqueue_accept(ctx, d_target, d_draft, d_dtok, k, vocab, temperature, greedy, d_u,
+                                      d_ures, d_accepted, d_tokens, rec_accept);
+            }))
+            return rc;
     }
-    if (int32_t rc = ensure_layer_scratch(ctx, stack->layers[0]->dev, stack->format)) return rc;
-    uint32_t tbits;
-    std::memcpy(&tbits, &temperature, 4);
-    std::vector<uint64_t> key = {2,          k64(stack), k64(d_h_in), k64(d_h), m, k64(d_target),
-                                 k64(d_draft), k64(d_dtok), vocab,     tbits,       (uint64_t)greedy,
-                                 k64(d_u),   k64(d_ures), k64(d_accepted), k64(d_tokens),
-                                 k64(d_status)};
-    return run_graphed(ctx, key, [&]() {
-        if (int32_t rc = enqueue_stack(ctx, stack, d_h_in, d_h, m, nullptr, nullptr, d_status)) return rc;
-        return enqueue_accept(ctx, d_target, d_draft, d_dtok, k, vocab, temperature, greedy, d_u,
-                              d_ures, d_accepted, d_tokens);
-    });
+    if (!rec_stack && !rec_accept) return TQF_HIP_OK;
+    TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    // the acceptance reads only the logits, so each part re-runs on its own
+    if (rec_stack && ctx->h_flags[kFlagStack] != 0)
+        if (int32_t rc = rerun_stack(ctx, stack, d_h, m, nullptr, nullptr, d_status)) return rc;
+    if (rec_accept && ctx->h_flags[kFlagAccept] != 0)
+        return rerun_accept(ctx, d_target, d_draft, d_dtok, k, vocab, temperature, greedy, d_u, d_ures, d_accepted,
+                            d_tokens);
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_recovery_counts(tqf_hip_ctx *ctx, uint64_t *stack_reruns, uint64_t *accept_reruns) {
+    TQF_ENTER(ctx);
+    if (stack_reruns) *stack_reruns = ctx->reruns[kFlagStack];
+    if (accept_reruns) *accept_reruns = ctx->reruns[kFlagAccept];
+    return TQF_HIP_OK;
 }
 
 // ===========================================================================

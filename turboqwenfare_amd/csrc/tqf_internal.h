@@ -296,7 +296,7 @@ struct StackSync {
     uint32_t release;  // epoch released by the last arrival, and the abort flag:
     uint32_t abort;    // one 64-bit poll load, on its own cache line
     uint32_t pad1[30];
-    uint32_t seq;  // launches completed (every launch advances it once, at its exit)
+    uint32_t step_base;  // layer steps of the launches completed (mod 2^31; the tags' base, tqf_tags.h)
     uint32_t pad2[31];
     // first-level arrivals: workgroup b counts on line b % kStackBarrierGroups
     // (one line per group; the last arrival of a group counts on `barrier`)
@@ -319,6 +319,10 @@ struct StackArgs {
     StackSync *sync;
     uint32_t members;   // workgroups per 64-row team in phase C
     uint32_t fail_at;   // layer whose barrier-B wait workgroup 0 takes as timed out (~0u: none)
+    int32_t *dev_status;  // receives TQF_HIP_ERR_DEVICE after a timed-out wait (may be null)
+    float *h_save;        // [kStackMT x kStackHidden]: a copy of h_in, written by the prologue
+    int32_t *host_flag;   // pinned host word: the last workgroup out writes 1 after an
+                          // abort, 0 otherwise (may be null)
 };
 // Words of one parity of the logit accumulator: kStackMT rows of the 256
 // routed experts and the shared-expert gate, then a non-finite flag.
@@ -331,6 +335,7 @@ struct StackScratch {
     float *hshared = nullptr;
     uint64_t *partial = nullptr;
     float *ssq = nullptr;
+    float *h_save = nullptr;  // [kStackMT x kStackHidden]
     uint32_t experts = 0, bp_down = 0, members = 0;
 };
 // Workgroups of a persistent launch (0 if the device cannot co-schedule it)
@@ -398,7 +403,13 @@ struct tqf_hip_ctx {
     void *noalloc_scratch = nullptr;
     // kernel variant selectors (TQF_HIP_VARIANT_*), from the environment at
     // creation, changed by tqf_hip_set_variant
-    int32_t variant[TQF_HIP_VARIANTS] = {1, 1, 1};
+    int32_t variant[TQF_HIP_VARIANTS] = {1, 1, 1, 1};
+    // recovery from a timed-out cross-workgroup wait: pinned host words the
+    // kernels report an abort in ([0] the persistent stack, [1] the one-launch
+    // acceptance), their device addresses, and the reruns so far
+    int32_t *h_flags = nullptr;
+    int32_t *d_flags = nullptr;
+    uint64_t reruns[2] = {0, 0};
 };
 
 namespace tqf {
@@ -450,10 +461,19 @@ hipError_t launch_embed_rows(hipStream_t s, const uint8_t *tiles, const MatrixDi
                              uint32_t n, const float *add, float *out, int32_t *status);
 hipError_t launch_rmsnorm_rows(hipStream_t s, const float *x, uint32_t n, uint32_t cols, const float *w,
                                float *out);
+// multi = true takes the three-kernel path (no wait between workgroups) even
+// where the one-launch kernel applies; scratch must then hold
+// accept_multi_scratch_bytes.  host_flag (pinned host word, may be null): the
+// one-launch kernel writes 1 there when a wait times out.
 hipError_t launch_accept(hipStream_t s, const float *target, const float *draft,
                          const int32_t *dtok, uint32_t k, uint32_t vocab, float temperature,
                          int32_t greedy, const float *u, const float *ures, int32_t *accepted,
-                         int32_t *tokens, void *scratch, hipEvent_t ev_start, hipEvent_t ev_stop);
+                         int32_t *tokens, void *scratch, hipEvent_t ev_start, hipEvent_t ev_stop,
+                         bool multi = false, int32_t *host_flag = nullptr);
+size_t accept_multi_scratch_bytes(uint32_t k, uint32_t vocab);
+// Whether launch_accept takes the one-launch kernel (whose workgroups wait on
+// one another) for k and vocab.
+bool accept_one_launch(uint32_t k, uint32_t vocab);
 hipError_t launch_top4(hipStream_t s, const float *logits, uint32_t rows, uint32_t vocab,
                        uint32_t *tokens4, float *logits4);
 

@@ -21,11 +21,12 @@ namespace tqf {
 
 // One wavefront per row, one lane per 32-element block (looping for rows of
 // more than 64 blocks).  Element j < 16 of a block is the low nibble of byte
-// j, element j + 16 its high nibble, each (q - 8) * d.
+// j, element j + 16 its high nibble, each (q - 8) * d.  `add` may be `out`
+// (the draft head adds its embedding in place): element c is read and then
+// written by the same thread, so neither pointer is declared __restrict__.
 __global__ __launch_bounds__(64) void embed_rows_kernel(const uint8_t *__restrict__ tiles, MatrixDims d,
                                                         const int32_t *__restrict__ tokens,
-                                                        const float *__restrict__ add,
-                                                        float *__restrict__ out,
+                                                        const float *add, float *out,
                                                         int32_t *__restrict__ status) {
     const uint32_t t = blockIdx.x;
     const int32_t tok = tokens[t];

@@ -44,12 +44,15 @@
 // not suffice even between the members of a team: their partial words were
 // not seen within the spin limit.)  Barrier waits are bounded in time: a
 // wait that exceeds kSpinLimit sets `abort`, after which every workgroup
-// leaves at its next barrier and the launch reports TQF_HIP_ERR_DEVICE; the
-// last workgroup to exit resets the barrier state for the next launch.
+// leaves at its next barrier and the launch reports TQF_HIP_ERR_DEVICE (in
+// dev_status, and as 1 in the host flag); the last workgroup to exit resets
+// the barrier state for the next launch.  The library then re-runs the stack
+// through the per-layer kernels from the prologue's copy of h_in.
 #include <hip/hip_runtime.h>
 
 #include "tqf_device.h"
 #include "tqf_internal.h"
+#include "tqf_tags.h"
 
 namespace tqf {
 
@@ -304,21 +307,28 @@ __device__ bool grid_sync(StackSync *sync, uint32_t &epoch, int32_t *status) {
 }
 
 // Last workgroup out resets the barrier state (every workgroup reaches this,
-// including after an abort); after an abort it also zeroes the logit
+// including after an abort), advances the layer-step base of the partial
+// words' tags by this launch's depth (stack_next_base) and reports the
+// outcome in the host flag; after an abort it also zeroes the logit
 // accumulators, which a completed launch leaves at zero.
-__device__ void stack_exit(StackSync *sync, uint64_t *lacc, uint32_t seq) {
+__device__ void stack_exit(StackSync *sync, uint64_t *lacc, uint32_t base, uint32_t n_layers,
+                           int32_t *host_flag) {
     wait_own_stores();
     __syncthreads();
     if (tid() == 0) {
         P.last = 0;
         if (counter_arrive(&sync->exit) == gridDim.x - 1) {
             P.last = __hip_atomic_load(&sync->abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ? 2 : 1;
+            // the launch's outcome for the host (read once the launch has ended)
+            if (host_flag)
+                __hip_atomic_store(host_flag, P.last == 2 ? 1 : 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             counter_reset(&sync->barrier);
             for (int g = 0; g < kStackBarrierGroups; ++g) counter_reset(&sync->group[g][0]);
             counter_reset(&sync->release);
             counter_reset(&sync->abort);
             counter_reset(&sync->exit);
-            __hip_atomic_store(&sync->seq, seq + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&sync->step_base, stack_next_base(base, n_layers), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     __syncthreads();
@@ -922,7 +932,12 @@ __device__ void member_tail(const StackArgs &a, uint32_t tau, uint32_t k, const 
 }
 
 // Layer 0's inputs: every member takes its team's rows of h_in (kept as the
-// first layer's residual in hres) and does its share of the tail.
+// first layer's residual in hres) and does its share of the tail.  Member 0
+// also copies the rows to h_save, from which the library re-runs the stack
+// after an aborted launch: every workgroup runs this prologue before any
+// grid barrier, and h (which may be h_in) is written only after the last
+// layer, which no workgroup reaches before all have passed the first barrier,
+// so the copy is of the input even when the launch updates h in place.
 __device__ void team_prologue(const StackArgs &a, float &hres) {
     const uint32_t tau = blockIdx.x % kStackTeams, k = blockIdx.x / kStackTeams;
     if (k >= a.members) return;
@@ -930,16 +945,16 @@ __device__ void team_prologue(const StackArgs &a, float &hres) {
     share_loads(a, 0, S);
     const uint32_t tt = tid() / 64, row = tid() % 64;
     hres = tid() < MT * 64 && tt < a.m ? load_coherent(&a.h_in[(size_t)tt * H + tau * 64 + row]) : 0.0f;
+    if (k == 0 && a.h_save && tid() < MT * 64 && tt < a.m) a.h_save[(size_t)tt * H + tau * 64 + row] = hres;
     member_tail(a, tau, k, S, hres, reinterpret_cast<float *>(s_dyn), a.lacc, 0);
 }
 
 // Phase C's partials travel as tagged 64-bit words: tag << 32 | f32 bits, the
-// tag counting (launch, layer) steps with the high bit set, so a word left by
-// an earlier layer or launch (or the zeroed allocation) never carries the
-// current tag.  Readers poll the words themselves, bounded like grid_wait.
-__device__ __forceinline__ uint32_t part_tag(uint32_t seq, uint32_t n_layers, uint32_t l) {
-    return 0x80000000u | ((seq * n_layers + l) & 0x7FFFFFFFu);
-}
+// tag counting layer steps over every launch on this scratch with the high
+// bit set (stack_part_tag: strictly increasing whatever the depth of each
+// launch), so a word left by an earlier layer or launch (or the zeroed
+// allocation) never carries the current tag.  Readers poll the words
+// themselves, bounded like grid_wait.
 
 // This thread's K partials (member order) of word `w0` (stride MT * 64 words
 // per member); false after a timeout (which sets abort) or another
@@ -967,8 +982,8 @@ __device__ bool poll_partials(const StackArgs &a, const uint64_t *w0, uint32_t K
                 t0 = now;
             } else if (now - t0 > kSpinLimit) {
                 __hip_atomic_store(&a.sync->abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (a.status)
-                    __hip_atomic_store(a.status, (int32_t)TQF_HIP_ERR_DEVICE, __ATOMIC_RELAXED,
+                if (a.dev_status)
+                    __hip_atomic_store(a.dev_status, (int32_t)TQF_HIP_ERR_DEVICE, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
                 return false;
             }
@@ -979,7 +994,7 @@ __device__ bool poll_partials(const StackArgs &a, const uint64_t *w0, uint32_t K
 
 // ---- phase C -------------------------------------------------------------------
 template <int LPRD, int MAXP>
-__device__ void phase_c(const StackArgs &a, uint32_t l, uint32_t seq, float &hres, const ShareLoads &SL) {
+__device__ void phase_c(const StackArgs &a, uint32_t l, uint32_t base, float &hres, const ShareLoads &SL) {
     uint4 *s_x = reinterpret_cast<uint4 *>(reinterpret_cast<uint8_t *>(s_dyn) + LdsLayout<LPRD, MAXP>::kXr);
     const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
     const int lane = tid() % kWave;
@@ -1086,7 +1101,7 @@ __device__ void phase_c(const StackArgs &a, uint32_t l, uint32_t seq, float &hre
     const int t = idx / RG, rr = idx % RG;
     // every token slot, so each word this launch reads was last written by it
     // or by the previous launch
-    const uint32_t tag = part_tag(seq, a.n_layers, l);
+    const uint32_t tag = stack_part_tag(base, l);
     if (reduced_first_copy<LPRD, NL>(lane))
         __hip_atomic_store(&a.partial[(((size_t)tau * K + k) * MT + t) * 64 + 8 * wave + j * RG + rr],
                            ((uint64_t)tag << 32) | __float_as_uint(s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1137,10 +1152,11 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
             if (k < (a.E + 1) * 3) s_mats[k] = load_global_ptr(L0.mats + k);
         }
     }
-    const uint32_t seq = __hip_atomic_load(&a.sync->seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // layer steps of every earlier launch on this scratch (the tags' base)
+    const uint32_t base = __hip_atomic_load(&a.sync->step_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     float hres = 0.0f;  // the residual: this thread's team row of h (phase C members)
     team_prologue(a, hres);
-    bool ok = grid_sync(a.sync, epoch, a.status);
+    bool ok = grid_sync(a.sync, epoch, a.dev_status);
     for (uint32_t l = 0; ok && l < a.n_layers; ++l) {
         UnitLoads U;
         SharedLoads S;
@@ -1181,7 +1197,7 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
         // this member's share of the next layer's router rows, gate and norm
         ShareLoads SL;
         if (l + 1 < a.n_layers) share_loads(a, l + 1, SL);
-        if (!(ok = grid_wait(a.sync, epoch, a.status, l == a.fail_at && blockIdx.x == 0))) break;
+        if (!(ok = grid_wait(a.sync, epoch, a.dev_status, l == a.fail_at && blockIdx.x == 0))) break;
         // the next layer's expert-matrix table: loads now, LDS after phase C
         // (whose down weights still come from this layer's table)
         const bool more = l + 1 < a.n_layers;
@@ -1194,7 +1210,7 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
                 mp[i] = load_global_ptr(Ln.mats + (k < (a.E + 1) * 3 ? k : 0));
             }
         }
-        phase_c<LPRD, MAXP>(a, l, seq, hres, SL);
+        phase_c<LPRD, MAXP>(a, l, base, hres, SL);
         if (more) {
             __syncthreads();  // every wavefront is past phase C's table reads
 #pragma unroll
@@ -1203,9 +1219,9 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
                 if (k < (a.E + 1) * 3) s_mats[k] = mp[i];
             }
         }
-        if (more && !(ok = grid_sync(a.sync, epoch, a.status))) break;
+        if (more && !(ok = grid_sync(a.sync, epoch, a.dev_status))) break;
     }
-    stack_exit(a.sync, a.lacc, seq);
+    stack_exit(a.sync, a.lacc, base, a.n_layers, a.host_flag);
 }
 
 namespace {
