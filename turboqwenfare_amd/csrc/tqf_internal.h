@@ -297,7 +297,8 @@ struct StackSync {
     uint32_t abort;    // one 64-bit poll load, on its own cache line
     uint32_t pad1[30];
     uint32_t step_base;  // layer steps of the launches completed (mod 2^31; the tags' base, tqf_tags.h)
-    uint32_t pad2[31];
+    uint32_t xcd_bad;    // set by a workgroup that is not on XCD blockIdx % 8 (this launch)
+    uint32_t pad2[30];
     // first-level arrivals: workgroup b counts on line b % kStackBarrierGroups
     // (one line per group; the last arrival of a group counts on `barrier`)
     uint32_t group[kStackBarrierGroups][32];

@@ -105,6 +105,7 @@ struct RoutePlan {
     int32_t last;
     int32_t ok;
     int32_t arrived_last;  // this workgroup released the current grid barrier
+    int32_t xcd_local;     // the team exchange goes through the XCD's L2 (xcd_local_ok)
 };
 
 // Workgroup-shared state (file scope, so that every access is a ds_* access).
@@ -326,6 +327,7 @@ __device__ void stack_exit(StackSync *sync, uint64_t *lacc, uint32_t base, uint3
             for (int g = 0; g < kStackBarrierGroups; ++g) counter_reset(&sync->group[g][0]);
             counter_reset(&sync->release);
             counter_reset(&sync->abort);
+            counter_reset(&sync->xcd_bad);
             counter_reset(&sync->exit);
             __hip_atomic_store(&sync->step_base, stack_next_base(base, n_layers), __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
@@ -956,21 +958,72 @@ __device__ void team_prologue(const StackArgs &a, float &hres) {
 // allocation) never carries the current tag.  Readers poll the words
 // themselves, bounded like grid_wait.
 
+// ---- the team exchange within one XCD ------------------------------------------------
+// Workgroup b runs on XCD b mod 8 under the dispatcher's round-robin placement
+// (checked at every launch: a workgroup that reads another id from its
+// XCC_ID register sets sync->xcd_bad before the first barrier), so the 8
+// members of team tau (workgroups tau + 32 k) share one L2.  Their partial
+// words then need not travel to the memory side: a plain store lands in the
+// L2 (the vector L1 is write-through), and a non-temporal load misses the
+// L1 and reads the L2 -- a round trip of about 0.8 us between two idle
+// compute units against 1.0-1.2 us at agent scope (measured).  Without the
+// placement, or with another team size, the exchange stays at agent scope.
+__device__ __forceinline__ uint32_t xcc_id() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    return v;
+}
+constexpr uint32_t kLocalMembers = 8;
+__device__ __forceinline__ void store_l2(uint64_t *p, uint64_t v) {
+    asm volatile("global_store_dwordx2 %0, %1, off" ::"v"(p), "v"(v) : "memory");
+}
+// The eight members' words of one row (stride MT * 64 words), all loads in
+// flight at once, then one wait.
+__device__ __forceinline__ void load8_l2(const uint64_t *w0, uint64_t (&w)[8]) {
+    constexpr size_t S = (size_t)MT * 64;
+    asm volatile(
+        "global_load_dwordx2 %0, %8, off nt\n\t"
+        "global_load_dwordx2 %1, %9, off nt\n\t"
+        "global_load_dwordx2 %2, %10, off nt\n\t"
+        "global_load_dwordx2 %3, %11, off nt\n\t"
+        "global_load_dwordx2 %4, %12, off nt\n\t"
+        "global_load_dwordx2 %5, %13, off nt\n\t"
+        "global_load_dwordx2 %6, %14, off nt\n\t"
+        "global_load_dwordx2 %7, %15, off nt\n\t"
+        "s_waitcnt vmcnt(0)"
+        : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]), "=&v"(w[6]), "=&v"(w[7])
+        : "v"(w0), "v"(w0 + S), "v"(w0 + 2 * S), "v"(w0 + 3 * S), "v"(w0 + 4 * S), "v"(w0 + 5 * S),
+          "v"(w0 + 6 * S), "v"(w0 + 7 * S)
+        : "memory");
+}
+
 // This thread's K partials (member order) of word `w0` (stride MT * 64 words
 // per member); false after a timeout (which sets abort) or another
 // workgroup's abort.
 __device__ bool poll_partials(const StackArgs &a, const uint64_t *w0, uint32_t K, uint32_t tag,
-                              float (&pv)[kMaxMembers]) {
+                              float (&pv)[kMaxMembers], bool local) {
     uint32_t need = (1u << K) - 1u;
     int64_t t0 = 0;
     for (uint32_t spin = 1;; ++spin) {
+        if (local) {  // K == kLocalMembers, through the L2
+            uint64_t w[8];
+            load8_l2(w0, w);
 #pragma unroll
-        for (int kk = 0; kk < kMaxMembers; ++kk) {
-            if ((need >> kk) & 1u) {
-                const uint64_t w = poll_load(w0 + (size_t)kk * MT * 64);
-                if ((uint32_t)(w >> 32) == tag) {
-                    pv[kk] = __uint_as_float((uint32_t)w);
+            for (int kk = 0; kk < 8; ++kk) {
+                if (((need >> kk) & 1u) && (uint32_t)(w[kk] >> 32) == tag) {
+                    pv[kk] = __uint_as_float((uint32_t)w[kk]);
                     need &= ~(1u << kk);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < kMaxMembers; ++kk) {
+                if ((need >> kk) & 1u) {
+                    const uint64_t w = poll_load(w0 + (size_t)kk * MT * 64);
+                    if ((uint32_t)(w >> 32) == tag) {
+                        pv[kk] = __uint_as_float((uint32_t)w);
+                        need &= ~(1u << kk);
+                    }
                 }
             }
         }
@@ -1102,9 +1155,12 @@ __device__ void phase_c(const StackArgs &a, uint32_t l, uint32_t base, float &hr
     // every token slot, so each word this launch reads was last written by it
     // or by the previous launch
     const uint32_t tag = stack_part_tag(base, l);
-    if (reduced_first_copy<LPRD, NL>(lane))
-        __hip_atomic_store(&a.partial[(((size_t)tau * K + k) * MT + t) * 64 + 8 * wave + j * RG + rr],
-                           ((uint64_t)tag << 32) | __float_as_uint(s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (reduced_first_copy<LPRD, NL>(lane)) {
+        uint64_t *word = &a.partial[(((size_t)tau * K + k) * MT + t) * 64 + 8 * wave + j * RG + rr];
+        const uint64_t v = ((uint64_t)tag << 32) | __float_as_uint(s);
+        if (P.xcd_local) store_l2(word, v);
+        else __hip_atomic_store(word, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     // team combine: every member polls all K members' words, then sums them
     // in member order (the same bits in every member) and takes its share of
     // the next layer's inputs
@@ -1114,7 +1170,7 @@ __device__ void phase_c(const StackArgs &a, uint32_t l, uint32_t base, float &hr
     const bool next = l + 1 < a.n_layers;
     if (tid() < MT * 64 && tt < m) {
         float pv[kMaxMembers];
-        if (poll_partials(a, a.partial + ((size_t)tau * K * MT + tt) * 64 + row, K, tag, pv)) {
+        if (poll_partials(a, a.partial + ((size_t)tau * K * MT + tt) * 64 + row, K, tag, pv, P.xcd_local != 0)) {
             float sum = 0.0f;
 #pragma unroll
             for (int kk = 0; kk < kMaxMembers; ++kk)
@@ -1154,9 +1210,17 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
     }
     // layer steps of every earlier launch on this scratch (the tags' base)
     const uint32_t base = __hip_atomic_load(&a.sync->step_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the team exchange's placement check (before the first barrier's drain)
+    if (tid() == 0 && xcc_id() != blockIdx.x % kStackBarrierGroups)
+        __hip_atomic_fetch_or(&a.sync->xcd_bad, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     float hres = 0.0f;  // the residual: this thread's team row of h (phase C members)
     team_prologue(a, hres);
     bool ok = grid_sync(a.sync, epoch, a.dev_status);
+    if (tid() == 0)
+        P.xcd_local = a.members == kLocalMembers && gridDim.x == kLocalMembers * kStackTeams &&
+                      kStackTeams % kStackBarrierGroups == 0 &&
+                      __hip_atomic_load(&a.sync->xcd_bad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0;
+    __syncthreads();
     for (uint32_t l = 0; ok && l < a.n_layers; ++l) {
         UnitLoads U;
         SharedLoads S;
