@@ -349,6 +349,47 @@ def lm_head_bench(be, seed: int, iters: int = 20):
     return out
 
 
+def sampler_bench(be, seed: int, iters: int = 20):
+    """One token from one row of V = 151,936 logits: the acceptance's draw at
+    k = 0 (exact fixed-point sums, the loop's default pick) beside the
+    reference-exact Sampler::select (sequential f32 sums, a sort), on the
+    bench's N(0, 9) logits at T = 0.7 (about 38k and 28k terms in the two
+    sums) and on flat N(0, 0.01) logits at T = 1 (every term in both).
+    Host wall time per synchronised call, and the select's kernels by HIP
+    events."""
+    from turboqwenfare_amd import _lib
+
+    out = {}
+    d_acc, d_tok, d_u = be.alloc(4), be.alloc(4), be.to_device(np.array([0.37], np.float32))
+    for name, scale, T in (("peaked", 3.0, TEMPERATURE), ("flat", 0.1, 1.0)):
+        lg = (np.random.default_rng(seed).standard_normal(V) * scale).astype(np.float32)
+        d = be.to_device(lg)
+        r = {}
+        for path in ("accept_draw", "sampler_select"):
+            def call():
+                if path == "accept_draw":
+                    be.accept_device(d, d, d_tok, 0, V, T, False, d_u, d_u, d_acc, d_tok)
+                else:
+                    be.sampler_select_device(d, 1, V, T, d_u, d_tok)
+            call()
+            be.synchronize()
+            be.profile_enable(True)
+            t0 = time.perf_counter()
+            for _ in range(iters):
+                call()
+                be.synchronize()
+            r[f"{path}_call_us"] = (time.perf_counter() - t0) / iters * 1e6
+            kind = _lib.KERNEL_ACCEPT if path == "accept_draw" else _lib.KERNEL_SAMPLE
+            n, ms, _ = be.profile_read(kind)
+            be.profile_enable(False)
+            r[f"{path}_gpu_us"] = ms / n * 1e3 if n else None
+        out[name] = r
+        be.free(d)
+    for b in (d_acc, d_tok, d_u):
+        be.free(b)
+    return out
+
+
 def verify_bench(be, model, inputs, steps: int, warmup: int, greedy: bool, distribution=True):
     """Config 4 on a resident model: verify steps/s (stream-ordered), the
     per-step distribution, HIP-event kernel times of eager launches, and the
@@ -612,6 +653,9 @@ def main():
     ap.add_argument("--gemv-only", action="store_true",
                     help="only run the Q4_0 config-1 GEMV pool (the command its rocprofv3 profile "
                          "is taken with) and exit")
+    ap.add_argument("--sampler-only", action="store_true",
+                    help="only the one-row draw: acceptance k = 0 against the reference-exact "
+                         "Sampler::select, and exit")
     ap.add_argument("--q4k-only", action="store_true",
                     help="only run the Q4_K config-1 GEMV pools (the command their rocprofv3 "
                          "profiles are taken with) and exit")
@@ -651,6 +695,10 @@ def main():
         return
     if args.lm_head_only:
         log("bench: LM head " + json.dumps(lm_head_bench(be, args.seed)))
+        be.close()
+        return
+    if args.sampler_only:
+        log("bench: one-row draw " + json.dumps(sampler_bench(be, args.seed)))
         be.close()
         return
     if args.gemv_only:
@@ -712,6 +760,8 @@ def main():
         log("bench: Q4_K config-1 pools " + json.dumps(extras["q4k_config1"]))
         extras["lm_head_q6k"] = lm_head_bench(be, args.seed)
         log("bench: LM head " + json.dumps(extras["lm_head_q6k"]))
+        extras["sampler_select"] = sampler_bench(be, args.seed)
+        log("bench: one-row draw " + json.dumps(extras["sampler_select"]))
         extras["grouped_gemm_config5"] = grouped_gemm_bench(be, model.layers[0], args.seed)
         log("bench: config-5 grouped GEMM " + json.dumps(extras["grouped_gemm_config5"]))
         extras["q4k_verify"] = q4k_verify_bench(be, args.layers, args.seed, inputs,

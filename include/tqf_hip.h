@@ -242,6 +242,20 @@ int32_t tqf_hip_accept_device_noalloc(tqf_hip_ctx *ctx, const float *d_target,
                                       int32_t greedy, const float *d_u,
                                       const float *d_u_resample, int32_t *d_accepted,
                                       int32_t *d_tokens_out);
+/* Sampler::select (sampling/mod.rs:68-74) for each of `rows` (<= 8) rows of
+ * vocab logits (device pointers), bit-identical to the reference: with
+ * temperature 0, Sampler::Greedy's argmax (top_logit_candidates'); otherwise
+ * the stochastic path with the default filters (no penalties, top_k, top_p or
+ * min_p): softmax(logits / temperature) with f32::exp and the token-order f32
+ * total (softmax, :166-190), the stable descending sort with ties to the
+ * lower token (compare_desc, :258-266), then draw's inverse CDF (:227-248)
+ * with d_u[row] in the place of rng.next_f32().  d_tokens [rows] receives
+ * the tokens.  The sums are sequential f32 folds, as in the reference, so a
+ * call takes about a millisecond at vocab 151,936 (the acceptance's draw,
+ * which sums in exact fixed point, takes microseconds); it is for callers
+ * that need the reference's token for the same uniform. */
+int32_t tqf_hip_sampler_select_device(tqf_hip_ctx *ctx, const float *d_logits, uint32_t rows, uint32_t vocab,
+                                      float temperature, const float *d_u, int32_t *d_tokens);
 /* top_logit_candidates (runtime/decode.rs:48-64) over `rows` rows of vocab
  * logits: tokens4/logits4 are [rows x 4]. */
 int32_t tqf_hip_top_logit_candidates(tqf_hip_ctx *ctx, const float *logits, uint32_t rows,
@@ -441,7 +455,8 @@ int32_t tqf_hip_recovery_counts(tqf_hip_ctx *ctx, uint64_t *stack_reruns, uint64
 #define TQF_HIP_KERNEL_Q4K_GEMV 9        /* Q4_K GEMV, fp32 semantics         */
 #define TQF_HIP_KERNEL_Q4K_MATVEC 10     /* Q4_K matvec, Q8_K semantics       */
 #define TQF_HIP_KERNEL_Q6K_MATVEC 11     /* Q6_K matvec / LM head (+ top-4)   */
-#define TQF_HIP_KERNEL_KINDS 12
+#define TQF_HIP_KERNEL_SAMPLE 12         /* Sampler::select, reference-exact  */
+#define TQF_HIP_KERNEL_KINDS 13
 /* While enabled, eager (non-graph) launches of each kind are bracketed by HIP
  * events on the context stream.  Enabling clears the totals. */
 int32_t tqf_hip_profile_enable(tqf_hip_ctx *ctx, int32_t enable);

@@ -49,9 +49,11 @@ def lm_head(model, x):
     return orc.q6_k_matvec(model.lm_head_host, VOCAB, H, x)
 
 
-def select(row, greedy, u):
+def select(row, greedy, u, sampler="fast"):
     if greedy:
         return int(orc.top_logit_candidates(row)[0][0])
+    if sampler == "reference":
+        return orc.softmax_draw(row, T, float(np.float32(u)))
     _, toks = orc.accept(row[None, :], np.zeros((0, VOCAB), np.float32), [], T, False,
                          np.zeros(0, np.float32), np.array([u], np.float32))
     return toks[0]
@@ -68,16 +70,21 @@ def check_target_pass(model, tr):
         assert np.array_equal(tr["target"][i], lm_head(model, tr["hn"][i])), f"target logits row {i}"
 
 
-@pytest.mark.parametrize("self_draft", [False, True], ids=["mtp_head", "self_draft"])
-@pytest.mark.parametrize("greedy", [False, True], ids=["stochastic", "greedy"])
-def test_mtp_loop_matches_the_oracle_step_by_step(backend, mtp_model, greedy, self_draft):
+@pytest.mark.parametrize("self_draft,greedy,sampler", [
+    (False, False, "fast"), (True, False, "fast"), (False, True, "fast"), (True, True, "fast"),
+    (False, False, "reference"), (True, False, "reference")],
+    ids=["mtp_head-stochastic", "self_draft-stochastic", "mtp_head-greedy", "self_draft-greedy",
+         "mtp_head-reference_sampler", "self_draft-reference_sampler"])
+def test_mtp_loop_matches_the_oracle_step_by_step(backend, mtp_model, greedy, self_draft, sampler):
     """The draft head's drafts are almost always rejected (its weights are
     unrelated to the target's); self-drafting makes q = p, so drafts are
     accepted and the bonus draw, h_prev at a > 0 and the controller's
-    enabling are exercised too."""
+    enabling are exercised too.  With the reference sampler every draft and
+    plain pick is Sampler::select's token (orc_softmax_draw), the plain picks'
+    uniforms from the reference generator seeded with the loop's seed."""
     md = mtp_model
     eng = DeviceEngine(backend, md, k=K, temperature=T, greedy=greedy, seed=5, trace=True,
-                       self_draft=self_draft)
+                       self_draft=self_draft, sampler=sampler)
     loop = MtpLoop(eng, k=K, window=3)
     try:
         recs = loop.run(1234, 6)
@@ -85,7 +92,9 @@ def test_mtp_loop_matches_the_oracle_step_by_step(backend, mtp_model, greedy, se
         eng.free()
     r0 = recs[0]
     check_target_pass(md, r0.trace)
-    assert r0.emitted == [select(r0.trace["target"][0], greedy, r0.trace["u_select"])]
+    assert r0.emitted == [select(r0.trace["target"][0], greedy, r0.trace["u_select"], sampler)]
+    if sampler == "reference":
+        assert np.float32(r0.trace["u_select"]) == np.float32(orc.Xoshiro(5).next_f32())
     prev_h, boundary = r0.trace["h"][0], r0.emitted[0]
     stats, ctl = mtp.MtpStatistics(), mtp.MtpController(3)
     for s, r in enumerate(recs[1:]):
@@ -104,7 +113,7 @@ def test_mtp_loop_matches_the_oracle_step_by_step(backend, mtp_model, greedy, se
                 yn = orc.qwen_rmsnorm(tr["draft_y"][i], norm)
                 assert rel_err(tr["draft_yn"][i], yn) < 1e-5
                 assert np.array_equal(tr["draft"][i], lm_head(md, tr["draft_yn"][i])), (s, i)
-                d = select(tr["draft"][i], greedy, float(tr["ud"][i]))
+                d = select(tr["draft"][i], greedy, float(tr["ud"][i]), sampler)
                 assert d == tr["drafts"][i], (s, i)
                 prev = d
             # the verify pass and the acceptance
@@ -118,7 +127,7 @@ def test_mtp_loop_matches_the_oracle_step_by_step(backend, mtp_model, greedy, se
             assert ctl.record_and_decide(r.accepted + 1) == r.enabled
         else:
             check_target_pass(md, tr)
-            assert r.emitted == [select(tr["target"][0], greedy, tr["u_select"])]
+            assert r.emitted == [select(tr["target"][0], greedy, tr["u_select"], sampler)]
             prev_h = tr["h"][0]
         boundary = r.emitted[-1]
     assert stats == loop.stats

@@ -31,7 +31,8 @@ KERNEL_GROUPED_AUX = 8
 KERNEL_Q4K_GEMV = 9
 KERNEL_Q4K_MATVEC = 10
 KERNEL_Q6K_MATVEC = 11
-KERNEL_KINDS = 12
+KERNEL_SAMPLE = 12
+KERNEL_KINDS = 13
 VARIANT_PERSISTENT = 0
 VARIANT_Q4K_FOLD = 1
 VARIANT_GRAPHS = 2
@@ -136,6 +137,7 @@ SIGNATURES = {
     "tqf_hip_set_variant": (_i32, [_vp, _i32, _i32]),
     "tqf_hip_get_variant": (_i32, [_vp, _i32, C.POINTER(_i32)]),
     "tqf_hip_recovery_counts": (_i32, [_vp, C.POINTER(_u64), C.POINTER(_u64)]),
+    "tqf_hip_sampler_select_device": (_i32, [_vp, _vp, _u32, _u32, C.c_float, _vp, _vp]),
     "tqf_hip_profile_enable": (_i32, [_vp, _i32]),
     "tqf_hip_profile_read": (_i32, [_vp, _i32, C.POINTER(_u64), C.POINTER(C.c_double),
                                     C.POINTER(C.c_double)]),

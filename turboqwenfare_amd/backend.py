@@ -554,6 +554,30 @@ class HipBackend:
             d_u.ptr if d_u else None, d_ures.ptr if d_ures else None, d_accepted.ptr,
             d_tokens.ptr))
 
+    def sampler_select_device(self, d_logits: DeviceBuffer, rows: int, vocab: int,
+                              temperature: float, d_u: DeviceBuffer | None,
+                              d_tokens: DeviceBuffer) -> None:
+        """Sampler::select on device rows (the reference's token for uniform d_u[row])."""
+        self._check(self.lib.tqf_hip_sampler_select_device(
+            self.ctx, d_logits.ptr, rows, vocab, float(temperature), d_u.ptr if d_u else None,
+            d_tokens.ptr))
+
+    def sampler_select(self, logits: np.ndarray, temperature: float, u) -> list:
+        """Host form: [V] or [rows, V] logits and one uniform per row -> tokens."""
+        lg = np.ascontiguousarray(logits, dtype=np.float32)
+        lg2 = lg.reshape(1, -1) if lg.ndim == 1 else lg
+        rows, vocab = lg2.shape
+        uu = np.ascontiguousarray(np.atleast_1d(np.asarray(u, dtype=np.float32)))
+        if uu.size != rows:
+            raise ValueError("one uniform per row")
+        d_l, d_u, d_t = self.to_device(lg2), self.to_device(uu), self.alloc(4 * rows)
+        try:
+            self.sampler_select_device(d_l, rows, vocab, temperature, d_u, d_t)
+            return [int(t) for t in self.read(d_t, np.int32, (rows,))]
+        finally:
+            for b in (d_l, d_u, d_t):
+                self.free(b)
+
     def top_logit_candidates(self, logits: np.ndarray):
         """[V] or [rows, V] logits -> (tokens [rows, 4] u32, logits [rows, 4])."""
         lg = np.ascontiguousarray(logits, dtype=np.float32)

@@ -739,6 +739,7 @@ extern "C" int32_t tqf_hip_destroy(tqf_hip_ctx *ctx) {
     (void)hipFree(ctx->d_q4k);
     (void)hipFree(ctx->d_lm);
     (void)hipFree(ctx->d_grouped);
+    (void)hipFree(ctx->d_sample);
     (void)hipFree(const_cast<const uint8_t **>(ctx->d_adhoc_mats));
     for (Slab &s : ctx->slabs) (void)hipFree(s.base);
     (void)hipHostFree(ctx->prof_ring);
@@ -1937,6 +1938,29 @@ extern "C" int32_t tqf_hip_accept(tqf_hip_ctx *ctx, const float *target, const f
     }
     *accepted = res[0];
     std::memcpy(tokens_out, res.data() + 1, (k + 1) * 4);
+    return TQF_HIP_OK;
+}
+
+extern "C" int32_t tqf_hip_sampler_select_device(tqf_hip_ctx *ctx, const float *d_logits, uint32_t rows,
+                                                 uint32_t vocab, float temperature, const float *d_u,
+                                                 int32_t *d_tokens) {
+    TQF_ENTER(ctx);
+    if (!d_logits || !d_tokens || (temperature != 0.0f && !d_u))
+        return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
+    if (rows == 0 || rows > (uint32_t)kMaxTokens) return fail(ctx, TQF_HIP_ERR_INVALID, "rows must be in 1..8");
+    if (vocab == 0 || vocab > (1u << 22)) return fail(ctx, TQF_HIP_ERR_INVALID, "vocab must be in 1..4194304");
+    if (!(temperature >= 0.0f) || !(temperature <= 3.402823466e38f))
+        return fail(ctx, TQF_HIP_ERR_INVALID, "temperature must be finite and >= 0");
+    const size_t need = sample_scratch_bytes(rows, vocab);
+    if (!ctx->d_sample || ctx->sample_bytes < need) {
+        TQF_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        TQF_HIP(ctx, grow(ctx->d_sample, ctx->sample_bytes, need));
+    }
+    Prof p(ctx);
+    hipError_t e = launch_sample_select(ctx->stream, d_logits, rows, vocab, temperature, d_u, d_tokens,
+                                        ctx->d_sample);
+    if (e != hipSuccess) return hip_fail(ctx, "sampler launch", e);
+    p.end(TQF_HIP_KERNEL_SAMPLE, (double)rows * vocab * 4, 0.0, nullptr);
     return TQF_HIP_OK;
 }
 

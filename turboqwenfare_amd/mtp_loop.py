@@ -24,8 +24,16 @@ between stages:
   embedding/hidden projection are out of scope. The sum stands in for that
   projection;
 - selection: greedy takes the LM head's fused top-1
-  (``top_logit_candidates``). Stochastic makes one draw from E_x / S of the
-  row: the acceptance kernel at k = 0 with one uniform;
+  (``top_logit_candidates``). Stochastic, with ``sampler="fast"`` (the
+  default), makes one draw from E_x / S of the row: the acceptance kernel at
+  k = 0 with one uniform (exact fixed-point sums, microseconds). With
+  ``sampler="reference"`` it is ``Sampler::select`` bit for bit
+  (``tqf_hip_sampler_select_device``: f32::exp, the token-order f32 total,
+  the stable sort, the inverse-CDF walk; about a millisecond per pick), and
+  the plain-decode picks take their uniforms from a ``Sampler`` seeded with
+  the loop's seed (Xoshiro256PlusPlus::from_seed, one next_f32 per pick), as
+  the reference's generation loop does: a loop that never speculates then
+  emits the reference's token stream for the same logits;
 - verification: ``tqf_hip_accept_device`` over the k + 1 target rows and the
   k draft rows.
 
@@ -56,6 +64,7 @@ import numpy as np
 
 from . import mtp, synth
 from .backend import DeviceBuffer
+from .sampling import Sampler
 from .workloads import H, SyntheticStack
 
 EMBED_TENSOR = 2_000_000_000
@@ -183,9 +192,15 @@ class DeviceEngine:
 
     def __init__(self, be, model: MtpModel, k: int = 3, temperature: float = 0.7,
                  greedy: bool = False, seed: int = 0, trace: bool = False,
-                 self_draft: bool = False):
+                 self_draft: bool = False, sampler: str = "fast"):
+        if sampler not in ("fast", "reference"):
+            raise ValueError("sampler must be 'fast' or 'reference'")
         self.be, self.model, self.k, self.T, self.greedy = be, model, k, temperature, greedy
         self.seed, self.trace_on, self.self_draft = seed, trace, self_draft
+        self.sampler = sampler
+        # the plain-decode picks' Sampler (reference mode): Sampler::new's
+        # generator, seeded once per generation
+        self.ref_sampler = Sampler(be, temperature, seed) if sampler == "reference" and not greedy else None
         V, m, L = model.vocab, k + 1, max(model.target.n_layers, 1)
         self.d_tok = be.alloc(4 * m)
         self.d_hin, self.d_h, self.d_hn = (be.alloc(4 * m * H) for _ in range(3))
@@ -223,15 +238,26 @@ class DeviceEngine:
     def _pick(self, d_logits: DeviceBuffer, row: int, uniform: float) -> int:
         """One token from logits row `row` of the last LM head call: its
         fused top-1 (greedy), or a draw with one uniform (the acceptance at
-        k = 0, whose draft pointer is unused)."""
+        k = 0, whose draft pointer is unused; or Sampler::select)."""
         be, V = self.be, self.model.vocab
         if self.greedy:
             return int(be.read(self.d_t4, np.uint32, (row + 1, 4))[row, 0])
         d_row = be.view(d_logits, 4 * row * V, 4 * V)
         be.write(self.d_sel_u, np.array([uniform], np.float32))
-        be.accept_device(d_row, d_row, self.d_tok, 0, V, self.T, False, self.d_sel_u,
-                         self.d_sel_u, self.d_sel_acc, self.d_sel_tok)
+        if self.sampler == "reference":
+            be.sampler_select_device(d_row, 1, V, self.T, self.d_sel_u, self.d_sel_tok)
+        else:
+            be.accept_device(d_row, d_row, self.d_tok, 0, V, self.T, False, self.d_sel_u,
+                             self.d_sel_u, self.d_sel_acc, self.d_sel_tok)
         return int(be.read(self.d_sel_tok, np.int32, (1,))[0])
+
+    def _plain_uniform(self, stream: int, step) -> float:
+        """The plain pick's uniform: the reference Sampler's next_f32, or a
+        Philox draw keyed by (seed + step, stream)."""
+        if self.ref_sampler is not None:
+            return float(self.ref_sampler.rng.next_f32())
+        key = self.seed if step is None else self.seed + step
+        return float(synth.philox_uniforms(key, stream, 1)[0])
 
     def _snap(self, buf, shape) -> np.ndarray:
         return self.be.read(buf, np.float32, shape).copy()
@@ -249,13 +275,13 @@ class DeviceEngine:
         """A plain decode of the prompt's last token."""
         if not 0 <= token < self.model.vocab:
             raise ValueError("token out of vocabulary")
-        u = float(synth.philox_uniforms(self.seed, 4, 1)[0])
+        u = self._plain_uniform(4, None)
         return self.plain(None, token, u)
 
     def plain(self, step, boundary: int, u: float | None = None):
         """One token without drafts; its hidden row becomes h_prev."""
         if u is None:
-            u = float(synth.philox_uniforms(self.seed + step, 3, 1)[0])
+            u = self._plain_uniform(3, step)
         self._target_pass([boundary])
         t = self._pick(self.d_target, 0, u)
         self._check_status()
@@ -302,13 +328,14 @@ class DeviceEngine:
             # the draft token, into the verify rows: the fused top-1, or one
             # draw (the acceptance at k = 0 with its uniform ud[i])
             if self.greedy:
-                src = be.view(self.d_t4, 0, 4)
+                be.copy_device(self._io(w_tok + 1 + i), be.view(self.d_t4, 0, 4), 4)
+            elif self.sampler == "reference":
+                be.sampler_select_device(d_row, 1, V, self.T, self._io(w_ud + i), self._io(w_tok + 1 + i))
             else:
                 d_ud = self._io(w_ud + i)
                 be.accept_device(d_row, d_row, self._io(w_tok), 0, V, self.T, False, d_ud, d_ud,
                                  self.d_sel_acc, self.d_sel_tok)
-                src = be.view(self.d_sel_tok, 0, 4)
-            be.copy_device(self._io(w_tok + 1 + i), src, 4)
+                be.copy_device(self._io(w_tok + 1 + i), be.view(self.d_sel_tok, 0, 4), 4)
         # verify and accept
         self._target_pass_device(self._io(w_tok, k + 1), k + 1)
         be.accept_device(self.d_target, None if self.greedy else self.d_draft, self._io(w_tok + 1, k),
@@ -342,3 +369,5 @@ class DeviceEngine:
         for name, b in list(vars(self).items()):
             if name.startswith("d_"):
                 self.be.free(b)
+        if self.ref_sampler is not None:
+            self.ref_sampler.free()
