@@ -304,6 +304,71 @@ int32_t tqf_hip_q4k_weights_upload_device(tqf_hip_ctx *ctx, const void *d_q4_k, 
  * 148-250's "reorder only if the values are proven unchanged"). */
 int32_t tqf_hip_q4k_weights_download(tqf_hip_ctx *ctx, const tqf_hip_weights *w, uint8_t *q4_k,
                                      size_t len);
+
+/* ---- routed-expert superextents of a .tqf container -> device ----------------
+ * The expert-index half of TqfReader (format/tqf/reader.rs:170-247, 312-327)
+ * and the staging path of Qwen36WeightLoader::expert_stored_bytes /
+ * load_expert (model/qwen36/weights.rs:1387-1444) with
+ * WholeExpertLfuCache::stage_expert_values (experts/mod.rs:512-545), over a
+ * container region the caller supplies (it reads or maps the file; file I/O
+ * and the BLAKE3 digests of the checksum table stay on its side).
+ * Decoded forms of the spec's section-124 records (the on-disk 32- and
+ * 24-byte little-endian layouts of format/tqf/records.rs:221-313).  The
+ * table functions run on the host only; their ctx may be NULL (it receives
+ * the last-error message). */
+#define TQF_HIP_MATRIX_GATE_UP 0
+#define TQF_HIP_MATRIX_DOWN 1
+typedef struct tqf_hip_expert_index {
+    uint8_t layer;
+    uint16_t expert;
+    uint16_t flags;          /* bit 0: per-tile checksums follow the expert's digest */
+    uint16_t layout_id;      /* quant layout; 2 = Q4_K passthrough */
+    uint64_t file_offset;    /* the superextent, from the start of the container */
+    uint32_t stored_bytes;
+    uint32_t tile_first;     /* into the tile table */
+    uint16_t tile_count;
+    uint32_t checksum_index;
+} tqf_hip_expert_index;
+typedef struct tqf_hip_expert_tile {
+    uint8_t matrix;          /* TQF_HIP_MATRIX_GATE_UP or _DOWN */
+    uint16_t tile_id;
+    uint16_t neuron_start, neuron_count;
+    uint32_t relative_offset, stored_bytes;  /* within the superextent */
+    uint16_t quant_layout_id;
+    uint16_t flags;
+} tqf_hip_expert_tile;
+typedef struct tqf_hip_expert_table tqf_hip_expert_table;
+/* Parses the expert-index blob (superblock expert_index_offset /
+ * expert_index_bytes): expert_count index records, then tile records to the
+ * end of the blob; expert_count is the ExpertIndex section's element_count,
+ * file_len the container's length, checksum_entries the checksum table's
+ * entry count.  TQF_HIP_ERR_INVALID (nothing allocated) unless, as TqfReader
+ * requires: the records fit, the tile part holds whole records with known
+ * matrices, every superextent lies inside the container, every tile range
+ * inside the tile table and exactly partitioning its superextent in order,
+ * and per-tile checksum ranges inside the checksum table. */
+int32_t tqf_hip_expert_table_open(tqf_hip_ctx *ctx, const uint8_t *blob, size_t blob_len, uint64_t expert_count,
+                                  uint64_t file_len, uint64_t checksum_entries, tqf_hip_expert_table **out);
+int32_t tqf_hip_expert_table_free(tqf_hip_ctx *ctx, tqf_hip_expert_table *table);
+int32_t tqf_hip_expert_table_counts(const tqf_hip_expert_table *table, uint64_t *experts, uint64_t *tiles);
+/* TqfReader::expert(layer, expert): the index record and its tiles
+ * (tiles_out may be NULL to ask for *n_tiles). */
+int32_t tqf_hip_expert_lookup(tqf_hip_ctx *ctx, const tqf_hip_expert_table *table, uint8_t layer, uint16_t expert,
+                              tqf_hip_expert_index *index_out, tqf_hip_expert_tile *tiles_out, size_t tiles_cap,
+                              size_t *n_tiles);
+/* The reservations to make before staging (expert_stored_bytes, the broker's
+ * reserve-before-allocate): the superextent's stored bytes (host staging),
+ * and the device bytes of its three Q4_K uploads. */
+int32_t tqf_hip_expert_reserve_bytes(tqf_hip_ctx *ctx, const tqf_hip_expert_table *table, uint8_t layer,
+                                     uint16_t expert, uint64_t *stored_bytes, uint64_t *device_bytes);
+/* load_expert's checks (layout Q4_K passthrough, 3 x 589,824 stored bytes,
+ * every tile Q4_K, classify_partition over the gate+up and down regions),
+ * then payload_parts and one Q4_K upload each of gate [512 x 2048], up
+ * [512 x 2048] and down [2048 x 512] from container[file_offset ..].  On
+ * failure nothing stays allocated. */
+int32_t tqf_hip_expert_upload(tqf_hip_ctx *ctx, const tqf_hip_expert_table *table, uint8_t layer, uint16_t expert,
+                              const uint8_t *container, size_t container_len, tqf_hip_weights **gate,
+                              tqf_hip_weights **up, tqf_hip_weights **down);
 /* fp32 semantics of backend::reference::q4k_gemv / q4k_gemm (backend/
  * reference.rs:49-81) and of the Metal tqf_q4k_gemv (backend/metal/
  * kernels.rs:535-593): y[t][r] = sum_i dequant(w[r])_i x[t][i].  x [m x cols],

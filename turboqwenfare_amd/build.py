@@ -20,7 +20,8 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_PATH = PKG_DIR / "libtqf_hip.so"
 SOURCES = ["tqf_q4.hip", "tqf_q4k.hip", "tqf_q6k.hip", "tqf_stack.hip", "tqf_grouped.hip",
-           "tqf_accept.hip", "tqf_sample.hip", "tqf_synth.hip", "tqf_loop.hip", "tqf_api.hip"]
+           "tqf_accept.hip", "tqf_sample.hip", "tqf_experts.hip", "tqf_synth.hip", "tqf_loop.hip",
+           "tqf_api.hip"]
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
