@@ -11,8 +11,11 @@ matrices come from the host Philox generator
 (synth.q4_0_synthetic), the same bytes the device generator writes.  The
 spread rel_err(h(h0 perturbed), h(h0)) is the floor below which no
 implementation that rounds differently from the oracle can be checked at
-this depth: tests/test_gpu_stack40.py bounds the GPU's error by a multiple of
-it.  CPU only, a few minutes:
+this depth.  It also replays the stack with only the device's activation
+rounding (replay_device_model: every matvec input as its 22-bit block
+records) and records that replay's distance from the oracle
+(``*_device_records``): tests/test_gpu_stack40.py bounds the GPU's error by
+it plus twice the every-layer spread.  CPU only, a few minutes:
 
     python tests/golden/make_stack40_spread.py
 """
@@ -28,7 +31,9 @@ sys.path[:0] = [str(HERE.parent.parent), str(HERE.parent), str(HERE.parent.paren
 from conftest import rel_err  # noqa: E402
 from stack_oracle import oracle_replay  # noqa: E402
 from turboqwenfare_amd import synth  # noqa: E402
-from turboqwenfare_amd.workloads import F, H, expert_tensor_ids, layer_host_f32  # noqa: E402
+from turboqwenfare_amd.workloads import E, F, H, expert_tensor_ids, layer_host_f32  # noqa: E402
+
+E_SHARED = E  # the shared expert's index in a layer's expert table
 
 LAYERS, TRIALS = 40, 3
 
@@ -65,6 +70,72 @@ def replay_noisy(st, h0, seed):
     return h, np.stack(routes)
 
 
+def records(v: np.ndarray) -> np.ndarray:
+    """The device's activation records of each 32-element block of v
+    (turboqwenfare_amd/csrc/tqf_device.h, block_scale and split_digits16):
+    with E the binary exponent of the block's largest |v| (blocks below
+    2^-100 are zero), every value becomes rint(v / 2^(E-21)) * 2^(E-21) --
+    a 22-bit integer of the block's scale."""
+    b = np.asarray(v, np.float64).reshape(-1, 32)
+    amax = np.abs(b).max(axis=1)
+    e = np.where(amax >= 2.0 ** -100, np.floor(np.log2(np.maximum(amax, 2.0 ** -100))) - 21, 0.0)
+    step = np.where(amax >= 2.0 ** -100, 2.0 ** e, 0.0)
+    q = np.where(step[:, None] > 0, np.rint(b / np.where(step > 0, step, 1.0)[:, None]) * step[:, None], 0.0)
+    return q.reshape(np.shape(v))
+
+
+def q4_0_dense(q: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """GGML Q4_0 bytes -> the exact float64 matrix [rows x cols]."""
+    blk = np.asarray(q, np.uint8).reshape(rows, cols // 32, 18)
+    d = blk[:, :, 0:2].copy().view(np.float16)[:, :, 0].astype(np.float64)
+    qs = blk[:, :, 2:18]
+    lo = (qs & 15).astype(np.float64) - 8.0
+    hi = (qs >> 4).astype(np.float64) - 8.0
+    return (np.concatenate([lo, hi], axis=2) * d[:, :, None]).reshape(rows, cols)
+
+
+def replay_device_model(st, h0, routes):
+    """The persistent kernel's arithmetic with only its activation rounding
+    kept: per layer, y = h * w_norm (f32), 1/rms from the row's sum of
+    squares, gate/up = (1/rms) * (W . records(y)), h_ffn = silu(gate) * up,
+    down = W_d . records(h_ffn), the shared pair scaled by sigmoid(gate . x)
+    and each route by its weight, h <- f32(h + sum).  Everything else in
+    float64, the routes taken from the oracle (the device's are bit-equal at
+    every layer), so the distance from the oracle's h is the activation
+    records' share of the device's."""
+    h = np.array(h0, np.float32)
+    m = h.shape[0]
+    for l in range(st.n_layers):
+        router, gate_vec, norm = st.host_f32[l]
+        y = (h * norm).astype(np.float32).astype(np.float64)
+        inv = 1.0 / np.sqrt((h.astype(np.float64) ** 2).sum(axis=1) / H + 1e-6)
+        ids = routes[l]
+        experts = sorted(set(int(v) for v in ids.reshape(-1)))
+        dense = {e: [q4_0_dense(mat, r, c) for mat, (r, c) in zip(st.expert_q4_0(l, e), ((F, H), (F, H), (H, F)))]
+                 for e in experts + [E_SHARED]}
+        xs = np.stack([records(y[t]) for t in range(m)])
+        out = np.zeros((m, H))
+        logits = (router.astype(np.float64) @ (y * inv[:, None]).T).T  # [m, E]
+        for t in range(m):
+            def expert(e):
+                g, u, dn = dense[e]
+                gt, ut = inv[t] * (g @ xs[t]), inv[t] * (u @ xs[t])
+                hf = gt / (1.0 + np.exp(-gt)) * ut
+                return dn @ records(hf)
+            gl = float(gate_vec.astype(np.float64) @ (y[t] * inv[t]))
+            acc = expert(E_SHARED) / (1.0 + np.exp(-gl))
+            lg = logits[t]
+            p = np.exp(lg - lg.max())
+            p /= p.sum()
+            top = ids[t].astype(int)
+            w = p[top] / p[top].sum()
+            for k in range(8):
+                acc = acc + w[k] * expert(int(top[k]))
+            out[t] = acc
+        h = (h.astype(np.float64) + out).astype(np.float32)
+    return h
+
+
 class _OneLayer:
     """Layer l of a HostStack as a one-layer stack."""
 
@@ -80,7 +151,9 @@ def main():
     out = {"layers": LAYERS,
            "noise": "h * (1 + 2^-24 n), n ~ N(0,1), numpy default_rng(seed): "
                     "<recipe>_m<M> on the input only (seeds 0..2), "
-                    "<recipe>_m<M>_every_layer before every layer (seeds 100..102)"}
+                    "<recipe>_m<M>_every_layer before every layer (seeds 100..102); "
+                    "<recipe>_m<M>_device_records: the replay with only the device's 22-bit "
+                    "block activation records (no noise)"}
     for recipe in ("zero_mean", "uniform"):
         st = HostStack(LAYERS, recipe)
         for m in (4, 1):
@@ -100,7 +173,9 @@ def main():
                 assert np.array_equal(ids, ids3), "a perturbation changed the routes"
                 every.append(float(rel_err(h3, h)))
             out[f"{recipe}_m{m}_every_layer"] = every
-            print(recipe, m, spreads, every, flush=True)
+            hd = replay_device_model(st, h0, ids)
+            out[f"{recipe}_m{m}_device_records"] = float(rel_err(hd, h))
+            print(recipe, m, spreads, every, out[f"{recipe}_m{m}_device_records"], flush=True)
         st.cache.clear()
     (HERE / "stack40_spread.json").write_text(json.dumps(out, indent=1) + "\n")
 

@@ -18,15 +18,17 @@ h is checked two ways:
   over the same resident layer) from the oracle's input to that layer, within
   1e-3 of |g - c| / max(|c|, 1) (backend/metal/expert.rs:309), the
   reference's own per-layer tolerance;
-- end to end over 40 layers, within 4x the oracle's own spread at that depth
-  (tests/golden/stack40_spread.json, made by make_stack40_spread.py: the
-  oracle's final h moves by 3.7e-4 to 4.6e-4 on the zero-mean stack when
-  rounding-level noise, 2^-24 relative, enters before every layer; by ~1e-6
-  on the uniform one).  The device rounds differently from the oracle at
-  every layer (its activation records hold 24 bits relative to each 32-value
-  block's maximum, a per-value rounding several times f32's), so its
-  end-to-end distance sits at a small multiple of that spread; a fixed 1e-3
-  is at the zero-mean stack's conditioning floor."""
+- end to end over 40 layers, within a bound derived from a model of the
+  device's rounding (tests/golden/stack40_spread.json, made by
+  make_stack40_spread.py).  The device's activation records round every
+  matvec input to 22 bits of its 32-value block's maximum; a float64 replay
+  that keeps exactly that rounding and nothing else (``*_device_records``)
+  ends 8.9e-4 from the oracle on the zero-mean stack and 5-6e-7 on the
+  uniform one -- the device's own distances are 0.86-1.08e-3 and 4.5-5.5e-7.
+  The rest of the device's rounding is f32 order and precision, whose effect
+  at this depth is measured by the oracle's own spread under 2^-24 relative
+  noise before every layer (``*_every_layer``: 3.7-4.6e-4 zero-mean, ~1e-6
+  uniform).  Bound: the records model's distance plus twice that spread."""
 import json
 from pathlib import Path
 
@@ -46,8 +48,10 @@ SPREAD = json.loads((Path(__file__).parent / "golden" / "stack40_spread.json").r
 
 
 def h_bound(recipe: str, m: int) -> float:
-    """4x the oracle's largest 40-layer spread under every-layer rounding noise."""
-    return 4.0 * max(SPREAD[f"{recipe}_m{m}_every_layer"])
+    """The activation records' share of the device's 40-layer distance (the
+    float64 replay with only the records' rounding), plus twice the oracle's
+    40-layer spread under every-layer f32-level noise."""
+    return SPREAD[f"{recipe}_m{m}_device_records"] + 2.0 * max(SPREAD[f"{recipe}_m{m}_every_layer"])
 
 
 @pytest.fixture(scope="module", params=["zero_mean", "uniform"])

@@ -189,3 +189,31 @@ def test_zero_mean_recipe_is_symmetric_and_keeps_scales():
     assert abs(q0.mean() + 0.5) < 0.01
     with pytest.raises(ValueError):
         synth.q4_0_synthetic(1, 32, 1, 1, 7)
+
+
+def test_device_record_model_rounds_like_the_records():
+    """make_stack40_spread.records (the 40-layer bound's model of the device's
+    activation records): each 32-value block keeps rint(v / 2^(E-21)) with E
+    the exponent of its largest |v|, so every value moves by at most 2^-22 of
+    the block maximum, values on the grid do not move, a block at or below
+    2^-100 is zero, and the largest value keeps 22-23 significant bits."""
+    import sys
+    from pathlib import Path
+
+    sys.path.insert(0, str(Path(__file__).resolve().parent / "golden"))
+    import make_stack40_spread as ms
+
+    rng = np.random.default_rng(5)
+    for scale in (1e-30, 1e-3, 1.0, 3e4):
+        v = (rng.standard_normal(256) * scale).astype(np.float32)
+        r = ms.records(v)
+        for b in range(8):
+            blk, rb = v[32 * b:32 * b + 32].astype(np.float64), r[32 * b:32 * b + 32]
+            amax = np.abs(blk).max()
+            assert np.abs(rb - blk).max() <= amax * 2.0 ** -22
+            step = 2.0 ** (np.floor(np.log2(amax)) - 21)
+            assert np.array_equal(rb / step, np.rint(rb / step))
+        assert np.array_equal(ms.records(r), r)
+    assert not ms.records(np.full(32, 2.0 ** -101, np.float32)).any()
+    grid = np.arange(-16, 16, dtype=np.float32) * 2.0 ** -10
+    assert np.array_equal(ms.records(grid), grid)
