@@ -250,12 +250,17 @@ int32_t tqf_hip_accept_device_noalloc(tqf_hip_ctx *ctx, const float *d_target,
  * total (softmax, :166-190), the stable descending sort with ties to the
  * lower token (compare_desc, :258-266), then draw's inverse CDF (:227-248)
  * with d_u[row] in the place of rng.next_f32().  d_tokens [rows] receives
- * the tokens.  The sums are sequential f32 folds, as in the reference, so a
- * call takes about a millisecond at vocab 151,936 (the acceptance's draw,
- * which sums in exact fixed point, takes microseconds); it is for callers
- * that need the reference's token for the same uniform. */
+ * the tokens.  The two sums are the reference's sequential f32 folds, bit for
+ * bit, computed in parallel: integer sums on the running sum's grid, with the
+ * crossings of a binade and the exact ties as single f32 adds.  d_sums (may
+ * be NULL; not written at temperature 0) receives [rows x 2]: the token-order
+ * total of the exponentials and the sorted-order total of the probabilities
+ * (NaN when a probability is NaN), for callers that check the softmax's
+ * normalisation.  For callers that need the reference's token for the same
+ * uniform; the acceptance's draw (exact fixed-point sums, no sort) is the
+ * faster pick. */
 int32_t tqf_hip_sampler_select_device(tqf_hip_ctx *ctx, const float *d_logits, uint32_t rows, uint32_t vocab,
-                                      float temperature, const float *d_u, int32_t *d_tokens);
+                                      float temperature, const float *d_u, int32_t *d_tokens, float *d_sums);
 /* top_logit_candidates (runtime/decode.rs:48-64) over `rows` rows of vocab
  * logits: tokens4/logits4 are [rows x 4]. */
 int32_t tqf_hip_top_logit_candidates(tqf_hip_ctx *ctx, const float *logits, uint32_t rows,

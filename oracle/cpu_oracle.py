@@ -54,6 +54,7 @@ _SIGS = {
     "orc_batch_union": (_u32, [_vp, _u32, _vp]),
     "orc_top_logit_candidates": (None, [_vp, _u32, _vp, _vp]),
     "orc_softmax_draw": (_u32, [_vp, _u32, _f32, _f32]),
+    "orc_softmax_draw_sums": (_u32, [_vp, _u32, _f32, _f32, _vp, _vp]),
     "orc_xoshiro_seed": (None, [C.POINTER(_Xoshiro), _u64]),
     "orc_xoshiro_next_u64": (_u64, [C.POINTER(_Xoshiro)]),
     "orc_xoshiro_next_f32": (_f32, [C.POINTER(_Xoshiro)]),
@@ -272,6 +273,15 @@ def top_logit_candidates(logits):
 def softmax_draw(logits, temperature: float, u: float) -> int:
     lg = _f32a(logits)
     return int(lib().orc_softmax_draw(_p(lg), lg.size, temperature, u))
+
+
+def softmax_draw_sums(logits, temperature: float, u: float):
+    """(token, total, psum): the draw with its token-order sum of the
+    exponentials and its sorted-order sum of the probabilities."""
+    lg = _f32a(logits)
+    t, ps = C.c_float(), C.c_float()
+    tok = int(lib().orc_softmax_draw_sums(_p(lg), lg.size, temperature, u, C.byref(t), C.byref(ps)))
+    return tok, np.float32(t.value), np.float32(ps.value)
 
 
 class Xoshiro:

@@ -529,6 +529,15 @@ static int cand_cmp(const void *pa, const void *pb)
 
 uint32_t orc_softmax_draw(const float *logits, uint32_t n, float temperature, float u)
 {
+    return orc_softmax_draw_sums(logits, n, temperature, u, NULL, NULL);
+}
+
+/* The same draw, also returning its two sums: *total, the token-order sum of
+ * the exponentials (sampling/mod.rs:176-178), and *psum, the sorted-order sum
+ * of the probabilities (:236); either pointer may be NULL. */
+uint32_t orc_softmax_draw_sums(const float *logits, uint32_t n, float temperature, float u, float *total_out,
+                               float *psum_out)
+{
     if (n == 0) return 0;
     float max = -INFINITY;
     for (uint32_t i = 0; i < n; ++i) max = fmaxf(max, logits[i]);
@@ -542,6 +551,8 @@ uint32_t orc_softmax_draw(const float *logits, uint32_t n, float temperature, fl
     qsort(c, n, sizeof(cand_t), cand_cmp);
     float psum = -0.0f;
     for (uint32_t i = 0; i < n; ++i) psum += c[i].value;
+    if (total_out) *total_out = total;
+    if (psum_out) *psum_out = psum;
     uint32_t result;
     if (!isfinite(psum) || psum <= 0.0f) {
         result = c[0].token;

@@ -150,6 +150,8 @@ void orc_top_logit_candidates(const float *logits, uint32_t n, uint32_t *tokens4
  * rng.next_f32() would supply.  Pinned: sampling/mod.rs:476-499 frequency
  * test, :500-519 temperature test, NaN tests. */
 uint32_t orc_softmax_draw(const float *logits, uint32_t n, float temperature, float u);
+uint32_t orc_softmax_draw_sums(const float *logits, uint32_t n, float temperature, float u, float *total_out,
+                               float *psum_out);
 
 typedef struct orc_xoshiro { uint64_t s[4]; } orc_xoshiro;
 /* sampling/mod.rs:283-298 SplitMix64 seeding. */

@@ -2,8 +2,11 @@
 against the C oracle's restatement of the reference's draw (orc_softmax_draw:
 softmax with f32::exp and the token-order total, the stable descending sort,
 the inverse-CDF walk; sampling/mod.rs:166-190, 227-266), bit for bit: the same
-token for the same logits, temperature and uniform.  The uniforms come from
-the reference's own generator (Xoshiro256PlusPlus::from_seed, next_f32)."""
+token for the same logits, temperature and uniform, and the same two f32 sums
+(the token-order total of the exponentials, the sorted-order total of the
+probabilities: orc_softmax_draw_sums), which the device computes with its
+exact parallel fold.  The uniforms come from the reference's own generator
+(Xoshiro256PlusPlus::from_seed, next_f32)."""
 import numpy as np
 import pytest
 
@@ -19,12 +22,28 @@ def logits_for(seed: int, scale: float = 3.0, vocab: int = V) -> np.ndarray:
     return (np.random.default_rng(seed).standard_normal(vocab) * scale).astype(np.float32)
 
 
+def same_f32(a, b) -> bool:
+    a, b = np.float32(a), np.float32(b)
+    return (np.isnan(a) and np.isnan(b)) or a.tobytes() == b.tobytes()
+
+
+def check_draws(backend, lg, T, us, what=None):
+    """The device's tokens and sums for rows lg against the oracle's."""
+    lg2 = np.atleast_2d(lg)
+    toks, sums = backend.sampler_select(lg2, T, list(us), sums=True)
+    for r in range(lg2.shape[0]):
+        tok, total, psum = orc.softmax_draw_sums(lg2[r], T, float(np.float32(us[r])))
+        assert toks[r] == tok, (what, r, toks[r], tok)
+        assert same_f32(sums[r, 0], total), (what, r, "total", sums[r, 0], total)
+        assert same_f32(sums[r, 1], psum), (what, r, "total2", sums[r, 1], psum)
+
+
 @pytest.mark.parametrize("seed", range(64))
 def test_select_equals_reference_draw(backend, seed):
     """The configuration's shape: V = 151,936, N(0, 9) logits, T = 0.7."""
     lg = logits_for(seed)
     u = Xoshiro256PlusPlus.from_seed(seed).next_f32()
-    assert backend.sampler_select(lg, 0.7, [u]) == [orc.softmax_draw(lg, 0.7, float(u))]
+    check_draws(backend, lg, 0.7, [u], seed)
 
 
 @pytest.mark.parametrize("scale,T", [(1.0, 1.0), (0.1, 1.0), (3.0, 2.0), (3.0, 0.05), (30.0, 0.7)])
@@ -33,8 +52,20 @@ def test_select_flat_and_peaked_rows(backend, scale, T):
     rng = Xoshiro256PlusPlus.from_seed(int(scale * 100 + T * 10))
     for s in range(3):
         lg = logits_for(1000 + s, scale)
-        u = rng.next_f32()
-        assert backend.sampler_select(lg, T, [u]) == [orc.softmax_draw(lg, T, float(u))], (scale, T, s)
+        check_draws(backend, lg, T, [rng.next_f32()], (scale, T, s))
+
+
+@pytest.mark.parametrize("T", [1.0, 0.5])
+def test_select_subnormal_exponentials(backend, T):
+    """Logits spread over 104 T below the maximum: about one exponential in
+    six is subnormal, and the token-order sum climbs through every binade from
+    the smallest subnormal's."""
+    rng = np.random.default_rng(int(T * 10))
+    lg = rng.uniform(-104.0 * T, 0.0, V).astype(np.float32)
+    lg[rng.integers(0, V)] = 0.0
+    us = Xoshiro256PlusPlus.from_seed(77)
+    for _ in range(3):
+        check_draws(backend, lg, T, [us.next_f32()], T)
 
 
 def test_select_rows_side_by_side(backend):
@@ -42,15 +73,14 @@ def test_select_rows_side_by_side(backend):
     lg = np.stack([logits_for(2000 + r, 1.0 + r) for r in range(8)])
     rng = Xoshiro256PlusPlus.from_seed(7)
     us = [rng.next_f32() for _ in range(8)]
-    want = [orc.softmax_draw(lg[r], 0.9, float(us[r])) for r in range(8)]
-    assert backend.sampler_select(lg, 0.9, us) == want
+    check_draws(backend, lg, 0.9, us)
 
 
 @pytest.mark.parametrize("u", [0.0, 2.0 ** -24, 0.5, 1.0 - 2.0 ** -24])
 def test_select_extreme_uniforms(backend, u):
     for seed in (11, 12):
         lg = logits_for(seed, 1.0)
-        assert backend.sampler_select(lg, 1.0, [u]) == [orc.softmax_draw(lg, 1.0, u)], (seed, u)
+        check_draws(backend, lg, 1.0, [u], (seed, u))
 
 
 def test_select_ties_nan_and_infinities(backend):
@@ -78,8 +108,7 @@ def test_select_ties_nan_and_infinities(backend):
     rows.append(t)
     for i, row in enumerate(rows):
         for _ in range(4):
-            u = rng.next_f32()
-            assert backend.sampler_select(row, 0.8, [u]) == [orc.softmax_draw(row, 0.8, float(u))], (i, u)
+            check_draws(backend, row, 0.8, [rng.next_f32()], i)
 
 
 @pytest.mark.parametrize("vocab", [1, 2, 63, 64, 65, 4095, 4096, 4097, 70_000])
@@ -87,8 +116,7 @@ def test_select_small_and_ragged_vocabularies(backend, vocab):
     rng = Xoshiro256PlusPlus.from_seed(vocab)
     for s in range(3):
         lg = logits_for(vocab * 10 + s, 2.0, vocab)
-        u = rng.next_f32()
-        assert backend.sampler_select(lg, 0.7, [u]) == [orc.softmax_draw(lg, 0.7, float(u))], (vocab, s)
+        check_draws(backend, lg, 0.7, [rng.next_f32()], (vocab, s))
 
 
 def test_greedy_is_the_argmax(backend):

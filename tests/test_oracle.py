@@ -397,6 +397,41 @@ def test_softmax_draw_inverse_cdf_boundaries():
     assert orc.softmax_draw(values, 1.0, 0.9999) == 3
 
 
+def _host_expf():
+    import ctypes
+    import ctypes.util
+
+    libm = ctypes.CDLL(ctypes.util.find_library("m"))
+    libm.expf.restype = ctypes.c_float
+    libm.expf.argtypes = [ctypes.c_float]
+    return libm.expf
+
+
+def test_softmax_draw_sums_are_the_sequential_f32_sums():
+    """The draw's two sums (orc_softmax_draw_sums) against numpy's float32
+    accumulate, which adds left to right in float32 (checked on a case where
+    a pairwise order would differ): the token-order total of the host C
+    library's expf((l - max) / T), then p = e / total and the sum of p in a
+    stable descending order.  Rows: the configuration's N(0, 9) logits,
+    flat ones, and one whose exponentials span the subnormal range."""
+    assert np.add.accumulate(np.float32([1.0, 2.0 ** -24, 2.0 ** -24]))[-1] == np.float32(1.0)
+    expf = _host_expf()
+    rng = np.random.default_rng(5)
+    rows = [((rng.standard_normal(151_936) * 3).astype(np.float32), 0.7),
+            ((rng.standard_normal(151_936) * 0.1).astype(np.float32), 1.0),
+            (rng.uniform(-104.0, 0.0, 20_000).astype(np.float32), 1.0)]
+    for lg, T in rows:
+        z = (lg - lg.max()) / np.float32(T)
+        e = np.array([expf(float(v)) for v in z], np.float32)
+        total = np.add.accumulate(e)[-1]
+        p = e / total
+        psum = np.add.accumulate(p[np.argsort(-p, kind="stable")])[-1]
+        tok, t_orc, p_orc = orc.softmax_draw_sums(lg, T, 0.37)
+        assert t_orc.tobytes() == total.tobytes() and p_orc.tobytes() == psum.tobytes()
+        assert tok == orc.softmax_draw(lg, T, 0.37)
+    assert np.count_nonzero((e > 0) & (e < np.finfo(np.float32).tiny)) > 1000  # subnormal terms
+
+
 # ---- Philox -------------------------------------------------------------------
 def philox_vectors():
     out = []

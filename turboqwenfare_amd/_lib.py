@@ -137,7 +137,7 @@ SIGNATURES = {
     "tqf_hip_set_variant": (_i32, [_vp, _i32, _i32]),
     "tqf_hip_get_variant": (_i32, [_vp, _i32, C.POINTER(_i32)]),
     "tqf_hip_recovery_counts": (_i32, [_vp, C.POINTER(_u64), C.POINTER(_u64)]),
-    "tqf_hip_sampler_select_device": (_i32, [_vp, _vp, _u32, _u32, C.c_float, _vp, _vp]),
+    "tqf_hip_sampler_select_device": (_i32, [_vp, _vp, _u32, _u32, C.c_float, _vp, _vp, _vp]),
     "tqf_hip_expert_table_open": (_i32, [_vp, _vp, C.c_size_t, _u64, _u64, _u64, C.POINTER(_vp)]),
     "tqf_hip_expert_table_free": (_i32, [_vp, _vp]),
     "tqf_hip_expert_table_counts": (_i32, [_vp, C.POINTER(_u64), C.POINTER(_u64)]),

@@ -556,14 +556,16 @@ class HipBackend:
 
     def sampler_select_device(self, d_logits: DeviceBuffer, rows: int, vocab: int,
                               temperature: float, d_u: DeviceBuffer | None,
-                              d_tokens: DeviceBuffer) -> None:
-        """Sampler::select on device rows (the reference's token for uniform d_u[row])."""
+                              d_tokens: DeviceBuffer, d_sums: DeviceBuffer | None = None) -> None:
+        """Sampler::select on device rows (the reference's token for uniform
+        d_u[row]); d_sums, if given, receives [rows x 2] (total, total2)."""
         self._check(self.lib.tqf_hip_sampler_select_device(
             self.ctx, d_logits.ptr, rows, vocab, float(temperature), d_u.ptr if d_u else None,
-            d_tokens.ptr))
+            d_tokens.ptr, d_sums.ptr if d_sums else None))
 
-    def sampler_select(self, logits: np.ndarray, temperature: float, u) -> list:
-        """Host form: [V] or [rows, V] logits and one uniform per row -> tokens."""
+    def sampler_select(self, logits: np.ndarray, temperature: float, u, sums: bool = False):
+        """Host form: [V] or [rows, V] logits and one uniform per row -> tokens,
+        and with sums=True also the [rows, 2] f32 folds (total, total2)."""
         lg = np.ascontiguousarray(logits, dtype=np.float32)
         lg2 = lg.reshape(1, -1) if lg.ndim == 1 else lg
         rows, vocab = lg2.shape
@@ -571,12 +573,15 @@ class HipBackend:
         if uu.size != rows:
             raise ValueError("one uniform per row")
         d_l, d_u, d_t = self.to_device(lg2), self.to_device(uu), self.alloc(4 * rows)
+        d_s = self.alloc(8 * rows) if sums else None
         try:
-            self.sampler_select_device(d_l, rows, vocab, temperature, d_u, d_t)
-            return [int(t) for t in self.read(d_t, np.int32, (rows,))]
+            self.sampler_select_device(d_l, rows, vocab, temperature, d_u, d_t, d_s)
+            toks = [int(t) for t in self.read(d_t, np.int32, (rows,))]
+            return (toks, self.read(d_s, np.float32, (rows, 2))) if sums else toks
         finally:
-            for b in (d_l, d_u, d_t):
-                self.free(b)
+            for b in (d_l, d_u, d_t, d_s):
+                if b is not None:
+                    self.free(b)
 
     def top_logit_candidates(self, logits: np.ndarray):
         """[V] or [rows, V] logits -> (tokens [rows, 4] u32, logits [rows, 4])."""

@@ -1943,7 +1943,7 @@ extern "C" int32_t tqf_hip_accept(tqf_hip_ctx *ctx, const float *target, const f
 
 extern "C" int32_t tqf_hip_sampler_select_device(tqf_hip_ctx *ctx, const float *d_logits, uint32_t rows,
                                                  uint32_t vocab, float temperature, const float *d_u,
-                                                 int32_t *d_tokens) {
+                                                 int32_t *d_tokens, float *d_sums) {
     TQF_ENTER(ctx);
     if (!d_logits || !d_tokens || (temperature != 0.0f && !d_u))
         return fail(ctx, TQF_HIP_ERR_INVALID, "null pointer");
@@ -1957,7 +1957,7 @@ extern "C" int32_t tqf_hip_sampler_select_device(tqf_hip_ctx *ctx, const float *
         TQF_HIP(ctx, grow(ctx->d_sample, ctx->sample_bytes, need));
     }
     Prof p(ctx);
-    hipError_t e = launch_sample_select(ctx->stream, d_logits, rows, vocab, temperature, d_u, d_tokens,
+    hipError_t e = launch_sample_select(ctx->stream, d_logits, rows, vocab, temperature, d_u, d_tokens, d_sums,
                                         ctx->d_sample);
     if (e != hipSuccess) return hip_fail(ctx, "sampler launch", e);
     p.end(TQF_HIP_KERNEL_SAMPLE, (double)rows * vocab * 4, 0.0, nullptr);

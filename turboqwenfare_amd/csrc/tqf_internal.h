@@ -481,11 +481,12 @@ bool accept_one_launch(uint32_t k, uint32_t vocab);
 hipError_t launch_top4(hipStream_t s, const float *logits, uint32_t rows, uint32_t vocab,
                        uint32_t *tokens4, float *logits4);
 // Sampler::select (tqf_sample.hip): one token per row of logits [rows x
-// vocab] from the uniform u[row]; temperature 0 takes the argmax.  scratch
-// holds sample_scratch_bytes(rows, vocab).
+// vocab] from the uniform u[row]; temperature 0 takes the argmax.  sums (may
+// be null) receives each row's two folds.  scratch holds
+// sample_scratch_bytes(rows, vocab).
 size_t sample_scratch_bytes(uint32_t rows, uint32_t vocab);
 hipError_t launch_sample_select(hipStream_t s, const float *logits, uint32_t rows, uint32_t vocab,
-                                float temperature, const float *u, int32_t *tokens, void *scratch);
+                                float temperature, const float *u, int32_t *tokens, float *sums, void *scratch);
 
 // ---- Q4_K (tqf_q4k.hip) ----------------------------------------------------
 // Activation records: q4k_prep writes the fp32-semantics GEMV's records
