@@ -431,19 +431,30 @@ __device__ void shared_rows(const StackArgs &a, const SharedLoads &S0) {
     }
 }
 
+// A unit's rows are software-pipelined: the loads of its first kAhead rows
+// (and the scale octets) are issued here, and gate_up_compute issues row
+// n + kAhead's just before it computes row n.  Issuing all of a wavefront's
+// rows at once stalls the wavefront until the shared weight stream has
+// nearly drained (the memory pipeline takes the loads only as fast as HBM
+// serves the whole chip), so its digit dots could only start after the
+// stream; pipelined, the dots of the rows that have landed run while the
+// later rows stream (measured per 40-layer launch: 1208 us issuing all
+// eight rows up front, 1152 / 1142 / 1147 / 1162 us with 1 / 3 / 4 / 6
+// rows ahead).
+constexpr int kAhead = 3;
 template <int RW>
 __device__ __forceinline__ void unit_loads_rw(int expert, int row0, UnitLoads &U) {
     const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
     const int lane = tid() % kWave;
     const RowLane Wg = row_lane(s_mats[expert * 3 + 0], kBpGate), Wu = row_lane(s_mats[expert * 3 + 1], kBpGate);
     const uint32_t r = (uint32_t)row0 + RW * wave;
+    U.sg = load_scales(Wg, r / 8, lane);
+    U.su = load_scales(Wu, r / 8, lane);
 #pragma unroll
-    for (int n = 0; n < RW; ++n) {
+    for (int n = 0; n < (RW < kAhead ? RW : kAhead); ++n) {
         U.ng[n] = load_nibbles(Wg, r + n, lane);
         U.nu[n] = load_nibbles(Wu, r + n, lane);
     }
-    U.sg = load_scales(Wg, r / 8, lane);
-    U.su = load_scales(Wu, r / 8, lane);
 }
 __device__ __forceinline__ void unit_loads(int expert, const UnitDesc &d, UnitLoads &U) {
     if (d.rw == 8) unit_loads_rw<8>(expert, d.row0, U);
@@ -453,8 +464,8 @@ __device__ __forceinline__ void unit_loads(int expert, const UnitDesc &d, UnitLo
 // This workgroup's first unit (blockIdx.x) from the routes alone, before the
 // pair plan exists: the expert of its pair, found with the plan's own pair
 // order (groups in first-demand order, a group's tokens ascending).  Every
-// wavefront issues its weight loads, which then fly while wavefront 0 builds
-// the plan.  False: the workgroup has no unit.
+// wavefront issues its first rows' weight loads (unit_loads_rw), which then
+// fly while wavefront 0 builds the plan.  False: the workgroup has no unit.
 __device__ __forceinline__ bool early_unit_loads(const StackArgs &a, UnitLoads &U) {
     const int lane = tid() % kWave;
     const int m = (int)a.m, n = m * kTopK;
@@ -786,12 +797,9 @@ __device__ void gate_up_compute(const StackArgs &a, const UnitDesc &d, UnitLoads
     const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
     const int lane = tid() % kWave;
     const int pos = (int)(((uint32_t)d.row0 + RW * wave) & 7);  // 0, or 4 in a 32-row unit
-    uint4 ng[RW], nu[RW];
-#pragma unroll
-    for (int n = 0; n < RW; ++n) {
-        ng[n] = q4_signed(U.ng[n]);
-        nu[n] = q4_signed(U.nu[n]);
-    }
+    const int expert = P.pair_expert[d.pair];
+    const RowLane Wg = row_lane(s_mats[expert * 3 + 0], kBpGate), Wu = row_lane(s_mats[expert * 3 + 1], kBpGate);
+    const uint32_t rbase = (uint32_t)d.row0 + RW * wave;
     const uint4 sg = U.sg, su = U.su;
     {
         const int i = 0, t = P.pair_tok[d.pair];
@@ -807,8 +815,16 @@ __device__ void gate_up_compute(const StackArgs &a, const UnitDesc &d, UnitLoads
         float v[2 * RW];
 #pragma unroll
         for (int n = 0; n < RW; ++n) {
-            v[2 * n] = octet_scale(sg, pos + n) * q4_block_dot(ng[n], x);
-            v[2 * n + 1] = octet_scale(su, pos + n) * q4_block_dot(nu[n], x);
+            // row n + kAhead's loads, then row n's dots; the scheduling
+            // barriers keep the compiler from hoisting every load to the top
+            if (n + kAhead < RW) {
+                U.ng[n + kAhead] = load_nibbles(Wg, rbase + n + kAhead, lane);
+                U.nu[n + kAhead] = load_nibbles(Wu, rbase + n + kAhead, lane);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            v[2 * n] = octet_scale(sg, pos + n) * q4_block_dot(q4_signed(U.ng[n]), x);
+            v[2 * n + 1] = octet_scale(su, pos + n) * q4_block_dot(q4_signed(U.nu[n]), x);
+            __builtin_amdgcn_sched_barrier(0);
         }
         // value 2n (gate row n) lands on lanes (64 / RW) n .., value 2n + 1 (up
         // row n) on the lanes 32 / RW above them
