@@ -292,7 +292,9 @@ def q4k_verify_bench(be, n_layers: int, seed: int, inputs, steps: int = 50, warm
 def gemv_pool_bench(be, n_mats: int, seed: int):
     """Config-1 GEMV bandwidth: one token against a rotating pool of distinct
     512 x 2048 Q4_0 matrices (far beyond the 256 MB Infinity Cache), one launch
-    per call, HIP events around the launches."""
+    per call: HIP events around the GEMV kernel (avg_us, gbs, frac), and the
+    host clock around whole calls, which add the x-record prep kernel and its
+    launch gap (call_us, call_gbs, call_frac)."""
     from turboqwenfare_amd import _lib, synth
 
     pool = [be.synth_q4_0(512, 2048, 900_000 + i, seed) for i in range(n_mats)]
@@ -306,6 +308,16 @@ def gemv_pool_bench(be, n_mats: int, seed: int):
     be.profile_enable(False)
     gemv = dict(matrices=n_mats, bytes_per_launch=by / n, avg_us=ms / n * 1e3, gbs=by / (ms * 1e-3) / 1e9)
     gemv["frac"] = gemv["gbs"] / HBM_PEAK_GBS
+    # the whole call: the x-record prep kernel, the GEMV and the gap between
+    # them (stream-ordered calls, host clock around 20 of them)
+    be.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(20):
+        be.q4_gemv_batched_device(pool, dx, dy)
+    be.synchronize()
+    call_s = (time.perf_counter() - t0) / 20
+    gemv.update(call_us=call_s * 1e6, call_gbs=gemv["bytes_per_launch"] / call_s / 1e9)
+    gemv["call_frac"] = gemv["call_gbs"] / HBM_PEAK_GBS
     for w in pool:
         be.free_weights(w)
     be.free(dx)
