@@ -244,8 +244,8 @@ int32_t ensure_stack_scratch(tqf_hip_ctx *ctx, uint32_t experts, uint32_t bp_dow
     // tagged words: zero holds no launch's tag
     TQF_HIP(ctx, hipMalloc(&sc.partial, (size_t)kStackTeams * members * kStackMT * 64 * 8));
     TQF_HIP(ctx, hipMemset(sc.partial, 0, (size_t)kStackTeams * members * kStackMT * 64 * 8));
-    TQF_HIP(ctx, hipMalloc(&sc.ssq, (size_t)kStackTeams * kStackMT * 4));
-    TQF_HIP(ctx, hipMemset(sc.ssq, 0, (size_t)kStackTeams * kStackMT * 4));
+    TQF_HIP(ctx, hipMalloc(&sc.ssq, (size_t)kStackTeams * kStackMT * 8));
+    TQF_HIP(ctx, hipMemset(sc.ssq, 0, (size_t)kStackTeams * kStackMT * 8));
     TQF_HIP(ctx, hipMalloc(&sc.h_save, (size_t)kStackMT * kStackHidden * 4));
     sc.experts = experts;
     sc.bp_down = bp_down;

@@ -316,7 +316,7 @@ struct StackArgs {
     uint32_t *hprep;    // [9 kStackMT pair rows of 28 x bp_down dwords]
     float *hshared;     // [kStackMT x F] the shared expert's silu(g) * u rows
     uint64_t *partial;  // [teams x members x kStackMT x 64] tagged words (tag << 32 | f32 bits)
-    float *ssq;         // [teams x kStackMT]
+    float *ssq;         // [teams x kStackMT] 64-bit words: layer-step tag << 32 | f32 sum of squares
     StackSync *sync;
     uint32_t members;   // workgroups per 64-row team in phase C
     uint32_t fail_at;   // layer whose barrier-B wait workgroup 0 takes as timed out (~0u: none)

@@ -5,9 +5,11 @@
 //   h <- h + MoE_l(rmsnorm_l(h))        (model/qwen36/runtime.rs:777-802)
 // with MoE_l = shared expert * sigmoid(gate . x) + sum_k w_k expert_k(x) over
 // the router's top-8 (experts/mod.rs:1540-1634).  Per layer two phases are
-// separated by grid barriers (every workgroup is resident, one per CU); the
+// separated by a grid barrier (every workgroup is resident, one per CU); the
 // input side of a layer (RMSNorm, router logits, activation records) is
-// produced by the previous layer's phase C (by a prologue for layer 0):
+// produced by the previous layer's phase C (by a prologue for layer 0), and
+// the layer's routing waits on those words themselves (the counted logit
+// words and tagged sums of squares) instead of on a second barrier:
 //
 //   B  every workgroup: 1/rms of the M rows from the per-team sums of
 //      squares; the router logits = 1/rms x the fixed-point sum of the
@@ -34,17 +36,25 @@
 //      y = h * w_norm, and the partial router logits sum_c R[e][c] y[c] of
 //      every expert (member k: experts [k E / K, (k + 1) E / K)) and of the
 //      shared-expert gate, added into a 2^-32 fixed-point accumulator with
-//      integer atomics (exact, so the sum over teams does not depend on
-//      their order).  h itself is written once, after the last layer.
+//      counted integer atomics (exact, so the sum over teams does not depend
+//      on their order), after the member's own record and sum-of-squares
+//      stores have completed.  h itself is written once, after the last
+//      layer.
 //
 // Everything exchanged between workgroups is written with agent-scope
 // atomic stores and read with agent-scope atomic loads, and every thread
-// drains its stores (s_waitcnt) before the barrier arrival, so no L2
-// write-back / invalidate is needed.  (Workgroup-scope stores and loads do
+// drains its stores (s_waitcnt) before the barrier arrival or, in the tail,
+// before its counted logit adds, so no L2 write-back / invalidate is needed.
+// What the removed second barrier ordered still holds: the next layer's
+// phase B writes (records of h, shared rows, tail inputs) can only start in a
+// workgroup once every member of every team has counted into every logit
+// word, i.e. has finished the layer (staging and exchange included), and the
+// partial words and the accumulator parity a layer zeroes stay ordered by
+// the layer's barrier.  (Workgroup-scope stores and loads do
 // not suffice even between the members of a team: their partial words were
 // not seen within the spin limit.)  Barrier waits are bounded in time: a
 // wait that exceeds kSpinLimit sets `abort`, after which every workgroup
-// leaves at its next barrier and the launch reports TQF_HIP_ERR_DEVICE (in
+// leaves at its next barrier or wait and the launch reports TQF_HIP_ERR_DEVICE (in
 // dev_status, and as 1 in the host flag); the last workgroup to exit resets
 // the barrier state for the next launch.  The library then re-runs the stack
 // through the per-layer kernels from the prologue's copy of h_in.
@@ -197,17 +207,30 @@ __device__ __forceinline__ void zero_lacc(uint64_t *acc, uint32_t part, uint32_t
         __hip_atomic_store(acc + k, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Router logits travel between phases as 2^-32 fixed point in 64-bit words:
-// each team adds llrint(partial * 2^32) with an integer atomic, so the sum over
-// the 32 teams is exact and independent of their order; a non-finite (or
-// out-of-range) partial sets the accumulator's flag word instead.
-__device__ __forceinline__ void add_fixed(uint64_t *word, uint64_t *flag, float v) {
+// Router logits travel between layers as 2^-32 fixed point in 64-bit words
+// that also count their contributors: each of the 32 teams adds
+// 2^58 + llrint(partial * 2^32) + 2^52 with an integer atomic, so the low 58
+// bits hold the exact sum (independent of the teams' order) plus 32 * 2^52,
+// and the top 6 bits count the teams that have added.  The next layer's
+// routing polls the words until all 32 have counted: the words carry their
+// own completion, and no grid barrier separates a layer's tail from the
+// next layer's routing.  |partial| must stay below 2^20 (about 931,000); a
+// partial that is larger or not finite sets the accumulator's flag word
+// instead and never counts, and the routing, which polls the flag with the
+// words, reports the router error.
+constexpr uint64_t kCountOne = 1ull << 58, kTermBias = 1ull << 52;
+__device__ __forceinline__ void add_counted(uint64_t *word, uint64_t *flag, float v) {
     const double d = (double)v * 4294967296.0;
-    if (fabs(d) < 9.0e18) {
-        __hip_atomic_fetch_add(word, (uint64_t)__double2ll_rn(d), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (fabs(d) < 4.0e15) {
+        __hip_atomic_fetch_add(word, kCountOne + (uint64_t)(__double2ll_rn(d) + (int64_t)kTermBias), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     } else {
         __hip_atomic_fetch_or(flag, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+__device__ __forceinline__ bool counted_done(uint64_t w) { return (w >> 58) == kStackTeams; }
+__device__ __forceinline__ uint64_t counted_value(uint64_t w) {
+    return (w & (kCountOne - 1)) - (uint64_t)kStackTeams * kTermBias;
 }
 __device__ __forceinline__ float logit_of(uint64_t fixed, float inv_rms) {
     return (float)((double)(int64_t)fixed * 0x1p-32 * (double)inv_rms);
@@ -500,7 +523,7 @@ __device__ __forceinline__ bool early_unit_loads(const StackArgs &a, UnitLoads &
 // After the loads are issued only LDS barriers are used: __syncthreads()
 // would wait for them.
 template <int LPRD, int MAXP>
-__device__ void compute_routes(const StackArgs &a, uint32_t l, UnitLoads &U, SharedLoads &S, bool &pre) {
+__device__ void compute_routes(const StackArgs &a, uint32_t l, UnitLoads &U, SharedLoads &S, bool &pre, uint32_t base) {
     const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
     const int lane = tid() % kWave;
     const uint32_t m = a.m, E = a.E;
@@ -515,14 +538,50 @@ __device__ void compute_routes(const StackArgs &a, uint32_t l, UnitLoads &U, Sha
     uint64_t fx[4], gfx = 0, flag = 0;
     float sq = 0.0f;
     if (wave < (int)m) {
+        // the words carry their own completion: poll until every team has
+        // counted into every logit word and stored its tagged sum of squares
+        // (or a team flagged a bad partial, or the wait times out)
+        const uint32_t qtag = stack_part_tag(base, l);
+        bool aborted = false;
+        const uint64_t *sq64 = reinterpret_cast<const uint64_t *>(a.ssq) + (lane % kStackTeams) * MT + t;
+        int64_t t0 = 0;
+        for (uint32_t spin = 1;; ++spin) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {  // unconditional loads: one round trip
-            const uint32_t e = (uint32_t)lane + 64u * i;
-            fx[i] = load_coherent_u64(lt + (e < E ? e : E - 1));
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t e = (uint32_t)lane + 64u * i;
+                fx[i] = load_coherent_u64(lt + (e < E ? e : E - 1));
+            }
+            gfx = load_coherent_u64(lt + E);
+            flag = load_coherent_u64(acc + (size_t)MT * (E + 1));
+            const uint64_t sw = load_coherent_u64(sq64);
+            sq = __uint_as_float((uint32_t)sw);
+            bool done = counted_done(gfx) && (uint32_t)(sw >> 32) == qtag;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) done = done && counted_done(fx[i]);
+            if (__all(done) || flag != 0) break;
+            if ((spin & 15) == 0) {
+                if (__hip_atomic_load(&a.sync->abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+                    aborted = true;  // no routes; the launch reports the abort
+                    break;
+                }
+                const int64_t now = wall_clock64();
+                if (t0 == 0) {
+                    t0 = now;
+                } else if (now - t0 > kSpinLimit) {
+                    __hip_atomic_store(&a.sync->abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (a.dev_status)
+                        __hip_atomic_store(a.dev_status, (int32_t)TQF_HIP_ERR_DEVICE, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                    aborted = true;
+                    break;
+                }
+            }
+            __builtin_amdgcn_s_sleep(1);
         }
-        gfx = load_coherent_u64(lt + E);
-        flag = load_coherent_u64(acc + (size_t)MT * (E + 1));
-        sq = load_coherent(&a.ssq[(lane % kStackTeams) * MT + t]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) fx[i] = counted_value(fx[i]);
+        gfx = counted_value(gfx);
+        if (aborted && lane == 0) P.bad = 2;
     }
     // the records only once the routing words are in (their 7 MB over all
     // workgroups would otherwise queue ahead of them), by the wavefronts
@@ -539,7 +598,7 @@ __device__ void compute_routes(const StackArgs &a, uint32_t l, UnitLoads &U, Sha
     if (blockIdx.x * kThreads < kLaccWords)
         zero_lacc(a.lacc + (size_t)((l + 1) & 1) * kLaccWords, blockIdx.x, gridDim.x);
     float lv[4], glog = 0.0f;
-    if (wave < (int)m) {
+    if (wave < (int)m && P.bad != 2) {  // 2: the wait for the words ended in an abort
         // 1/rms (RMSNorm, weights.rs:216-239) of row t from the 32 teams' sums
         const float inv = 1.0f / sqrtf(v / (float)H + 1e-6f);
         if (lane == 0) P.inv_rms[t] = inv;
@@ -903,7 +962,7 @@ __device__ __forceinline__ void share_loads(const StackArgs &a, uint32_t ln, Sha
 // pays per atomic instruction: 4-lane atomics straight from the reductions'
 // lanes took 1131 us per 40-layer launch, the gathered form 1098 us.
 __device__ void member_tail(const StackArgs &a, uint32_t tau, uint32_t k, const ShareLoads &S, float hv,
-                            float *s_y, uint64_t *acc, uint32_t ln) {
+                            float *s_y, uint64_t *acc, uint32_t ln, uint32_t base) {
     const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
     const int lane = tid() % kWave;
     const uint32_t m = a.m, E = a.E, K = a.members;
@@ -919,7 +978,10 @@ __device__ void member_tail(const StackArgs &a, uint32_t tau, uint32_t k, const 
         }
         if (k == 0) {
             const float v = group_reduce<64>(hv * hv, AddOp());
-            if (lane == 0) store_coherent(&a.ssq[tau * MT + t], v);
+            if (lane == 0)
+                __hip_atomic_store(reinterpret_cast<uint64_t *>(a.ssq) + tau * MT + t,
+                                   ((uint64_t)stack_part_tag(base, ln) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
         }
         if (k == K - 1) {  // the shared-expert gate, one column per lane
             const float g = group_reduce<64>(S.g * y, AddOp());
@@ -945,10 +1007,11 @@ __device__ void member_tail(const StackArgs &a, uint32_t tau, uint32_t k, const 
             }
         }
         lds_barrier();
+        if (i == 0) wait_own_stores();  // records and sums of squares before any count
         const uint32_t t = tid() / 32, ee = e0 + 32 * i + tid() % 32;
-        if (tid() < MT * 32 && t < m && ee < e1) add_fixed(acc + (size_t)t * (E + 1) + ee, flag, s_lv[t][tid() % 32]);
+        if (tid() < MT * 32 && t < m && ee < e1) add_counted(acc + (size_t)t * (E + 1) + ee, flag, s_lv[t][tid() % 32]);
         if (i == 0 && k == K - 1 && tid() >= MT * 32 && tid() < MT * 32 + m)
-            add_fixed(acc + (size_t)(tid() - MT * 32) * (E + 1) + E, flag, s_lv[tid() - MT * 32][32]);
+            add_counted(acc + (size_t)(tid() - MT * 32) * (E + 1) + E, flag, s_lv[tid() - MT * 32][32]);
         lds_barrier();  // s_lv is rewritten by the next pass
     };
 #pragma unroll
@@ -968,7 +1031,7 @@ __device__ void member_tail(const StackArgs &a, uint32_t tau, uint32_t k, const 
 // grid barrier, and h (which may be h_in) is written only after the last
 // layer, which no workgroup reaches before all have passed the first barrier,
 // so the copy is of the input even when the launch updates h in place.
-__device__ void team_prologue(const StackArgs &a, float &hres) {
+__device__ void team_prologue(const StackArgs &a, float &hres, uint32_t base) {
     const uint32_t tau = blockIdx.x % kStackTeams, k = blockIdx.x / kStackTeams;
     if (k >= a.members) return;
     ShareLoads S;
@@ -976,7 +1039,7 @@ __device__ void team_prologue(const StackArgs &a, float &hres) {
     const uint32_t tt = tid() / 64, row = tid() % 64;
     hres = tid() < MT * 64 && tt < a.m ? load_coherent(&a.h_in[(size_t)tt * H + tau * 64 + row]) : 0.0f;
     if (k == 0 && a.h_save && tid() < MT * 64 && tt < a.m) a.h_save[(size_t)tt * H + tau * 64 + row] = hres;
-    member_tail(a, tau, k, S, hres, reinterpret_cast<float *>(s_dyn), a.lacc, 0);
+    member_tail(a, tau, k, S, hres, reinterpret_cast<float *>(s_dyn), a.lacc, 0, base);
 }
 
 // Phase C's partials travel as tagged 64-bit words: tag << 32 | f32 bits, the
@@ -1223,7 +1286,7 @@ __device__ void phase_c(const StackArgs &a, uint32_t l, uint32_t base, float &hr
         return;
     }
     member_tail(a, tau, k, SL, hres, reinterpret_cast<float *>(s_x), a.lacc + (size_t)((l + 1) & 1) * kLaccWords,
-                l + 1);
+                l + 1, base);
 }
 
 }  // namespace
@@ -1248,7 +1311,7 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
     if (tid() == 0 && xcc_id() != blockIdx.x % kStackBarrierGroups)
         __hip_atomic_fetch_or(&a.sync->xcd_bad, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     float hres = 0.0f;  // the residual: this thread's team row of h (phase C members)
-    team_prologue(a, hres);
+    team_prologue(a, hres, base);
     bool ok = grid_sync(a.sync, epoch, a.dev_status);
     if (tid() == 0)
         P.xcd_local = a.members == kLocalMembers && gridDim.x == kLocalMembers * kStackTeams &&
@@ -1259,13 +1322,13 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
         UnitLoads U;
         SharedLoads S;
         bool pre;
-        compute_routes<LPRD, MAXP>(a, l, U, S, pre);
+        compute_routes<LPRD, MAXP>(a, l, U, S, pre, base);
         if (blockIdx.x == 0 && tid() < a.m * kTopK) {
             const uint32_t t = tid() / kTopK, kk = tid() % kTopK;
             if (a.ids_out) a.ids_out[((size_t)l * a.m + t) * kTopK + kk] = P.bad ? 0 : (uint16_t)P.ids[t][kk];
             if (a.w_out) a.w_out[((size_t)l * a.m + t) * kTopK + kk] = P.bad ? 0.0f : P.w[t][kk];
         }
-        if (blockIdx.x == 0 && tid() == 0 && P.bad && a.status)
+        if (blockIdx.x == 0 && tid() == 0 && P.bad == 1 && a.status)
             __hip_atomic_store(a.status, (int32_t)TQF_HIP_ERR_ROUTER, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
         const int n_units = P.n_groups > 0 ? (int)a.m * kTopK * (int)(a.F / 64) : 0;
@@ -1309,6 +1372,7 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
             }
         }
         phase_c<LPRD, MAXP>(a, l, base, hres, SL);
+        if (!(ok = P.ok != 0)) break;
         if (more) {
             __syncthreads();  // every wavefront is past phase C's table reads
 #pragma unroll
@@ -1317,7 +1381,6 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
                 if (k < (a.E + 1) * 3) s_mats[k] = mp[i];
             }
         }
-        if (more && !(ok = grid_sync(a.sync, epoch, a.dev_status))) break;
     }
     stack_exit(a.sync, a.lacc, base, a.n_layers, a.host_flag);
 }
