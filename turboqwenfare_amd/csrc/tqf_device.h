@@ -62,20 +62,71 @@ __device__ __forceinline__ int readlane_i(int v, int lane) {
     return __builtin_amdgcn_readlane(v, lane);
 }
 
-// The wavefront's maximum, broadcast through a scalar register: the row
-// maximum by the four DPP steps, then row_bcast:15 (lane 15 of rows 0 / 2
-// into rows 1 / 3) and row_bcast:31 (lane 31 into rows 2 and 3) leave the
-// wave's maximum in lane 63.  Every lane must be active.
-__device__ __forceinline__ float wave_max_bcast(float v) {
-    v = fmaxf(v, dpp_f<kDppXor1>(v));
-    v = fmaxf(v, dpp_f<kDppXor2>(v));
-    v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
-    v = fmaxf(v, dpp_f<kDppMirror>(v));
-    const int b15 = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x142, 0xA, 0xF, false);
-    v = fmaxf(v, __int_as_float(b15));
-    const int b31 = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x143, 0xC, 0xF, false);
-    v = fmaxf(v, __int_as_float(b31));
-    return readlane_f(v, 63);
+// The wavefront's maximum of an unsigned key, broadcast through scalar
+// registers: each DPP step is one fused v_max_u32_dpp (a float maximum needs
+// a move, a canonicalise and the maximum per step), then the four rows'
+// maxima are combined in scalar registers.  Every lane must be active.
+__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppXor1, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppXor2, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppHalfMirror, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppMirror, 0xF, 0xF, false));
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+    const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return max(max(a, b), max(c, d));
+}
+// Order-preserving map of a float (not NaN) to an unsigned key, and back.
+__device__ __forceinline__ uint32_t f2key(float x) {
+    const uint32_t b = __float_as_uint(x);
+    return b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
+}
+__device__ __forceinline__ float key2f(uint32_t k) {
+    return __uint_as_float(k ^ ((uint32_t)((int32_t)~k >> 31) | 0x80000000u));
+}
+// The wavefront's maximum of four floats per lane (none NaN), to every lane.
+__device__ __forceinline__ float wave_max4(const float (&v)[4]) {
+    return key2f(wave_umax(max(max(f2key(v[0]), f2key(v[1])), max(f2key(v[2]), f2key(v[3])))));
+}
+
+// The router's top-8 (experts/mod.rs:134-197: the stable descending sort of
+// the probabilities, so equal probabilities in ascending id order) of the
+// E <= 256 probabilities p[i] of ids lane + 64 i, in the order taken.  Keys
+// (bits(p) + 1) << 2 | (3 - i) order entries by probability (0 <= p <= 1, so
+// the bits order as the values and the key fits 32 bits), then by the smaller
+// i, i.e. the smaller id (lane < 64); equal keys are broken by the lowest
+// lane, the smallest id again; 0 marks no expert.  Each lane first orders its
+// four keys, then 8 rounds take the largest lane head.  Every lane of the
+// wavefront must be active; psel / idsel are uniform.
+__device__ __forceinline__ void top8_by_probability(const float (&p)[4], int lane, uint32_t E, float (&psel)[8],
+                                                    int (&idsel)[8]) {
+    uint32_t q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        q[i] = ((uint32_t)lane + 64u * i < E) ? ((__float_as_uint(p[i]) + 1u) << 2) | (3u - (uint32_t)i) : 0u;
+    auto order = [&](int x, int y) {
+        const uint32_t hi = max(q[x], q[y]), lo = min(q[x], q[y]);
+        q[x] = hi;
+        q[y] = lo;
+    };
+    order(0, 1);
+    order(2, 3);
+    order(0, 2);
+    order(1, 3);
+    order(1, 2);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t best = wave_umax(q[0]);
+        const int l_win = (int)__builtin_ctzll(__ballot(q[0] == best));
+        psel[k] = __uint_as_float((best >> 2) - 1u);
+        idsel[k] = l_win + 64 * (int)(3u - (best & 3u));
+        const bool won = lane == l_win;
+        q[0] = won ? q[1] : q[0];
+        q[1] = won ? q[2] : q[1];
+        q[2] = won ? q[3] : q[2];
+        q[3] = won ? 0u : q[3];
+    }
 }
 
 // All-reduce over aligned groups of LANES lanes (2..64); every lane of a

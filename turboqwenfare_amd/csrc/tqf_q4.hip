@@ -408,7 +408,7 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
             if (lane == 0) s_bad = 1;
             continue;
         }
-        const float mx = wave_max_bcast(fmaxf(fmaxf(lv[0], lv[1]), fmaxf(lv[2], lv[3])));
+        const float mx = wave_max4(lv);
         float p[4], ssum = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -419,50 +419,10 @@ __global__ __launch_bounds__(256) void route_kernel(LayerDev L, const float *__r
         ssum = group_reduce<64>(ssum, AddOp());
 #pragma unroll
         for (int i = 0; i < 4; ++i) p[i] = ((uint32_t)lane + 64u * i < E) ? p[i] / ssum : -1.0f;
-        // top-8 by (probability descending, id ascending): each lane orders
-        // its four entries (ids lane + 64 i), then 8 rounds take the largest
-        // lane head, the lowest id among equal heads
-        float q[4] = {p[0], p[1], p[2], p[3]};
-        int qi[4] = {0, 1, 2, 3};
-        auto order = [&](int x, int y) {
-            const bool sw = q[y] > q[x] || (q[y] == q[x] && qi[y] < qi[x]);
-            const float tq = sw ? q[y] : q[x], uq = sw ? q[x] : q[y];
-            const int ti = sw ? qi[y] : qi[x], ui = sw ? qi[x] : qi[y];
-            q[x] = tq;
-            q[y] = uq;
-            qi[x] = ti;
-            qi[y] = ui;
-        };
-        order(0, 1);
-        order(2, 3);
-        order(0, 2);
-        order(1, 3);
-        order(1, 2);
+        // top-8 by (probability descending, id ascending)
         float psel[kTopK];
         int idsel[kTopK];
-#pragma unroll
-        for (int k = 0; k < kTopK; ++k) {
-            const float best = wave_max_bcast(q[0]);
-            const uint64_t cand = __ballot(q[0] == best);
-            int l_win = (int)__builtin_ctzll(cand);
-            if (__builtin_popcountll(cand) > 1) {  // equal heads: the lowest id
-                const uint64_t c0 = __ballot(q[0] == best && qi[0] == 0);
-                const uint64_t c1 = __ballot(q[0] == best && qi[0] == 1);
-                const uint64_t c2 = __ballot(q[0] == best && qi[0] == 2);
-                l_win = (int)__builtin_ctzll(c0 ? c0 : c1 ? c1 : c2 ? c2 : cand);
-            }
-            psel[k] = best;
-            idsel[k] = l_win + 64 * __builtin_amdgcn_readlane(qi[0], l_win);
-            if (lane == l_win) {
-                q[0] = q[1];
-                q[1] = q[2];
-                q[2] = q[3];
-                q[3] = -2.0f;
-                qi[0] = qi[1];
-                qi[1] = qi[2];
-                qi[2] = qi[3];
-            }
-        }
+        top8_by_probability(p, lane, E, psel, idsel);
         if (lane == 0) {
             float total = -0.0f;
             for (int k = 0; k < kTopK; ++k) total += psel[k];

@@ -518,6 +518,7 @@ __device__ __forceinline__ bool early_unit_loads(const StackArgs &a, UnitLoads &
     return true;
 }
 
+
 // ---- phase B: routes ------------------------------------------------------------
 // `pre`: whether this workgroup's first unit's loads were issued (in `U`).
 // After the loads are issued only LDS barriers are used: __syncthreads()
@@ -617,7 +618,7 @@ __device__ void compute_routes(const StackArgs &a, uint32_t l, UnitLoads &U, Sha
         if (__any(!fin)) {
             if (lane == 0) P.bad = 1;
         } else {
-            const float mx = wave_max_bcast(fmaxf(fmaxf(lv[0], lv[1]), fmaxf(lv[2], lv[3])));
+            const float mx = wave_max4(lv);
             float p[4], ssum = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -629,51 +630,10 @@ __device__ void compute_routes(const StackArgs &a, uint32_t l, UnitLoads &U, Sha
 #pragma unroll
             for (int i = 0; i < 4; ++i) p[i] = ((uint32_t)lane + 64u * i < E) ? p[i] / ssum : -1.0f;
             // top-8 by (probability descending, id ascending), as the stable
-            // descending sort of from_logits: each lane first orders its four
-            // entries (ids lane + 64 i), then 8 rounds take the largest lane
-            // head; among equal heads the lowest id wins (the common
-            // single-candidate case needs one ballot)
-            float q[4] = {p[0], p[1], p[2], p[3]};
-            int qi[4] = {0, 1, 2, 3};
-            auto order = [&](int x, int y) {
-                const bool sw = q[y] > q[x] || (q[y] == q[x] && qi[y] < qi[x]);
-                const float tq = sw ? q[y] : q[x], uq = sw ? q[x] : q[y];
-                const int ti = sw ? qi[y] : qi[x], ui = sw ? qi[x] : qi[y];
-                q[x] = tq;
-                q[y] = uq;
-                qi[x] = ti;
-                qi[y] = ui;
-            };
-            order(0, 1);
-            order(2, 3);
-            order(0, 2);
-            order(1, 3);
-            order(1, 2);
+            // descending sort of from_logits
             float psel[kTopK];
             int idsel[kTopK];
-#pragma unroll
-            for (int k = 0; k < kTopK; ++k) {
-                const float best = wave_max_bcast(q[0]);
-                const uint64_t cand = __ballot(q[0] == best);
-                int l_win = (int)__builtin_ctzll(cand);
-                if (__builtin_popcountll(cand) > 1) {  // equal heads: the lowest id
-                    const uint64_t c0 = __ballot(q[0] == best && qi[0] == 0);
-                    const uint64_t c1 = __ballot(q[0] == best && qi[0] == 1);
-                    const uint64_t c2 = __ballot(q[0] == best && qi[0] == 2);
-                    l_win = (int)__builtin_ctzll(c0 ? c0 : c1 ? c1 : c2 ? c2 : cand);
-                }
-                psel[k] = best;
-                idsel[k] = l_win + 64 * __builtin_amdgcn_readlane(qi[0], l_win);
-                if (lane == l_win) {
-                    q[0] = q[1];
-                    q[1] = q[2];
-                    q[2] = q[3];
-                    q[3] = -2.0f;
-                    qi[0] = qi[1];
-                    qi[1] = qi[2];
-                    qi[2] = qi[3];
-                }
-            }
+            top8_by_probability(p, lane, E, psel, idsel);
             // renormalise (experts/mod.rs:159-166): the total is the route-order
             // sum; each lane k < 8 divides its own weight
             float total = -0.0f;
