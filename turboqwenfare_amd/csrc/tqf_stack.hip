@@ -109,7 +109,7 @@ struct RoutePlan {
     int32_t grp_base[1 + MT * kTopK];   // first pair index of the group
     int32_t grp_tok[1 + MT * kTopK][MT];
     int32_t pair_expert[MT * (kTopK + 1)];
-    int32_t pair_tok[64 + 64];  // [0, 9 MT): pairs; [64, 128): plan scratch
+    int32_t pair_tok[MT * (kTopK + 1)];
     float pair_coef[MT * (kTopK + 1)];
     float inv_rms[MT];
     int32_t last;
@@ -485,35 +485,48 @@ __device__ __forceinline__ void unit_loads(int expert, const UnitDesc &d, UnitLo
     else unit_loads_rw<4>(expert, d.row0, U);
 }
 
-// This workgroup's first unit (blockIdx.x) from the routes alone, before the
-// pair plan exists: the expert of its pair, found with the plan's own pair
-// order (groups in first-demand order, a group's tokens ascending).  Every
-// wavefront issues its first rows' weight loads (unit_loads_rw), which then
-// fly while wavefront 0 builds the plan.  False: the workgroup has no unit.
-__device__ __forceinline__ bool early_unit_loads(const StackArgs &a, UnitLoads &U) {
-    const int lane = tid() % kWave;
-    const int m = (int)a.m, n = m * kTopK;
-    const int u = (int)blockIdx.x;
-    if (u >= n * ((int)a.F / 64)) return false;
-    const UnitDesc d = unit_desc(u, (int)a.F, m);
-    // route entry i = (t, k) on lane i; other lanes carry distinct dummy keys
-    const int e_i = lane < n ? P.ids[lane / kTopK][lane % kTopK] : 256 + lane;
-    const uint64_t peers = match_peers((uint32_t)e_i);
-    const uint64_t below = (1ull << lane) - 1ull;
-    const int first = (int)__builtin_ctzll(peers);  // the group's first entry
-    const int rank = __builtin_popcountll(peers & below);
-    // entries of groups that start before this entry's group: an exclusive
-    // prefix sum, in lane order, of each group's size at its first entry
-    const int size_at_first = (lane < n && first == lane) ? __builtin_popcountll(peers) : 0;
+// The pair plan's order (experts/mod.rs forward_batch's union: groups in
+// first-demand order, a group's tokens ascending) for route entry i = (t, k)
+// on lane i of a wavefront, from the routes alone: the lanes of equal experts
+// (match_peers), the group's first entry, this entry's rank in its group,
+// and the entries of the groups that start before it (an exclusive prefix
+// sum, in lane order, of each group's size at its first entry).  Lanes >= n
+// carry distinct dummy keys.  The entry's pair is m + before + rank.
+struct RouteEntry {
+    int e, first, rank, cnt, before;
+    uint64_t fmask;  // lanes that start a group
+};
+__device__ __forceinline__ RouteEntry route_entry(int lane, int n) {
+    RouteEntry r;
+    r.e = lane < n ? P.ids[lane / kTopK][lane % kTopK] : 256 + lane;
+    const uint64_t peers = match_peers((uint32_t)r.e);
+    r.first = (int)__builtin_ctzll(peers);
+    r.rank = __builtin_popcountll(peers & ((1ull << lane) - 1ull));
+    r.cnt = __builtin_popcountll(peers);
+    const bool starts = lane < n && r.first == lane;
+    r.fmask = __ballot(starts);
+    const int size_at_first = starts ? r.cnt : 0;
     int incl = size_at_first;
 #pragma unroll
     for (int off = 1; off < kWave; off <<= 1) {
         const int o = __shfl_up(incl, off);
         if (lane >= off) incl += o;
     }
-    const int before = __shfl(incl - size_at_first, first);
-    const uint64_t hit = __ballot(lane < n && m + before + rank == d.pair);
-    const int expert = __builtin_amdgcn_readlane(e_i, (int)__builtin_ctzll(hit));
+    r.before = __shfl(incl - size_at_first, r.first);
+    return r;
+}
+
+// This workgroup's first unit (blockIdx.x) from the route entries: every
+// wavefront issues its first rows' weight loads (unit_loads_rw).  False: the
+// workgroup has no unit.
+__device__ __forceinline__ bool early_unit_loads(const StackArgs &a, const RouteEntry &r, UnitLoads &U) {
+    const int lane = tid() % kWave;
+    const int m = (int)a.m, n = m * kTopK;
+    const int u = (int)blockIdx.x;
+    if (u >= n * ((int)a.F / 64)) return false;
+    const UnitDesc d = unit_desc(u, (int)a.F, m);
+    const uint64_t hit = __ballot(lane < n && m + r.before + r.rank == d.pair);
+    const int expert = __builtin_amdgcn_readlane(r.e, (int)__builtin_ctzll(hit));
     unit_loads(expert, d, U);
     return true;
 }
@@ -674,44 +687,24 @@ __device__ void compute_routes(const StackArgs &a, uint32_t l, UnitLoads &U, Sha
     // the shared expert's rows (records and row loads are in by now), before
     // any unit load is issued, so that they wait for nothing else
     shared_rows<LPRD, MAXP>(a, S);
-    // the pair plan, one route entry i = (t, k) per lane of wavefront 0: the
-    // entries of the same expert as bits of one mask (broadcast LDS reads).
-    // Wavefront 0 builds it before issuing its own unit loads: the others'
-    // loads already stream meanwhile, and issuing stalls once the CU's memory
-    // pipeline is full.
+    // the pair plan, one route entry i = (t, k) per lane (every wavefront
+    // computes the entries for its own first unit; wavefront 0 also writes
+    // the plan)
+    const int n = (int)m * kTopK;
+    const RouteEntry r = route_entry(lane, n);
     if (wave == 0) {
-        const int n = (int)m * kTopK;
-        const int *flat = &P.ids[0][0];
-        const int e_i = lane < n ? flat[lane] : -1 - lane;
-        uint32_t eq = 0;
-#pragma unroll
-        for (int j = 0; j < MT * kTopK; ++j) eq |= (j < n && flat[j] == e_i) ? (1u << j) : 0u;
-        const int cnt = __builtin_popcount(eq);
-        const int rank = __builtin_popcount(eq & ((1u << (lane & 31)) - 1u));
-        const int first = lane < n ? __builtin_ctz(eq) : lane;
-        const bool flag = lane < n && first == lane;
-        const uint64_t fmask = __ballot(flag);
-        P.pair_tok[64 + lane] = first;  // scratch row: every entry's group start
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        int before = 0;  // route entries whose group starts before this entry's group
-#pragma unroll
-        for (int j = 0; j < MT * kTopK; ++j)
-            before += (j < n && P.pair_tok[64 + j] < first) ? 1 : 0;
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        const int g = 1 + __builtin_popcountll(fmask & ((1ull << first) - 1ull));
+        const int g = 1 + __builtin_popcountll(r.fmask & ((1ull << r.first) - 1ull));
         if (lane < n) {
             const int t = lane / kTopK;
-            const int pair = (int)m + before + rank;
-            P.pair_expert[pair] = e_i;
+            const int pair = (int)m + r.before + r.rank;
+            P.pair_expert[pair] = r.e;
             P.pair_tok[pair] = t;
             P.pair_coef[pair] = P.w[t][lane % kTopK];
-            P.grp_tok[g][rank] = t;
-            if (flag) {
-                P.grp_expert[g] = e_i;
-                P.grp_cnt[g] = cnt;
-                P.grp_base[g] = (int)m + before;
+            P.grp_tok[g][r.rank] = t;
+            if (r.first == lane) {
+                P.grp_expert[g] = r.e;
+                P.grp_cnt[g] = r.cnt;
+                P.grp_base[g] = (int)m + r.before;
             }
         }
         if (lane < (int)m) {
@@ -724,11 +717,11 @@ __device__ void compute_routes(const StackArgs &a, uint32_t l, UnitLoads &U, Sha
             P.grp_expert[0] = (int)E;
             P.grp_cnt[0] = (int)m;
             P.grp_base[0] = 0;
-            P.n_groups = 1 + __builtin_popcountll(fmask);
+            P.n_groups = 1 + __builtin_popcountll(r.fmask);
             P.n_pairs = (int)m * (kTopK + 1);
         }
     }
-    pre = early_unit_loads(a, U);
+    pre = early_unit_loads(a, r, U);
     lds_barrier();
 }
 
