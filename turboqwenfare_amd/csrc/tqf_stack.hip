@@ -684,9 +684,6 @@ __device__ void compute_routes(const StackArgs &a, uint32_t l, UnitLoads &U, Sha
         lds_barrier();
         return;
     }
-    // the shared expert's rows (records and row loads are in by now), before
-    // any unit load is issued, so that they wait for nothing else
-    shared_rows<LPRD, MAXP>(a, S);
     // the pair plan, one route entry i = (t, k) per lane (every wavefront
     // computes the entries for its own first unit; wavefront 0 also writes
     // the plan)
@@ -802,8 +799,8 @@ __device__ bool prefetch_down(const StackArgs &a) {
 
 // ---- phase B: one gate/up unit -------------------------------------------------
 // `preloaded`: U already holds this unit's loads (early_unit_loads).
-template <int RW, int LPRD, int MAXP>
-__device__ void gate_up_compute(const StackArgs &a, const UnitDesc &d, UnitLoads &U) {
+template <int RW, int LPRD, int MAXP, class Hook>
+__device__ void gate_up_compute(const StackArgs &a, const UnitDesc &d, UnitLoads &U, Hook &&hook) {
     // one token: the pair's
     const uint4 *xr = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint8_t *>(s_dyn) +
                                                       LdsLayout<LPRD, MAXP>::kXr);
@@ -835,6 +832,10 @@ __device__ void gate_up_compute(const StackArgs &a, const UnitDesc &d, UnitLoads
                 U.nu[n + kAhead] = load_nibbles(Wu, rbase + n + kAhead, lane);
             }
             __builtin_amdgcn_sched_barrier(0);
+            if (n == 0) {  // the caller's work while the first rows' weights are in flight
+                hook();
+                __builtin_amdgcn_sched_barrier(0);
+            }
             v[2 * n] = octet_scale(sg, pos + n) * q4_block_dot(q4_signed(U.ng[n]), x);
             v[2 * n + 1] = octet_scale(su, pos + n) * q4_block_dot(q4_signed(U.nu[n]), x);
             __builtin_amdgcn_sched_barrier(0);
@@ -849,15 +850,15 @@ __device__ void gate_up_compute(const StackArgs &a, const UnitDesc &d, UnitLoads
     }
 }
 
-template <int LPRD, int MAXP>
-__device__ void gate_up_unit(const StackArgs &a, const UnitDesc &d, UnitLoads &U, bool preloaded) {
+template <int LPRD, int MAXP, class Hook>
+__device__ void gate_up_unit(const StackArgs &a, const UnitDesc &d, UnitLoads &U, bool preloaded, Hook &&hook) {
     const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
     const int lane = tid() % kWave;
     const int cnt = 1;
     // the weights (HBM), unless early_unit_loads already issued them; the
     // activation records are in LDS
     if (!preloaded) unit_loads(P.pair_expert[d.pair], d, U);
-    gate_up_compute<8, LPRD, MAXP>(a, d, U);
+    gate_up_compute<8, LPRD, MAXP>(a, d, U, hook);
     lds_barrier();
     // h records: one (token, 32-row block) per half-wavefront, from the last
     // wavefront down (the wavefronts that issue no prefetch copies)
@@ -1287,8 +1288,14 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
         const int n_units = P.n_groups > 0 ? (int)a.m * kTopK * (int)(a.F / 64) : 0;
         // the preloaded first unit (pre holds exactly when blockIdx.x <
         // n_units); both branches use U, so no path leaves its loads pending
+        // the shared expert's rows go inside the first unit, once its first
+        // kAhead + 1 rows' loads are issued: they compute while those rows'
+        // weights are in flight (measured per 40-layer launch: 1055 us before
+        // the unit's loads are issued, 1038 us here, 1055 / 1071 / 1108 /
+        // 1131 us after rows 0 / 1 / 2 / 3's dot products)
         if (pre) {
-            gate_up_unit<LPRD, MAXP>(a, unit_desc(blockIdx.x, (int)a.F, (int)a.m), U, true);
+            gate_up_unit<LPRD, MAXP>(a, unit_desc(blockIdx.x, (int)a.F, (int)a.m), U, true,
+                                     [&] { shared_rows<LPRD, MAXP>(a, S); });
         } else {
 #pragma unroll
             for (int n = 0; n < 8; ++n) {
@@ -1297,9 +1304,10 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
             }
             consume(U.sg);
             consume(U.su);
+            if (P.n_groups > 0) shared_rows<LPRD, MAXP>(a, S);
         }
         for (int u = blockIdx.x + gridDim.x; u < n_units; u += gridDim.x)
-            gate_up_unit<LPRD, MAXP>(a, unit_desc(u, (int)a.F, (int)a.m), U, false);
+            gate_up_unit<LPRD, MAXP>(a, unit_desc(u, (int)a.F, (int)a.m), U, false, [] {});
         // arrive once every load of phase B is consumed and this thread's
         // record and row stores are complete (a compiler-visible wait, which
         // also settles the compiler's own bookkeeping of those loads); then
