@@ -362,17 +362,23 @@ __device__ void stack_exit(StackSync *sync, uint64_t *lacc, uint32_t base, uint3
 }
 
 // ---- phase B: gate/up units ------------------------------------------------------
-// Unit u < 8 M (F / 64) is rows [64 (u % (F / 64)), +64) of routed pair
-// M + u / (F / 64) in the plan's pair order (wavefront w: the octet of rows
-// 8w..8w+7).
+// A unit is R = 8 URW rows of one routed pair's gate and up, URW rows per
+// wavefront: URW = 8 (64 rows, one octet per wavefront) in the kernel for
+// M >= 3, URW = 4 (32 rows) in the one for M <= 2, where 64-row units would
+// leave most compute units without gate/up loads (a quarter of them carry the
+// weight stream at M = 1); with 32-row units the 8 M F / R units cover half
+// the grid at M = 1 and all of it at M = 2.  Unit u < 8 M (F / R) is rows
+// [R (u % (F / R)), +R) of routed pair M + u / (F / R) in the plan's pair
+// order (wavefront w: rows URW w .. URW w + URW - 1 of the unit).
 struct UnitDesc {
     int pair, row0, rw;  // pair, first row, rows per wavefront
 };
+template <int URW>
 __device__ __forceinline__ UnitDesc unit_desc(int u, int F, int m) {
     UnitDesc d;
-    d.pair = m + u / (F / 64);
-    d.row0 = (u % (F / 64)) * 64;
-    d.rw = 8;
+    d.rw = URW;
+    d.pair = m + u / (F / (8 * URW));
+    d.row0 = (u % (F / (8 * URW))) * 8 * URW;
     return d;
 }
 
@@ -519,12 +525,13 @@ __device__ __forceinline__ RouteEntry route_entry(int lane, int n) {
 // This workgroup's first unit (blockIdx.x) from the route entries: every
 // wavefront issues its first rows' weight loads (unit_loads_rw).  False: the
 // workgroup has no unit.
+template <int URW>
 __device__ __forceinline__ bool early_unit_loads(const StackArgs &a, const RouteEntry &r, UnitLoads &U) {
     const int lane = tid() % kWave;
     const int m = (int)a.m, n = m * kTopK;
     const int u = (int)blockIdx.x;
-    if (u >= n * ((int)a.F / 64)) return false;
-    const UnitDesc d = unit_desc(u, (int)a.F, m);
+    if (u >= n * ((int)a.F / (8 * URW))) return false;
+    const UnitDesc d = unit_desc<URW>(u, (int)a.F, m);
     const uint64_t hit = __ballot(lane < n && m + r.before + r.rank == d.pair);
     const int expert = __builtin_amdgcn_readlane(r.e, (int)__builtin_ctzll(hit));
     unit_loads(expert, d, U);
@@ -536,7 +543,7 @@ __device__ __forceinline__ bool early_unit_loads(const StackArgs &a, const Route
 // `pre`: whether this workgroup's first unit's loads were issued (in `U`).
 // After the loads are issued only LDS barriers are used: __syncthreads()
 // would wait for them.
-template <int LPRD, int MAXP>
+template <int LPRD, int MAXP, int URW>
 __device__ void compute_routes(const StackArgs &a, uint32_t l, UnitLoads &U, SharedLoads &S, bool &pre, uint32_t base) {
     const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
     const int lane = tid() % kWave;
@@ -718,7 +725,7 @@ __device__ void compute_routes(const StackArgs &a, uint32_t l, UnitLoads &U, Sha
             P.n_pairs = (int)m * (kTopK + 1);
         }
     }
-    pre = early_unit_loads(a, r, U);
+    pre = early_unit_loads<URW>(a, r, U);
     lds_barrier();
 }
 
@@ -850,7 +857,7 @@ __device__ void gate_up_compute(const StackArgs &a, const UnitDesc &d, UnitLoads
     }
 }
 
-template <int LPRD, int MAXP, class Hook>
+template <int LPRD, int MAXP, int URW, class Hook>
 __device__ void gate_up_unit(const StackArgs &a, const UnitDesc &d, UnitLoads &U, bool preloaded, Hook &&hook) {
     const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
     const int lane = tid() % kWave;
@@ -858,7 +865,7 @@ __device__ void gate_up_unit(const StackArgs &a, const UnitDesc &d, UnitLoads &U
     // the weights (HBM), unless early_unit_loads already issued them; the
     // activation records are in LDS
     if (!preloaded) unit_loads(P.pair_expert[d.pair], d, U);
-    gate_up_compute<8, LPRD, MAXP>(a, d, U, hook);
+    gate_up_compute<URW, LPRD, MAXP>(a, d, U, hook);
     lds_barrier();
     // h records: one (token, 32-row block) per half-wavefront, from the last
     // wavefront down (the wavefronts that issue no prefetch copies)
@@ -1245,7 +1252,7 @@ __device__ void phase_c(const StackArgs &a, uint32_t l, uint32_t base, float &hr
 
 }  // namespace
 
-template <int LPRD, int MAXP>
+template <int LPRD, int MAXP, int URW>
 __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
     uint32_t epoch = 0;
     // layer 0's expert-matrix table into LDS (later layers': during the
@@ -1276,7 +1283,7 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
         UnitLoads U;
         SharedLoads S;
         bool pre;
-        compute_routes<LPRD, MAXP>(a, l, U, S, pre, base);
+        compute_routes<LPRD, MAXP, URW>(a, l, U, S, pre, base);
         if (blockIdx.x == 0 && tid() < a.m * kTopK) {
             const uint32_t t = tid() / kTopK, kk = tid() % kTopK;
             if (a.ids_out) a.ids_out[((size_t)l * a.m + t) * kTopK + kk] = P.bad ? 0 : (uint16_t)P.ids[t][kk];
@@ -1285,7 +1292,7 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
         if (blockIdx.x == 0 && tid() == 0 && P.bad == 1 && a.status)
             __hip_atomic_store(a.status, (int32_t)TQF_HIP_ERR_ROUTER, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
-        const int n_units = P.n_groups > 0 ? (int)a.m * kTopK * (int)(a.F / 64) : 0;
+        const int n_units = P.n_groups > 0 ? (int)a.m * kTopK * (int)(a.F / (8 * URW)) : 0;
         // the preloaded first unit (pre holds exactly when blockIdx.x <
         // n_units); both branches use U, so no path leaves its loads pending
         // the shared expert's rows go inside the first unit, once its first
@@ -1294,7 +1301,7 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
         // the unit's loads are issued, 1038 us here, 1055 / 1071 / 1108 /
         // 1131 us after rows 0 / 1 / 2 / 3's dot products)
         if (pre) {
-            gate_up_unit<LPRD, MAXP>(a, unit_desc(blockIdx.x, (int)a.F, (int)a.m), U, true,
+            gate_up_unit<LPRD, MAXP, URW>(a, unit_desc<URW>(blockIdx.x, (int)a.F, (int)a.m), U, true,
                                      [&] { shared_rows<LPRD, MAXP>(a, S); });
         } else {
 #pragma unroll
@@ -1307,7 +1314,7 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
             if (P.n_groups > 0) shared_rows<LPRD, MAXP>(a, S);
         }
         for (int u = blockIdx.x + gridDim.x; u < n_units; u += gridDim.x)
-            gate_up_unit<LPRD, MAXP>(a, unit_desc(u, (int)a.F, (int)a.m), U, false, [] {});
+            gate_up_unit<LPRD, MAXP, URW>(a, unit_desc<URW>(u, (int)a.F, (int)a.m), U, false, [] {});
         // arrive once every load of phase B is consumed and this thread's
         // record and row stores are complete (a compiler-visible wait, which
         // also settles the compiler's own bookkeeping of those loads); then
@@ -1366,19 +1373,20 @@ size_t stack_lds_bytes(uint32_t bp_down, uint32_t members) {
 }
 
 namespace {
-template <int LPRD>
+template <int LPRD, int URW>
 const void *pick(uint32_t maxp, int &chosen) {
-    if (maxp <= 5) { chosen = 5; return (const void *)stack_kernel<LPRD, 5>; }
-    if (maxp <= 9) { chosen = 9; return (const void *)stack_kernel<LPRD, 9>; }
+    if (maxp <= 5) { chosen = 5; return (const void *)stack_kernel<LPRD, 5, URW>; }
+    if (maxp <= 9) { chosen = 9; return (const void *)stack_kernel<LPRD, 9, URW>; }
     chosen = 0;
     return nullptr;
 }
-const void *kernel_for(uint32_t bp_down, uint32_t members) {
+// small: the kernel for M <= 2 (32-row gate/up units)
+const void *kernel_for(uint32_t bp_down, uint32_t members, bool small) {
     const uint32_t maxp = member_max_pairs(members);
     int chosen = 0;
-    if (bp_down == 16) return pick<16>(maxp, chosen);
-    if (bp_down == 32) return pick<32>(maxp, chosen);
-    if (bp_down == 64) return pick<64>(maxp, chosen);
+    if (bp_down == 16) return small ? pick<16, 4>(maxp, chosen) : pick<16, 8>(maxp, chosen);
+    if (bp_down == 32) return small ? pick<32, 4>(maxp, chosen) : pick<32, 8>(maxp, chosen);
+    if (bp_down == 64) return small ? pick<64, 4>(maxp, chosen) : pick<64, 8>(maxp, chosen);
     return nullptr;
 }
 }  // namespace
@@ -1399,17 +1407,21 @@ uint32_t stack_grid(int device, uint32_t bp_down) {
     // dynamic LDS beyond the default limit, set once per context for every
     // variant this grid can launch (bp_down 16 / 32 / 64)
     for (uint32_t bp : {16u, 32u, 64u}) {
-        const void *kv = kernel_for(bp, members);
-        if (kv && hipFuncSetAttribute(kv, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      (int)stack_lds_bytes(bp, members)) != hipSuccess)
+        for (bool small : {false, true}) {
+            const void *kv = kernel_for(bp, members, small);
+            if (kv && hipFuncSetAttribute(kv, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)stack_lds_bytes(bp, members)) != hipSuccess)
+                return 0;
+        }
+    }
+    const size_t lds = stack_lds_bytes(bp_down, members);
+    for (bool small : {false, true}) {
+        const void *k = kernel_for(bp_down, members, small);
+        int per_cu = 0;
+        if (!k || hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kThreads, lds) != hipSuccess ||
+            per_cu < 1)
             return 0;
     }
-    const void *k = kernel_for(bp_down, members);
-    if (!k) return 0;
-    int per_cu = 0;
-    const size_t lds = stack_lds_bytes(bp_down, members);
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kThreads, lds) != hipSuccess || per_cu < 1)
-        return 0;
     return grid;
 }
 
@@ -1419,7 +1431,7 @@ uint32_t stack_grid(int device, uint32_t bp_down) {
 // TQF_HIP_ERR_DEVICE), so the cooperative launch's guarantee is not needed;
 // it cost about 15 us of dispatch per launch.
 hipError_t launch_stack(hipStream_t s, const StackArgs &a, uint32_t grid, uint32_t bp_down) {
-    const void *k = kernel_for(bp_down, a.members);
+    const void *k = kernel_for(bp_down, a.members, a.m <= 2);
     if (!k) return hipErrorInvalidValue;
     StackArgs args = a;
     void *params[] = {&args};
