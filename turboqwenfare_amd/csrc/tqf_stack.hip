@@ -739,6 +739,12 @@ struct MemberShare {
     __device__ int cnt() const { return ns + r1 - r0; }
     __device__ int pair(int q) const { return q < ns ? k + K * q : r0 + q - ns; }
 };
+// URW: the kernel's unit rows per wavefront.  In the kernel for M <= 2
+// (URW = 4), at M = 1 the routed pairs are split with the shared pair counted
+// as two routed ones (member 0, which builds the shared pair's records from
+// raw rows, takes fewer routed pairs): 865 -> 830 us per 40-layer launch;
+// the same weighting cost 31 us at M = 2 and 8 us at M = 4.
+template <int URW>
 __device__ __forceinline__ MemberShare member_share(int k, int K, int m, int n_pairs) {
     MemberShare s;
     s.k = k;
@@ -749,8 +755,19 @@ __device__ __forceinline__ MemberShare member_share(int k, int K, int m, int n_p
     }
     s.ns = k < m ? (m - 1 - k) / K + 1 : 0;
     const int R = n_pairs - m;
-    s.r0 = m + k * R / K;
-    s.r1 = m + (k + 1) * R / K;
+    if (URW == 4 && m == 1) {
+        constexpr int W = 2;
+        const int T = R + W;
+        auto start = [&](int kk) {
+            const int v = kk * T / K - (kk > 0 ? W : 0);
+            return v < 0 ? 0 : v > R ? R : v;
+        };
+        s.r0 = m + start(k);
+        s.r1 = m + start(k + 1);
+    } else {
+        s.r0 = m + k * R / K;
+        s.r1 = m + (k + 1) * R / K;
+    }
     return s;
 }
 
@@ -773,7 +790,7 @@ struct PrefetchOps {
 // pair, or the shared expert's down matrix when it has none), so each of
 // wavefronts 0..5 issues exactly PrefetchOps::kPerWave copies.  The poller's
 // wavefront issues none.  Returns whether this wavefront issued copies.
-template <int LPRD, int MAXP>
+template <int LPRD, int MAXP, int URW>
 __device__ bool prefetch_down(const StackArgs &a) {
     using PF = DownPrefetch<LPRD, MAXP>;
     using OPS = PrefetchOps<LPRD, MAXP>;
@@ -782,7 +799,7 @@ __device__ bool prefetch_down(const StackArgs &a) {
         const uint32_t tau = blockIdx.x % kStackTeams, k = blockIdx.x / kStackTeams;
         const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
         if (k >= K || wave >= kDmaWaves) return false;
-        const MemberShare sh = member_share((int)k, (int)K, (int)a.m, P.n_pairs);
+        const MemberShare sh = member_share<URW>((int)k, (int)K, (int)a.m, P.n_pairs);
         const int cnt = sh.cnt();
         const int lane = tid() % kWave;
 #pragma unroll
@@ -1099,7 +1116,7 @@ __device__ bool poll_partials(const StackArgs &a, const uint64_t *w0, uint32_t K
 }
 
 // ---- phase C -------------------------------------------------------------------
-template <int LPRD, int MAXP>
+template <int LPRD, int MAXP, int URW>
 __device__ void phase_c(const StackArgs &a, uint32_t l, uint32_t base, float &hres, const ShareLoads &SL) {
     uint4 *s_x = reinterpret_cast<uint4 *>(reinterpret_cast<uint8_t *>(s_dyn) + LdsLayout<LPRD, MAXP>::kXr);
     const int wave = __builtin_amdgcn_readfirstlane(tid() / kWave);
@@ -1111,7 +1128,7 @@ __device__ void phase_c(const StackArgs &a, uint32_t l, uint32_t base, float &hr
     const uint32_t K = a.members;
     const uint32_t tau = blockIdx.x % kStackTeams, k = blockIdx.x / kStackTeams;
     if (k >= K) return;
-    const MemberShare share = member_share((int)k, (int)K, (int)a.m, P.n_pairs);
+    const MemberShare share = member_share<URW>((int)k, (int)K, (int)a.m, P.n_pairs);
     const int cnt = share.cnt();
     const uint32_t j = (uint32_t)lane / LPRD, b = (uint32_t)lane % LPRD;
     const uint32_t r0 = tau * 64 + 8 * wave;  // this wavefront's octet
@@ -1322,7 +1339,7 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
         // them stalls until the memory pipeline takes them, so they go out
         // after the arrival)
         grid_arrive(a.sync, epoch);
-        prefetch_down<LPRD, MAXP>(a);
+        prefetch_down<LPRD, MAXP, URW>(a);
         // this member's share of the next layer's router rows, gate and norm
         ShareLoads SL;
         if (l + 1 < a.n_layers) share_loads(a, l + 1, SL);
@@ -1339,7 +1356,7 @@ __global__ __launch_bounds__(kThreads) void stack_kernel(StackArgs a) {
                 mp[i] = load_global_ptr(Ln.mats + (k < (a.E + 1) * 3 ? k : 0));
             }
         }
-        phase_c<LPRD, MAXP>(a, l, base, hres, SL);
+        phase_c<LPRD, MAXP, URW>(a, l, base, hres, SL);
         if (!(ok = P.ok != 0)) break;
         if (more) {
             __syncthreads();  // every wavefront is past phase C's table reads
