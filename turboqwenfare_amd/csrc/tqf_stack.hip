@@ -17,14 +17,16 @@
 //      renormalise; experts/mod.rs:134-197) on wavefronts 0..M-1 --
 //      computed identically in every workgroup, so the plan needs no further
 //      exchange -- then gate/up units of 64 rows (one row octet per
-//      wavefront) of one routed (expert, token) pair, with the activation
-//      records of y = h * w_norm of every row in LDS (1/rms scales the dot
-//      products: rmsnorm(h) . W = (1/rms) (y . W)); h = silu(g) * u is
-//      written as records per pair.  M = 4 tokens have 32 routed pairs: 256
-//      units of equal work, one per workgroup.  The shared expert (all M
-//      tokens) is spread thinner: every workgroup takes two of its rows, one
-//      (row, token) per wavefront, and writes raw h values; the phase C
-//      member that owns the shared pairs turns them into records.
+//      wavefront; 32 rows in the kernel instantiation for M <= 2) of one
+//      routed (expert, token) pair, with the activation records of
+//      y = h * w_norm of every row in LDS (1/rms scales the dot products:
+//      rmsnorm(h) . W = (1/rms) (y . W)); h = silu(g) * u is written as
+//      records per pair.  M = 4 tokens have 32 routed pairs: 256 units of
+//      equal work, one per workgroup.  The shared expert (all M tokens) is
+//      spread thinner: every workgroup takes two of its rows, one (row,
+//      token) per wavefront, computed inside its unit while the unit's first
+//      weights are in flight, and writes raw h values; the phase C member
+//      that owns the shared pairs turns them into records.
 //   C  teams of workgroups own 64 output rows each; a team member takes a
 //      contiguous share of the expert-sorted pair list (8 rows per
 //      wavefront, every weight load issued up front) and publishes its
