@@ -530,6 +530,31 @@ def test_persistent_stack_abort_is_recovered(backend, stack3, monkeypatch, fail_
     assert np.array_equal(again[1], want[1]) and rel_err(again[0], want[0]) < FFN_TOL
 
 
+def test_persistent_stack_recovers_from_logit_range(backend, stack3):
+    """Rows of h around 1e7 keep ordinary (normalised) router logits, but a
+    team's partial sum of router row times y exceeds the persistent kernel's
+    fixed-point range (2^20): with recovery on the launch aborts and the
+    library re-runs the stack through the per-layer kernels, so the call
+    returns exactly their h and routes with status 0 and counts one re-run;
+    with recovery off the call reports the router error."""
+    _, _, st = stack3
+    h0 = (synth.normal((4, 2048), seed=433) * 1e7).astype(np.float32)
+    want = _stack_run(backend, st, h0, 4, 3, False)
+    assert want[3] == 0
+    before = backend.recovery_counts()
+    got = _stack_run(backend, st, h0, 4, 3, True)
+    assert got[3] == 0
+    assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
+    assert backend.recovery_counts() == (before[0] + 1, before[1])
+    with backend.variant(_lib.VARIANT_RECOVER, False):
+        off = _stack_run(backend, st, h0, 4, 3, True)
+    assert off[3] == ERR_ROUTER
+    # a clean launch afterwards runs the persistent path bit-identically
+    h1 = synth.normal((4, 2048), seed=434)
+    a1, b1 = _stack_run(backend, st, h1, 4, 3, True), _stack_run(backend, st, h1, 4, 3, True)
+    assert a1[3] == 0 and np.array_equal(a1[0], b1[0]) and backend.recovery_counts()[0] == before[0] + 1
+
+
 def test_verify_step_recovers_both_parts(backend, stack3, monkeypatch):
     """A verify step whose persistent stack and one-launch acceptance both
     time out (forced from the host) still returns the per-layer stack's h

@@ -217,17 +217,24 @@ __device__ __forceinline__ void zero_lacc(uint64_t *acc, uint32_t part, uint32_t
 // routing polls the words until all 32 have counted: the words carry their
 // own completion, and no grid barrier separates a layer's tail from the
 // next layer's routing.  |partial| must stay below 2^20 (about 931,000); a
-// partial that is larger or not finite sets the accumulator's flag word
-// instead and never counts, and the routing, which polls the flag with the
-// words, reports the router error.
+// partial that is larger or not finite sets a bit of the accumulator's flag
+// word instead and never counts, and the routing polls the flag with the
+// words.  A non-finite partial (kFlagNonFinite) is the router error of the
+// reference's validation; a finite one beyond the range (kFlagRange: rows of
+// h with |h| around 10^7, whose normalised logits are ordinary) is a limit of
+// this accumulator only, so the routing aborts the launch, and with recovery
+// on the library re-runs the stack through the per-layer kernels, which sum
+// the logits in f32.
 constexpr uint64_t kCountOne = 1ull << 58, kTermBias = 1ull << 52;
+constexpr uint64_t kFlagNonFinite = 1, kFlagRange = 2;
 __device__ __forceinline__ void add_counted(uint64_t *word, uint64_t *flag, float v) {
     const double d = (double)v * 4294967296.0;
     if (fabs(d) < 4.0e15) {
         __hip_atomic_fetch_add(word, kCountOne + (uint64_t)(__double2ll_rn(d) + (int64_t)kTermBias), __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
     } else {
-        __hip_atomic_fetch_or(flag, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_or(flag, fabsf(v) <= 3.402823466e38f ? kFlagRange : kFlagNonFinite, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 __device__ __forceinline__ bool counted_done(uint64_t w) { return (w >> 58) == kStackTeams; }
@@ -604,6 +611,18 @@ __device__ void compute_routes(const StackArgs &a, uint32_t l, UnitLoads &U, Sha
 #pragma unroll
         for (int i = 0; i < 4; ++i) fx[i] = counted_value(fx[i]);
         gfx = counted_value(gfx);
+        if (!aborted && (flag & kFlagRange) && !(flag & kFlagNonFinite)) {
+            // a finite partial beyond the accumulator's range: abort (every
+            // workgroup leaves at its next wait; without recovery the call
+            // reports the router error, with it the library re-runs the stack)
+            if (lane == 0) {
+                __hip_atomic_store(&a.sync->abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (a.dev_status)
+                    __hip_atomic_store(a.dev_status, (int32_t)TQF_HIP_ERR_ROUTER, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+            aborted = true;
+        }
         if (aborted && lane == 0) P.bad = 2;
     }
     // the records only once the routing words are in (their 7 MB over all
@@ -628,7 +647,7 @@ __device__ void compute_routes(const StackArgs &a, uint32_t l, UnitLoads &U, Sha
 #pragma unroll
         for (int i = 0; i < 4; ++i) lv[i] = logit_of(fx[i], inv);
         glog = logit_of(gfx, inv);
-        if (flag != 0 && lane == 0) P.bad = 1;  // a non-finite partial logit
+        if ((flag & kFlagNonFinite) && lane == 0) P.bad = 1;  // a non-finite partial logit
         bool fin = true;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
