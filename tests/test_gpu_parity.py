@@ -176,8 +176,9 @@ class Layer:
     """One synthetic layer resident on the device with host copies for the
     oracle (router ~N(0, 1/2048), shared input gate ~N(0, 1/2048))."""
 
-    def __init__(self, be, layer_id: int, seed: int = 0, router_std=2048 ** -0.5, router=None):
-        E, H, F = 256, 2048, 512
+    def __init__(self, be, layer_id: int, seed: int = 0, router_std=2048 ** -0.5, router=None, E=256,
+                 F=512):
+        H = 2048
         base = 10_000 * (layer_id + 1)
         self.router = (synth.normal((E, H), seed=base + 1, std=router_std) if router is None
                        else np.ascontiguousarray(router, np.float32))
@@ -193,7 +194,7 @@ class Layer:
         host = [[be.download_q4_0(t) for t in m] for m in mats]
         self.host = orc.MoeLayerHost(self.router, self.gate_vec, *host[E],
                                      [h[0] for h in host[:E]], [h[1] for h in host[:E]],
-                                     [h[2] for h in host[:E]])
+                                     [h[2] for h in host[:E]], width=F)
         self.mats = mats
 
 
@@ -528,6 +529,34 @@ def test_persistent_stack_abort_is_recovered(backend, stack3, monkeypatch, fail_
     again = _stack_run(backend, st, h0, m, 3, True)
     assert again[3] == 0 and backend.recovery_counts() == after
     assert np.array_equal(again[1], want[1]) and rel_err(again[0], want[0]) < FFN_TOL
+
+
+@pytest.mark.parametrize("F", [256, 1024, 2048])
+def test_persistent_stack_other_widths(backend, F):
+    """Expert widths other than the model's 512 select the other kernel
+    instantiations (down rows of 16 / 32 / 64 blocks; 64- and 32-row gate/up
+    units, several per workgroup where 8 M F / R exceeds the grid): a 2-layer
+    stack at M = 1, 2, 4 matches the per-layer kernels and the oracle's
+    routes."""
+    layers = [Layer(backend, 20 + F // 256 + i, F=F) for i in range(2)]
+    norms = [1.0 + 0.1 * synth.normal((2048,), seed=950 + i) for i in range(2)]
+    st = backend.prepare_stack([l.dev for l in layers], [backend.upload_f32(n) for n in norms])
+    try:
+        for m in (1, 2, 4):
+            h0 = synth.normal((4, 2048), seed=960 + m)
+            h_p, ids_p, _, s_p = _stack_run(backend, st, h0, m, 2, True)
+            h_k, ids_k, _, s_k = _stack_run(backend, st, h0, m, 2, False)
+            assert s_p == 0 and s_k == 0
+            assert np.array_equal(ids_p, ids_k), (F, m)
+            assert rel_err(h_p, h_k) < FFN_TOL, (F, m)
+            hc, routes = oracle_stack(layers, norms, h0[:m])
+            for l in range(2):
+                assert np.array_equal(ids_p[l], routes[l]), (F, m, l)
+            assert rel_err(h_p, hc) < FFN_TOL, (F, m, rel_err(h_p, hc))
+    finally:
+        backend.free_stack(st)
+        for L in layers:
+            backend.free_moe_layer(L.dev)
 
 
 def test_persistent_stack_recovers_from_logit_range(backend, stack3):
