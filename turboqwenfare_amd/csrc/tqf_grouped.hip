@@ -83,110 +83,143 @@ __device__ __forceinline__ int d_row(int v, int half) { return 8 * (v / 4) + 4 *
 }  // namespace
 
 // ---- plan: counting sort of the (token, k) pairs by expert ------------------
-// Positions are stable in pair order (p = 8 t + k): within one round of 1024
-// pairs a wavefront ranks equal experts with ballots, and per-wavefront counts
-// in LDS order the wavefronts.  The histogram adds one count per peer group
-// (no atomic contention on a popular expert).  Tile i of expert e covers
-// positions off[e] + 32 i .. + rows; a tile entry is {first position,
-// e | rows << 16}.
+// Positions are stable in pair order (p = 8 t + k).  The pairs go in batches
+// of kPlanRounds x 1024: in each round a wavefront ranks equal experts with
+// ballots and the first lane of each peer group writes the group's size to
+// the count slot (round, wavefront) of its expert; one thread per expert
+// then turns its slots into exclusive prefixes (slot order is pair order),
+// so a pair's position is base[e] + the positions of e in earlier batches +
+// its slot's prefix + its rank, with three workgroup barriers per batch.
+// base[e] is the exclusive scan of the expert counts: with one batch these
+// are the slot totals; with more, a first pass counts every pair (one count
+// per peer group).  Tile i of expert e covers positions off[e] + 32 i ..
+// + rows; a tile entry is {first position, e | rows << 16}.
+constexpr int kPlanRounds = 4;
+constexpr uint32_t kPlanBatch = kPlanRounds * kPlanThreads;
+constexpr int kPlanSlots = kPlanRounds * kPlanWaves;
 __global__ __launch_bounds__(kPlanThreads) void gg_plan_kernel(
     const uint16_t *__restrict__ ids, uint32_t pairs, uint32_t E, int32_t *__restrict__ pos_of_pair,
     int32_t *__restrict__ pair_of_pos, uint2 *__restrict__ tiles, int32_t *__restrict__ n_tiles,
     int32_t *__restrict__ status) {
-    __shared__ int32_t hist[256], base[256], tbase[256], cursor[256];
-    __shared__ uint16_t wcnt[kPlanWaves][256];
+    __shared__ uint16_t cnt[kPlanSlots][256];  // per slot: count of expert e, then its prefix
+    __shared__ int32_t hist[256], base[256], tbase[256], done[256], total[256];
     __shared__ int32_t s_bad;
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-    for (int i = tid; i < 256; i += kPlanThreads) {
-        hist[i] = 0;
-        cursor[i] = 0;
+    const uint64_t below = (1ull << lane) - 1;
+    const bool one = pairs <= kPlanBatch;
+    if (tid < 256) {
+        hist[tid] = 0;
+        done[tid] = 0;
     }
-    for (int i = tid; i < kPlanWaves * 256; i += kPlanThreads) (&wcnt[0][0])[i] = 0;
     if (tid == 0) s_bad = 0;
     __syncthreads();
-    const uint64_t below = (1ull << lane) - 1;
-    for (uint32_t r = 0; r < pairs; r += kPlanThreads) {
-        const uint32_t p = r + tid;
-        uint32_t key = 256u;  // no expert
-        if (p < pairs) {
-            const uint32_t e = ids[p];
-            if (e < E) key = e;
-            else s_bad = 1;
+    if (!one) {
+        for (uint32_t r = 0; r < pairs; r += kPlanThreads) {
+            const uint32_t p = r + tid;
+            uint32_t key = 256u;  // no expert
+            if (p < pairs) {
+                const uint32_t e = ids[p];
+                if (e < E) key = e;
+                else s_bad = 1;
+            }
+            const uint64_t peers = match_peers(key);
+            if (key < 256u && (peers & below) == 0) atomicAdd(&hist[key], (int)__popcll(peers));
         }
-        const uint64_t peers = match_peers(key);
-        if (key < 256u && (peers & below) == 0) atomicAdd(&hist[key], (int)__popcll(peers));
     }
-    __syncthreads();
-    if (s_bad) {
-        if (tid == 0) {
-            *n_tiles = 0;
-            if (status) *status = TQF_HIP_ERR_INVALID;
-        }
-        return;
-    }
-    if (wave == 0) {  // exclusive scans of pair and tile counts, 4 experts per lane
-        int c[4], tc[4], s = 0, ts = 0;
+    bool planned = false;
+    for (uint32_t b0 = 0; b0 < pairs; b0 += kPlanBatch) {
+        uint32_t key[kPlanRounds];
+        int rank[kPlanRounds];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t e = 4 * lane + j;
-            c[j] = e < E ? hist[e] : 0;
-            tc[j] = (c[j] + kTileM - 1) / kTileM;
-            s += c[j];
-            ts += tc[j];
-        }
-        int is = s, its = ts;
-#pragma unroll
-        for (int d = 1; d < kWave; d *= 2) {
-            const int a = __shfl_up(is, d), b = __shfl_up(its, d);
-            if (lane >= d) {
-                is += a;
-                its += b;
+        for (int i = 0; i < kPlanRounds; ++i) {
+            const uint32_t p = b0 + (uint32_t)i * kPlanThreads + tid;
+            key[i] = 256u;
+            if (p < pairs) {
+                const uint32_t e = ids[p];
+                if (e < E) key[i] = e;
+                else s_bad = 1;
             }
         }
-        int o = is - s, to = its - ts;
+        for (int i = tid; i < kPlanSlots * 256 / 8; i += kPlanThreads)
+            reinterpret_cast<uint4 *>(&cnt[0][0])[i] = make_uint4(0, 0, 0, 0);
+        __syncthreads();
+        if (s_bad) {
+            if (tid == 0) {
+                *n_tiles = 0;
+                if (status) *status = TQF_HIP_ERR_INVALID;
+            }
+            return;
+        }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t e = 4 * lane + j;
-            base[e] = o;
-            tbase[e] = to;
-            o += c[j];
-            to += tc[j];
-        }
-        if (lane == kWave - 1) *n_tiles = its;
-    }
-    __syncthreads();
-    for (uint32_t e = tid; e < E; e += kPlanThreads) {
-        const int c = hist[e];
-        for (int i = 0; i * kTileM < c; ++i) {
-            const int rows = c - i * kTileM < kTileM ? c - i * kTileM : kTileM;
-            tiles[tbase[e] + i] = make_uint2((uint32_t)(base[e] + i * kTileM), e | ((uint32_t)rows << 16));
-        }
-    }
-    for (uint32_t r = 0; r < pairs; r += kPlanThreads) {
-        const uint32_t p = r + tid;
-        const bool valid = p < pairs;
-        const uint32_t e = valid ? ids[p] : 256u;  // 256: no expert
-        const uint64_t peers = match_peers(e);
-        const int rank = __popcll(peers & below);
-        if (valid && rank == 0) wcnt[wave][e] = (uint16_t)__popcll(peers);
-        __syncthreads();
-        if (valid) {
-            int before = 0;
-            for (int w = 0; w < wave; ++w) before += wcnt[w][e];
-            const int pos = base[e] + cursor[e] + before + rank;
-            pos_of_pair[p] = pos;
-            pair_of_pos[pos] = (int32_t)p;
+        for (int i = 0; i < kPlanRounds; ++i) {
+            const uint64_t peers = match_peers(key[i]);
+            rank[i] = __popcll(peers & below);
+            if (key[i] < 256u && rank[i] == 0) cnt[i * kPlanWaves + wave][key[i]] = (uint16_t)__popcll(peers);
         }
         __syncthreads();
-        for (uint32_t x = tid; x < E; x += kPlanThreads) {
+        if (tid < (int)E) {
             int s = 0;
-            for (int w = 0; w < kPlanWaves; ++w) {
-                s += wcnt[w][x];
-                wcnt[w][x] = 0;
+            for (int v = 0; v < kPlanSlots; ++v) {
+                const int c = cnt[v][tid];
+                cnt[v][tid] = (uint16_t)s;
+                s += c;
             }
-            cursor[x] += s;
+            total[tid] = s;
+            if (one) hist[tid] = s;
         }
         __syncthreads();
+        if (!planned) {
+            planned = true;
+            if (wave == 0) {  // exclusive scans of pair and tile counts, 4 experts per lane
+                int c[4], tc[4], s = 0, ts = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t e = 4 * lane + j;
+                    c[j] = e < E ? hist[e] : 0;
+                    tc[j] = (c[j] + kTileM - 1) / kTileM;
+                    s += c[j];
+                    ts += tc[j];
+                }
+                int is = s, its = ts;
+#pragma unroll
+                for (int d = 1; d < kWave; d *= 2) {
+                    const int a = __shfl_up(is, d), b = __shfl_up(its, d);
+                    if (lane >= d) {
+                        is += a;
+                        its += b;
+                    }
+                }
+                int o = is - s, to = its - ts;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t e = 4 * lane + j;
+                    base[e] = o;
+                    tbase[e] = to;
+                    o += c[j];
+                    to += tc[j];
+                }
+                if (lane == kWave - 1) *n_tiles = its;
+            }
+            __syncthreads();
+            for (uint32_t e = tid; e < E; e += kPlanThreads) {
+                const int c = hist[e];
+                for (int i = 0; i * kTileM < c; ++i) {
+                    const int rows = c - i * kTileM < kTileM ? c - i * kTileM : kTileM;
+                    tiles[tbase[e] + i] = make_uint2((uint32_t)(base[e] + i * kTileM), e | ((uint32_t)rows << 16));
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kPlanRounds; ++i) {
+            if (key[i] < 256u) {
+                const uint32_t p = b0 + (uint32_t)i * kPlanThreads + tid;
+                const int pos = base[key[i]] + done[key[i]] + cnt[i * kPlanWaves + wave][key[i]] + rank[i];
+                pos_of_pair[p] = pos;
+                pair_of_pos[pos] = (int32_t)p;
+            }
+        }
+        __syncthreads();
+        if (tid < (int)E) done[tid] += total[tid];
     }
 }
 
