@@ -220,26 +220,12 @@ def q4k_verify_bench(be, n_layers: int, seed: int, inputs, steps: int = 50, warm
     integer path (bit-identical per matvec to q4_k_dot_pre).  The experts are
     device repacks of 8 seeded centred GGML Q4_K matrices per shape, each at
     its own HBM address."""
-    from turboqwenfare_amd import _lib, mtp, synth
+    from turboqwenfare_amd import _lib, mtp
+    from turboqwenfare_amd.workloads import SyntheticQ4KStack
 
     target, draft, dtok, u, ur, h0 = inputs
-    shapes = ((F, H), (F, H), (H, F))
-    staging = [[be.to_device(synth.centered_q4_k(r, c, seed * 1000 + 10 * i + j)) for j in range(8)]
-               for i, (r, c) in enumerate(shapes)]
-    layers, norms, weights = [], [], []
-    for l in range(n_layers):
-        base = 3_000_000 * (l + 1)
-        mats = [tuple(be.upload_q4_k_device(staging[i][(l * 5 + e * 3 + i) % 8], r, c)
-                      for i, (r, c) in enumerate(shapes)) for e in range(E + 1)]
-        weights += [w for m in mats for w in m]
-        router = be.upload_f32(synth.normal((E, H), seed=base + 7, std=H ** -0.5))
-        gate = be.upload_f32(synth.normal((H,), seed=base + 8, std=H ** -0.5))
-        layers.append(be.prepare_moe_layer(router, gate, mats[E], [m[0] for m in mats[:E]],
-                                           [m[1] for m in mats[:E]], [m[2] for m in mats[:E]]))
-        norms.append(be.upload_f32((1.0 + 0.05 * synth.normal((H,), seed=base + 9)).astype(np.float32)))
-    for b in (b for row in staging for b in row):
-        be.free(b)
-    st = be.prepare_stack(layers, norms)
+    model = SyntheticQ4KStack(be, n_layers, seed)
+    st = model.stack
     d = {k: be.to_device(v) for k, v in dict(t=target, d=draft, dt=dtok, u=u, ur=ur, h0=h0,
                                               h=h0).items()}
     d_acc, d_tok = be.alloc(4), be.alloc(4 * M)
@@ -281,11 +267,7 @@ def q4k_verify_bench(be, n_layers: int, seed: int, inputs, steps: int = 50, warm
                stack_bytes_per_step=stack_bytes, kernels=prof)
     for b in list(d.values()) + [d_acc, d_tok, d_ids, d_tmp]:
         be.free(b)
-    be.free_stack(st)
-    for L in layers:
-        be.free_moe_layer(L)
-    for w in weights:
-        be.free_weights(w)
+    model.free()
     return out
 
 

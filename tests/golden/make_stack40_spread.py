@@ -15,9 +15,21 @@ this depth.  It also replays the stack with only the device's activation
 rounding (replay_device_model: every matvec input as its 22-bit block
 records) and records that replay's distance from the oracle
 (``*_device_records``): tests/test_gpu_stack40.py bounds the GPU's error by
-it plus twice the every-layer spread.  CPU only, a few minutes:
+it plus twice the every-layer spread.
 
-    python tests/golden/make_stack40_spread.py
+The Q4_K stack (workloads.SyntheticQ4KStack, whose expert bytes are host
+generated) is chaotic at this depth: the Q8_K quantization of every matvec
+input (weights.rs:898-931) turns a rounding-level change of its input into
+whole quantization steps, and the oracle's own routes change within 5-16
+layers under the same noise.  For it the script records, per trial, the
+first layer whose routes differ from the unperturbed replay
+(``q4k_m<M>_first_flip``, ``q4k_m<M>_every_layer_first_flip``) and the
+distance at layer 40; no implementation that rounds differently from the
+oracle can be compared with it end to end, so tests/test_gpu_stack40_q4k.py
+checks the device layer by layer instead.  CPU only, a few minutes:
+
+    python tests/golden/make_stack40_spread.py          # everything
+    python tests/golden/make_stack40_spread.py --q4k    # the Q4_K entries only (merged)
 """
 import json
 import sys
@@ -29,9 +41,10 @@ HERE = Path(__file__).resolve().parent
 sys.path[:0] = [str(HERE.parent.parent), str(HERE.parent), str(HERE.parent.parent / "oracle")]
 
 from conftest import rel_err  # noqa: E402
-from stack_oracle import oracle_replay  # noqa: E402
+from stack_oracle import OneLayer, oracle_replay  # noqa: E402
 from turboqwenfare_amd import synth  # noqa: E402
-from turboqwenfare_amd.workloads import E, F, H, expert_tensor_ids, layer_host_f32  # noqa: E402
+from turboqwenfare_amd.workloads import (E, F, H, expert_tensor_ids, layer_host_f32,  # noqa: E402
+                                         q4k_layer_host_f32, q4k_matrices, q4k_matrix_index)
 
 E_SHARED = E  # the shared expert's index in a layer's expert table
 
@@ -55,6 +68,20 @@ class HostStack:
         return self.cache[(l, e)]
 
 
+class HostQ4KStack:
+    """The SyntheticQ4KStack's tensors on the host (oracle_replay's interface)."""
+
+    fmt = "q4_k"
+
+    def __init__(self, n_layers):
+        self.n_layers = n_layers
+        self.host_f32 = [q4k_layer_host_f32(l) for l in range(n_layers)]
+        self.host_q4k = q4k_matrices(0)
+
+    def expert_q4_k(self, l, e):
+        return tuple(self.host_q4k[i][q4k_matrix_index(l, e, i)] for i in range(3))
+
+
 def replay_noisy(st, h0, seed):
     """oracle_replay with rounding-level noise injected into h before every
     layer (the model of an implementation that rounds differently from the
@@ -64,7 +91,7 @@ def replay_noisy(st, h0, seed):
     routes = []
     for l in range(st.n_layers):
         h = (h * (1 + 2.0 ** -24 * rng.standard_normal(h.shape))).astype(np.float32)
-        one = _OneLayer(st, l)
+        one = OneLayer(st, l)
         h, ids, _ = oracle_replay(one, h)
         routes.append(ids[0])
     return h, np.stack(routes)
@@ -136,48 +163,84 @@ def replay_device_model(st, h0, routes):
     return h
 
 
-class _OneLayer:
-    """Layer l of a HostStack as a one-layer stack."""
+def spreads_of(st, h0, ids, h):
+    """(input-only spreads, every-layer spreads) of the oracle's 40-layer h."""
+    spreads, every = [], []
+    for seed in range(TRIALS):
+        n = np.random.default_rng(seed).standard_normal(h0.shape)
+        hp = (h0 * (1 + 2.0 ** -24 * n)).astype(np.float32)
+        h2, ids2, _ = oracle_replay(st, hp)
+        assert np.array_equal(ids, ids2), "a perturbation changed the routes"
+        spreads.append(float(rel_err(h2, h)))
+    for seed in range(TRIALS):
+        h3, ids3 = replay_noisy(st, h0, 100 + seed)
+        assert np.array_equal(ids, ids3), "a perturbation changed the routes"
+        every.append(float(rel_err(h3, h)))
+    return spreads, every
 
-    def __init__(self, st, l):
-        self.st, self.l, self.n_layers = st, l, 1
-        self.host_f32 = [st.host_f32[l]]
 
-    def expert_q4_0(self, _, e):
-        return self.st.expert_q4_0(self.l, e)
+def first_flip(st, h0, ids, h, seed, every):
+    """(first layer whose routes differ from ids, distance from h at the last
+    layer) of a replay with the input perturbed (every=False) or with noise
+    before every layer (every=True)."""
+    rng = np.random.default_rng(seed)
+    x = np.array(h0, np.float32)
+    if not every:
+        x = (x * (1 + 2.0 ** -24 * rng.standard_normal(x.shape))).astype(np.float32)
+    first = None
+    for l in range(st.n_layers):
+        if every:
+            x = (x * (1 + 2.0 ** -24 * rng.standard_normal(x.shape))).astype(np.float32)
+        x, r, _ = oracle_replay(OneLayer(st, l), x)
+        if first is None and not np.array_equal(r[0], ids[l]):
+            first = l
+    return first, float(rel_err(x, h))
+
+
+def q4k_entries(out):
+    st = HostQ4KStack(LAYERS)
+    for m in (4, 1):
+        h0 = synth.normal((4, H), seed=1)[:m]
+        h, ids, _ = oracle_replay(st, h0)
+        for key, every, seeds in (("", False, range(TRIALS)), ("_every_layer", True, range(100, 100 + TRIALS))):
+            res = [first_flip(st, h0, ids, h, sd, every) for sd in seeds]
+            out[f"q4k_m{m}{key}_first_flip"] = [r[0] for r in res]
+            out[f"q4k_m{m}{key}"] = [r[1] for r in res]
+            print("q4k", m, key, res, flush=True)
+
+
+NOISE = ("h * (1 + 2^-24 n), n ~ N(0,1), numpy default_rng(seed): "
+         "<recipe>_m<M> on the input only (seeds 0..2), "
+         "<recipe>_m<M>_every_layer before every layer (seeds 100..102); "
+         "<recipe>_m<M>_device_records: the replay with only the device's 22-bit "
+         "block activation records (no noise); q4k_m<M>, q4k_m<M>_every_layer: the same "
+         "distances at layer 40 for the Q4_K stack (workloads.SyntheticQ4KStack), whose "
+         "routes change under this noise: *_first_flip is the first layer with other routes")
 
 
 def main():
-    out = {"layers": LAYERS,
-           "noise": "h * (1 + 2^-24 n), n ~ N(0,1), numpy default_rng(seed): "
-                    "<recipe>_m<M> on the input only (seeds 0..2), "
-                    "<recipe>_m<M>_every_layer before every layer (seeds 100..102); "
-                    "<recipe>_m<M>_device_records: the replay with only the device's 22-bit "
-                    "block activation records (no noise)"}
+    path = HERE / "stack40_spread.json"
+    if "--q4k" in sys.argv[1:]:
+        out = json.loads(path.read_text())
+        out["noise"] = NOISE
+        q4k_entries(out)
+        path.write_text(json.dumps(out, indent=1) + "\n")
+        return
+    out = {"layers": LAYERS, "noise": NOISE}
     for recipe in ("zero_mean", "uniform"):
         st = HostStack(LAYERS, recipe)
         for m in (4, 1):
             h0 = synth.normal((4, H), seed=1)[:m]
             h, ids, _ = oracle_replay(st, h0)
-            spreads = []
-            for seed in range(TRIALS):
-                n = np.random.default_rng(seed).standard_normal(h0.shape)
-                hp = (h0 * (1 + 2.0 ** -24 * n)).astype(np.float32)
-                h2, ids2, _ = oracle_replay(st, hp)
-                assert np.array_equal(ids, ids2), "a perturbation changed the routes"
-                spreads.append(float(rel_err(h2, h)))
+            spreads, every = spreads_of(st, h0, ids, h)
             out[f"{recipe}_m{m}"] = spreads
-            every = []
-            for seed in range(TRIALS):
-                h3, ids3 = replay_noisy(st, h0, 100 + seed)
-                assert np.array_equal(ids, ids3), "a perturbation changed the routes"
-                every.append(float(rel_err(h3, h)))
             out[f"{recipe}_m{m}_every_layer"] = every
             hd = replay_device_model(st, h0, ids)
             out[f"{recipe}_m{m}_device_records"] = float(rel_err(hd, h))
             print(recipe, m, spreads, every, out[f"{recipe}_m{m}_device_records"], flush=True)
         st.cache.clear()
-    (HERE / "stack40_spread.json").write_text(json.dumps(out, indent=1) + "\n")
+    q4k_entries(out)
+    path.write_text(json.dumps(out, indent=1) + "\n")
 
 
 if __name__ == "__main__":

@@ -217,3 +217,28 @@ def test_device_record_model_rounds_like_the_records():
     assert not ms.records(np.full(32, 2.0 ** -101, np.float32)).any()
     grid = np.arange(-16, 16, dtype=np.float32) * 2.0 ** -10
     assert np.array_equal(ms.records(grid), grid)
+
+
+def test_q4k_stack_routes_change_under_rounding_noise():
+    """The Q4_K 40-layer stack (workloads.SyntheticQ4KStack, host copy) is
+    chaotic at rounding level, which is why its GPU test checks the device
+    layer by layer: with the input rows perturbed by 2^-24 relative noise
+    (trial 2 of make_stack40_spread.py --q4k, M = 1) the oracle takes other
+    routes from layer 5 on and ends O(1) away at layer 40, as recorded."""
+    import json
+    import sys
+    from pathlib import Path
+
+    golden = Path(__file__).resolve().parent / "golden"
+    sys.path.insert(0, str(golden))
+    import make_stack40_spread as ms
+    from stack_oracle import oracle_replay
+
+    spread = json.loads((golden / "stack40_spread.json").read_text())
+    st = ms.HostQ4KStack(ms.LAYERS)
+    h0 = synth.normal((4, 2048), seed=1)[:1]
+    h, ids, _ = oracle_replay(st, h0)
+    first, dist = ms.first_flip(st, h0, ids, h, 2, False)
+    assert first == spread["q4k_m1_first_flip"][2] == 5
+    assert dist == pytest.approx(spread["q4k_m1"][2], rel=1e-6)
+    assert dist > 1.0
