@@ -174,3 +174,28 @@ def test_grouped_rejects_bad_arguments(backend, small):
     assert e.value.status == ERR_INVALID
     # the context stays usable after an argument error
     assert rel_err(backend.grouped_gemm(small.layer, x, ids, w), small.want(x, ids, w)) < FFN_TOL
+
+
+@pytest.mark.parametrize("t, where", [(700, (699, 7)), (700, (3, 0)), (1100, (600, 4))])
+def test_grouped_bad_id_in_any_plan_batch(backend, small, t, where):
+    """The plan counts pairs in batches of 4096: an out-of-range id in the
+    first or a later batch sets the status and leaves y unwritten, and the
+    next call on good ids is bit-identical to the host form."""
+    x, ids, w = small.inputs(t, 6)
+    dx, dids, dw = backend.to_device(x), backend.to_device(ids), backend.to_device(w)
+    sentinel = np.full((t, 256), 7.25, np.float32)
+    dy = backend.to_device(sentinel)
+    dst = backend.to_device(np.zeros(1, np.int32))
+    bad = ids.copy()
+    bad[where] = 300
+    backend.write(dids, bad)
+    backend.grouped_gemm_device(small.layer, dx, t, dids, dw, dy, dst)
+    assert backend.read(dst, np.int32, (1,))[0] == ERR_INVALID
+    assert np.array_equal(backend.read(dy, np.float32, (t, 256)), sentinel)
+    backend.write(dids, ids)
+    backend.write(dst, np.zeros(1, np.int32))
+    backend.grouped_gemm_device(small.layer, dx, t, dids, dw, dy, dst)
+    assert backend.read(dst, np.int32, (1,))[0] == 0
+    assert np.array_equal(backend.read(dy, np.float32, (t, 256)), backend.grouped_gemm(small.layer, x, ids, w))
+    for b in (dx, dids, dw, dy, dst):
+        backend.free(b)
